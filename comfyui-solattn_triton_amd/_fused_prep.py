@@ -1,0 +1,53 @@
+"""Fused preprocess for the INT8 path (host side).
+
+Mirrors /root/reference/_fused_prep.py:62-98: pooled keys centred by their own
+mean (K smoothing), thresholds tau*sigma, per-token INT8 Q and smoothed K,
+per-channel INT8 V, all from the gfx950 kernels.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from ._capi import call, ptr, stream
+from ._preprocess import BLOCK_SIZE, Routing, as_kernel_input, route
+
+__all__ = ["fused_preprocess", "fused_preprocess_routing"]
+
+
+def fused_preprocess_routing(q, k, v, *, tau, scale, int8_pv=True, block=BLOCK_SIZE,
+                             sink_blocks=(0, 0), sink_q=(0, 0)):
+    """(Routing, qi, qs, ki, ks, vi) -- the INT8 path's inputs to the forward."""
+    r: Routing = route(q, k, v, scale=scale, tau=tau, block=block, int8=True, v_absmax=int8_pv,
+                       sink_blocks=sink_blocks, sink_q=sink_q)
+    q, k, v = as_kernel_input(q), as_kernel_input(k), as_kernel_input(v)
+    B, T, H, D = q.shape
+    dev = q.device
+    qi = torch.empty((B, T, H, D), device=dev, dtype=torch.int8)
+    ki = torch.empty_like(qi)
+    qs = torch.empty((B, T, H), device=dev, dtype=torch.float32)
+    ks = torch.empty_like(qs)
+    vi = torch.empty_like(qi) if int8_pv else None
+    with torch.cuda.device(dev):
+        s = stream(dev)
+        call("solattn_quant_rows", ptr(q), q.stride(0), q.stride(1), q.stride(2), B, T, H, D,
+             None, ptr(qi), ptr(qs), T, s)
+        call("solattn_quant_rows", ptr(k), k.stride(0), k.stride(1), k.stride(2), B, T, H, D,
+             ptr(r.kc_mean), ptr(ki), ptr(ks), T, s)
+        if int8_pv:
+            call("solattn_quant_v", ptr(v), v.stride(0), v.stride(1), v.stride(2), B, T, H, D,
+                 ptr(r.vscale), ptr(vi), T, s)
+    return r, qi, qs, ki, ks, vi
+
+
+def fused_preprocess(q, k, v, *, tau, scale, tokens=None, int8_pv=True, block=BLOCK_SIZE):
+    """Returns (kc, vc, threshold, qi, qs, ki, ks, vi, vsc) with K smoothed, as
+    /root/reference/_fused_prep.py:62-98 (vsc is [B*H, D]; vi/vsc are None
+    without int8_pv)."""
+    if tokens is not None and tokens != q.shape[1]:
+        q, k, v = q[:, :tokens], k[:, :tokens], v[:, :tokens]
+    r, qi, qs, ki, ks, vi = fused_preprocess_routing(q, k, v, tau=tau, scale=scale,
+                                                     int8_pv=int8_pv, block=block)
+    B, _, H, D = q.shape
+    vsc = r.vscale.reshape(B * H, D) if int8_pv else None
+    return r.kc, r.vc, r.threshold, qi, qs, ki, ks, vi, vsc

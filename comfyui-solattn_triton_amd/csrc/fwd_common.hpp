@@ -1,0 +1,363 @@
+// Building blocks shared by the BF16 and INT8 Sol-Attn forwards on gfx950.
+//
+// A workgroup serves one query block (BLK rows, BLK/32 waves of 32 rows).
+// Its work is a sequence of 64-key tiles: first the pooled tiles (chunks of 64
+// pooled keys with at least one approximate block), then the exact tiles (64
+// tokens each, BLK/64 per exact block, ascending block order). Tiles are
+// staged in LDS, double buffered: K row-major [64][136] and V transposed
+// [128][68] (bf16 elements, padded rows).
+#pragma once
+
+#include "common.hpp"
+
+namespace solattn {
+
+constexpr int kKeys = 64;             // keys per tile
+constexpr int kD = 128;               // head dim
+constexpr int kKStride = kD + 8;      // bf16 per K row in LDS (272 B)
+constexpr int kVStride = kKeys + 4;   // bf16 per V^T row in LDS (136 B)
+constexpr int kMaxNT = 2048;          // query/key blocks per head
+constexpr int kMaxPool = kMaxNT / 64; // pooled tiles per query block
+
+struct TileBuf {
+  uint16_t k[kKeys * kKStride];
+  uint16_t vt[kD * kVStride];
+};
+
+template <int BLK>
+struct FwdShared {
+  TileBuf buf[2];
+  uint64_t pmask[kMaxPool];  // approximate-block mask of each pooled tile
+  int16_t pchunk[kMaxPool];  // pooled tile -> chunk of 64 pooled keys
+  int16_t blist[kMaxNT];     // exact key blocks, ascending
+  int npool;
+  int nexact;
+};
+
+struct KVSource {
+  const uint16_t* k;  // token rows (this batch/head)
+  int64_t sk;
+  const uint16_t* v;
+  int64_t sv;
+  const uint16_t* kc;  // pooled rows (this batch/head)
+  int64_t skc;         // row stride of kc and vc
+  const uint16_t* vc;
+};
+
+struct TileDesc {
+  int pooled;
+  int first;       // first token row (exact) or pooled row (pooled)
+  int nvalid;      // rows < nvalid are real
+  uint64_t amask;  // keys taking part in the softmax
+};
+
+// Workgroup -> (batch*head, query block). Workgroups are dealt round-robin to
+// the 8 XCDs; remap so each XCD walks a contiguous run of query blocks of the
+// same heads, which keeps their K/V blocks in that XCD's L2.
+__device__ __forceinline__ void tile_coords(uint32_t w, uint32_t total, int NT, int& bh, int& qb) {
+  uint32_t logical = w;
+  if ((total & 7u) == 0u) logical = (w & 7u) * (total >> 3) + (w >> 3);
+  bh = static_cast<int>(logical / static_cast<uint32_t>(NT));
+  qb = static_cast<int>(logical % static_cast<uint32_t>(NT));
+}
+
+template <int BLK>
+__device__ int build_tile_list(FwdShared<BLK>& sh, const int32_t* __restrict__ counts,
+                               const int16_t* __restrict__ lists, const uint32_t* __restrict__ mask,
+                               int64_t row, int NT, int W, int T) {
+  const int cnt = min(max(counts[row], 0), NT);
+  for (int e = threadIdx.x; e < cnt; e += blockDim.x) sh.blist[e] = lists[row * NT + e];
+  if (threadIdx.x == 0) {
+    const uint32_t* mrow = mask + row * W;
+    int np = 0;
+    for (int c = 0; c * 64 < NT; ++c) {
+      uint64_t ex = mrow[2 * c];
+      if (2 * c + 1 < W) ex |= static_cast<uint64_t>(mrow[2 * c + 1]) << 32;
+      const int nvalid = min(64, NT - 64 * c);
+      const uint64_t valid = nvalid >= 64 ? ~0ull : ((1ull << nvalid) - 1ull);
+      const uint64_t ap = ~ex & valid;
+      if (ap) {
+        sh.pmask[np] = ap;
+        sh.pchunk[np] = static_cast<int16_t>(c);
+        ++np;
+      }
+    }
+    sh.npool = np;
+    constexpr int S = BLK / kKeys;
+    int ne = cnt * S;
+    const int tail = T - (NT - 1) * BLK;
+    if (S == 2 && cnt > 0 && lists[row * NT + cnt - 1] == NT - 1 && tail <= kKeys) ne -= 1;
+    sh.nexact = ne;
+  }
+  __syncthreads();
+  return sh.npool + sh.nexact;
+}
+
+template <int BLK>
+__device__ __forceinline__ TileDesc tile_desc(const FwdShared<BLK>& sh, int n, int T, int NT) {
+  TileDesc td;
+  if (n < sh.npool) {
+    td.pooled = 1;
+    td.first = sh.pchunk[n] * kKeys;
+    td.nvalid = min(kKeys, NT - td.first);
+    td.amask = sh.pmask[n];
+  } else {
+    constexpr int S = BLK / kKeys;
+    const int e = n - sh.npool;
+    const int j = min(max(static_cast<int>(sh.blist[e / S]), 0), NT - 1);
+    td.pooled = 0;
+    td.first = j * BLK + (e % S) * kKeys;
+    td.nvalid = max(0, min(kKeys, T - td.first));
+    td.amask = td.nvalid >= kKeys ? ~0ull : ((1ull << td.nvalid) - 1ull);
+  }
+  return td;
+}
+
+// Per-thread share of one tile on its way from HBM to LDS.
+template <int NTHREADS>
+struct TileRegs {
+  static constexpr int KCH = kKeys * kD / 8 / NTHREADS;  // 16-byte K chunks
+  static constexpr int VU = kKeys * kD / 32 / NTHREADS;  // 4-key x 8-channel V units
+  uint4 k[KCH];
+  uint4 v[VU][4];
+};
+
+__device__ __forceinline__ uint4 ld16(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
+
+template <int BLK, int NTHREADS>
+__device__ __forceinline__ void load_tile(TileRegs<NTHREADS>& r, const FwdShared<BLK>& sh, int n,
+                                          const KVSource& src, int T, int NT) {
+  const TileDesc td = tile_desc<BLK>(sh, n, T, NT);
+  const uint16_t* kb = td.pooled ? src.kc : src.k;
+  const uint16_t* vb = td.pooled ? src.vc : src.v;
+  const int64_t ks = td.pooled ? src.skc : src.sk;
+  const int64_t vs = td.pooled ? src.skc : src.sv;
+  const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+  for (int u = 0; u < TileRegs<NTHREADS>::KCH; ++u) {
+    const int e = threadIdx.x + NTHREADS * u;
+    const int row = e >> 4, cc = e & 15;
+    r.k[u] = row < td.nvalid ? ld16(kb + static_cast<int64_t>(td.first + row) * ks + cc * 8) : z;
+  }
+#pragma unroll
+  for (int u = 0; u < TileRegs<NTHREADS>::VU; ++u) {
+    const int e = threadIdx.x + NTHREADS * u;
+    const int kq = e & 15, dc = e >> 4;
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+      const int row = 4 * kq + x;
+      r.v[u][x] = row < td.nvalid ? ld16(vb + static_cast<int64_t>(td.first + row) * vs + dc * 8) : z;
+    }
+  }
+}
+
+__device__ __forceinline__ uint32_t word_of(const uint4& a, int w) {
+  return w == 0 ? a.x : (w == 1 ? a.y : (w == 2 ? a.z : a.w));
+}
+
+template <int NTHREADS>
+__device__ __forceinline__ void store_tile(const TileRegs<NTHREADS>& r, TileBuf& buf) {
+#pragma unroll
+  for (int u = 0; u < TileRegs<NTHREADS>::KCH; ++u) {
+    const int e = threadIdx.x + NTHREADS * u;
+    const int row = e >> 4, cc = e & 15;
+    *reinterpret_cast<uint4*>(&buf.k[row * kKStride + cc * 8]) = r.k[u];
+  }
+#pragma unroll
+  for (int u = 0; u < TileRegs<NTHREADS>::VU; ++u) {
+    const int e = threadIdx.x + NTHREADS * u;
+    const int kq = e & 15, dc = e >> 4;
+#pragma unroll
+    for (int el = 0; el < 8; ++el) {
+      const uint32_t a0 = word_of(r.v[u][0], el >> 1), a1 = word_of(r.v[u][1], el >> 1);
+      const uint32_t a2 = word_of(r.v[u][2], el >> 1), a3 = word_of(r.v[u][3], el >> 1);
+      uint2 p;
+      if ((el & 1) == 0) {
+        p.x = (a0 & 0xffffu) | (a1 << 16);
+        p.y = (a2 & 0xffffu) | (a3 << 16);
+      } else {
+        p.x = (a0 >> 16) | (a1 & 0xffff0000u);
+        p.y = (a2 >> 16) | (a3 & 0xffff0000u);
+      }
+      *reinterpret_cast<uint2*>(&buf.vt[(dc * 8 + el) * kVStride + 4 * kq]) = p;
+    }
+  }
+}
+
+// S^T (64 keys x 32 query rows of this wave) = K . Q^T. s[m] covers keys
+// 32m + 8(r/4) + 4*half + (r%4) for accumulator element r, query row `col`.
+__device__ __forceinline__ void qk_bf16(const TileBuf& tb, const bf16x8 (&qreg)[8], int col, int half,
+                                        f32x16 (&s)[2]) {
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[m][r] = 0.f;
+#pragma unroll
+  for (int cc = 0; cc < 8; ++cc) {
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const bf16x8 a =
+          *reinterpret_cast<const bf16x8*>(&tb.k[(32 * m + col) * kKStride + cc * 16 + half * 8]);
+      s[m] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qreg[cc], s[m], 0, 0, 0);
+    }
+  }
+}
+
+struct SoftmaxState {
+  float m;          // running max, in the exp2 domain (score * c)
+  float l;          // partial row sum over this lane's keys
+  f32x16 acc[4];    // O^T: channel 32dt + 8(r/4) + 4*half + (r%4), query row `col`
+  __device__ __forceinline__ void init() {
+    m = -INFINITY;
+    l = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[dt][r] = 0.f;
+  }
+};
+
+// Online softmax over one tile: p = exp2(s*c - m_new) replaces s in place.
+// Pooled keys carry weight len_j in the row sum (/root/reference/_tri_fwd.py:302-307).
+template <int BLK>
+__device__ __forceinline__ void softmax_update(SoftmaxState& st, f32x16 (&s)[2], const TileDesc& td,
+                                               float c, int half, int NT, int T) {
+  if (td.amask != ~0ull) {
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int kl = 32 * m + 8 * (r >> 2) + 4 * half + (r & 3);
+        if (!((td.amask >> kl) & 1ull)) s[m][r] = -INFINITY;
+      }
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[m][r]);
+  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  const float m_new = fmaxf(st.m, mx * c);
+  const float alpha = st.m == m_new ? 1.f : __builtin_amdgcn_exp2f(st.m - m_new);
+  const float neg = -m_new;
+  float psum = 0.f;
+  if (td.pooled) {
+    const int tail = T - (NT - 1) * BLK;
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int kl = 32 * m + 8 * (r >> 2) + 4 * half + (r & 3);
+        const float p = __builtin_amdgcn_exp2f(fmaf(s[m][r], c, neg));
+        s[m][r] = p;
+        const float w = (td.first + kl == NT - 1) ? static_cast<float>(tail) : static_cast<float>(BLK);
+        psum = fmaf(p, w, psum);
+      }
+  } else {
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = __builtin_amdgcn_exp2f(fmaf(s[m][r], c, neg));
+        s[m][r] = p;
+        psum += p;
+      }
+  }
+  st.l = fmaf(st.l, alpha, psum);
+  if (__any(alpha != 1.f)) {
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) st.acc[dt][r] *= alpha;
+  }
+  st.m = m_new;
+}
+
+__device__ __forceinline__ bf16x8 to_bf16x8(const f32x16& s, int off) {
+  bf16x8 b;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) b[e] = static_cast<__bf16>(s[off + e]);
+  return b;
+}
+
+// O^T += V^T . P^T over the tile's 64 keys, 16 keys per MFMA step.
+__device__ __forceinline__ void pv_bf16(const TileBuf& tb, const f32x16 (&p)[2], int col, int half,
+                                        f32x16 (&acc)[4]) {
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    const bf16x8 b = to_bf16x8(p[ks >> 1], 8 * (ks & 1));
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      const uint16_t* vrow = &tb.vt[(32 * dt + col) * kVStride + 16 * ks + 4 * half];
+      const bf16x4 lo = *reinterpret_cast<const bf16x4*>(vrow);
+      const bf16x4 hi = *reinterpret_cast<const bf16x4*>(vrow + 8);
+      const bf16x8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[dt], 0, 0, 0);
+    }
+  }
+}
+
+// o[qrow, :] = acc / l (bf16), rows past T skipped.
+__device__ __forceinline__ void store_output(const SoftmaxState& st, uint16_t* __restrict__ obase,
+                                             int64_t so_t, int qrow, int T, int half) {
+  const float l = st.l + __shfl_xor(st.l, 32);
+  const float inv = 1.f / l;
+  if (qrow >= T) return;
+  uint16_t* orow = obase + static_cast<int64_t>(qrow) * so_t;
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint2 w;
+      w.x = pack_bf16x2(st.acc[dt][4 * i] * inv, st.acc[dt][4 * i + 1] * inv);
+      w.y = pack_bf16x2(st.acc[dt][4 * i + 2] * inv, st.acc[dt][4 * i + 3] * inv);
+      *reinterpret_cast<uint2*>(orow + 32 * dt + 8 * i + 4 * half) = w;
+    }
+}
+
+inline int check_fwd_common(const void* q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
+                            const void* kc, const void* vc, int64_t npad, const int32_t* counts,
+                            const int16_t* lists, const uint32_t* mask, int64_t B, int64_t T,
+                            int64_t H, int64_t D, int64_t block, const void* o, int64_t so_b,
+                            int64_t so_t, int64_t so_h, const char* what) {
+  SOLATTN_REQUIRE(D == kD, SOLATTN_EUNSUPPORTED, "%s: head_dim %lld != 128", what, (long long)D);
+  SOLATTN_REQUIRE(block == 64 || block == 128, SOLATTN_EUNSUPPORTED, "%s: block %lld not in {64, 128}",
+                  what, (long long)block);
+  SOLATTN_REQUIRE(B > 0 && T > 0 && H > 0, SOLATTN_EINVAL, "%s: bad sizes", what);
+  const int64_t NT = cdiv(T, block);
+  SOLATTN_REQUIRE(NT <= kMaxNT, SOLATTN_EUNSUPPORTED, "%s: %lld blocks exceed %d", what,
+                  (long long)NT, kMaxNT);
+  SOLATTN_REQUIRE(B * H * NT < (1ll << 31), SOLATTN_EUNSUPPORTED, "%s: grid too large", what);
+  SOLATTN_REQUIRE(npad >= cdiv(NT, 64) * 64, SOLATTN_EINVAL,
+                  "%s: npad %lld must cover whole 64-block chunks", what, (long long)npad);
+  SOLATTN_REQUIRE(q && kc && vc && counts && lists && mask && o, SOLATTN_EINVAL, "%s: null pointer",
+                  what);
+  SOLATTN_REQUIRE(reinterpret_cast<uintptr_t>(q) % 16 == 0 && sq_b % 8 == 0 && sq_t % 8 == 0 &&
+                      sq_h % 8 == 0,
+                  SOLATTN_EINVAL, "%s: q must be 16-byte aligned with strides multiple of 8", what);
+  SOLATTN_REQUIRE(reinterpret_cast<uintptr_t>(kc) % 16 == 0 && reinterpret_cast<uintptr_t>(vc) % 16 == 0,
+                  SOLATTN_EINVAL, "%s: kc/vc must be 16-byte aligned", what);
+  SOLATTN_REQUIRE(reinterpret_cast<uintptr_t>(o) % 8 == 0 && so_b % 4 == 0 && so_t % 4 == 0 &&
+                      so_h % 4 == 0,
+                  SOLATTN_EINVAL, "%s: o must be 8-byte aligned with strides multiple of 4", what);
+  return 0;
+}
+
+inline int check_fwd_args(const void* q, int64_t sq_b, int64_t sq_t, int64_t sq_h, const void* k,
+                          int64_t sk_b, int64_t sk_t, int64_t sk_h, const void* v, int64_t sv_b,
+                          int64_t sv_t, int64_t sv_h, const void* kc, const void* vc, int64_t npad,
+                          const int32_t* counts, const int16_t* lists, const uint32_t* mask,
+                          int64_t B, int64_t T, int64_t H, int64_t D, int64_t block, const void* o,
+                          int64_t so_b, int64_t so_t, int64_t so_h, const char* what) {
+  if (int rc = check_fwd_common(q, sq_b, sq_t, sq_h, kc, vc, npad, counts, lists, mask, B, T, H, D,
+                                block, o, so_b, so_t, so_h, what))
+    return rc;
+  SOLATTN_REQUIRE(k && v, SOLATTN_EINVAL, "%s: null k/v", what);
+  SOLATTN_REQUIRE(reinterpret_cast<uintptr_t>(k) % 16 == 0 && sk_b % 8 == 0 && sk_t % 8 == 0 &&
+                      sk_h % 8 == 0 && reinterpret_cast<uintptr_t>(v) % 16 == 0 && sv_b % 8 == 0 &&
+                      sv_t % 8 == 0 && sv_h % 8 == 0,
+                  SOLATTN_EINVAL, "%s: k/v must be 16-byte aligned with strides multiple of 8", what);
+  return 0;
+}
+
+}  // namespace solattn

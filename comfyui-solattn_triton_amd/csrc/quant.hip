@@ -1,0 +1,123 @@
+// Per-token and per-channel INT8 quantisation for the Sol-Attn INT8 path.
+//
+// Built with -ffp-contract=off; divisions are IEEE (HIP's default correctly
+// rounded fp32 divide), so codes and scales match the CPU oracle bit for bit.
+// One row (token, head) of 128 channels is held by 16 lanes x 8 channels; the
+// row's |max| is reduced with 4 xor shuffles inside the 16-lane group.
+#include "common.hpp"
+
+namespace solattn {
+
+constexpr int kQD = 128;
+constexpr int kQuantThreads = 256;
+constexpr int kRowsPerWG = kQuantThreads / 16;
+
+__device__ __forceinline__ int8_t round_half_away_clamp(float val) {
+  float r = val >= 0.f ? truncf(val + 0.5f) : truncf(val - 0.5f);
+  r = fminf(fmaxf(r, -127.f), 127.f);
+  return static_cast<int8_t>(static_cast<int>(r));
+}
+
+__device__ __forceinline__ uint32_t pack_i8x4(int8_t a, int8_t b, int8_t c, int8_t d) {
+  return static_cast<uint32_t>(static_cast<uint8_t>(a)) |
+         (static_cast<uint32_t>(static_cast<uint8_t>(b)) << 8) |
+         (static_cast<uint32_t>(static_cast<uint8_t>(c)) << 16) |
+         (static_cast<uint32_t>(static_cast<uint8_t>(d)) << 24);
+}
+
+// /root/reference/_fused_quant.py:403-426 (per token, optional smoothing mean)
+// and /root/reference/_fused_prep.py:325-331 (Q; clamp-then-round gives the
+// same codes). vscale != nullptr switches to the per-channel V rule,
+// /root/reference/_fused_quant.py:455-472.
+__global__ void __launch_bounds__(kQuantThreads)
+quant_kernel(const uint16_t* __restrict__ x, int64_t sx_b, int64_t sx_t, int64_t sx_h,
+             uint32_t T, uint32_t H, uint32_t rows, const float* __restrict__ mean,
+             const float* __restrict__ vscale, int8_t* __restrict__ xi, float* __restrict__ xs,
+             int64_t TP) {
+  const uint32_t row = blockIdx.x * kRowsPerWG + (threadIdx.x >> 4);
+  if (row >= rows) return;
+  const int c8 = (threadIdx.x & 15) * 8;
+  const uint32_t h = row % H;
+  const uint32_t bt = row / H;
+  const uint32_t t = bt % T;
+  const uint32_t b = bt / T;
+  const uint4 raw =
+      *reinterpret_cast<const uint4*>(x + b * sx_b + static_cast<int64_t>(t) * sx_t + h * sx_h + c8);
+  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+  float y[8];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    y[2 * e] = lo_bf16(w[e]);
+    y[2 * e + 1] = hi_bf16(w[e]);
+  }
+  const int64_t bh = static_cast<int64_t>(b) * H + h;
+  int8_t code[8];
+  if (vscale) {
+    const float4* sp = reinterpret_cast<const float4*>(vscale + bh * kQD + c8);
+    const float4 s0 = sp[0], s1 = sp[1];
+    const float s[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) code[e] = round_half_away_clamp(y[e] / s[e]);
+  } else {
+    if (mean) {
+      const float4* mp = reinterpret_cast<const float4*>(mean + bh * kQD + c8);
+      const float4 m0 = mp[0], m1 = mp[1];
+      const float m[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) y[e] = y[e] - m[e];
+    }
+    float amax = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(y[e]));
+#pragma unroll
+    for (int s = 1; s < 16; s <<= 1) amax = fmaxf(amax, __shfl_xor(amax, s));
+    const float sc = amax / 127.0f;
+    const float ss = sc > 1e-8f ? sc : 1e-8f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) code[e] = round_half_away_clamp(y[e] / ss);
+    if ((threadIdx.x & 15) == 0) xs[(static_cast<int64_t>(b) * TP + t) * H + h] = ss;
+  }
+  uint2 o;
+  o.x = pack_i8x4(code[0], code[1], code[2], code[3]);
+  o.y = pack_i8x4(code[4], code[5], code[6], code[7]);
+  *reinterpret_cast<uint2*>(xi + ((static_cast<int64_t>(b) * TP + t) * H + h) * kQD + c8) = o;
+}
+
+int launch_quant(const uint16_t* x, int64_t sx_b, int64_t sx_t, int64_t sx_h, int64_t B,
+                 int64_t T, int64_t H, int64_t D, const float* mean, const float* vscale,
+                 int8_t* xi, float* xs, int64_t TP, hipStream_t stream, const char* what) {
+  SOLATTN_REQUIRE(D == kQD, SOLATTN_EUNSUPPORTED, "%s: head_dim %lld != 128", what, (long long)D);
+  SOLATTN_REQUIRE(B > 0 && T > 0 && H > 0 && TP >= T, SOLATTN_EINVAL, "%s: bad sizes", what);
+  SOLATTN_REQUIRE(B * T * H < (1ll << 31), SOLATTN_EUNSUPPORTED, "%s: too many rows", what);
+  SOLATTN_REQUIRE(x && xi && (vscale || xs), SOLATTN_EINVAL, "%s: null pointer", what);
+  SOLATTN_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && sx_b % 8 == 0 && sx_t % 8 == 0 &&
+                      sx_h % 8 == 0 && reinterpret_cast<uintptr_t>(xi) % 8 == 0,
+                  SOLATTN_EINVAL, "%s: unaligned input or strides", what);
+  const uint32_t rows = static_cast<uint32_t>(B * T * H);
+  hipLaunchKernelGGL(quant_kernel, dim3(static_cast<uint32_t>(cdiv(rows, kRowsPerWG))),
+                     dim3(kQuantThreads), 0, stream, x, sx_b, sx_t, sx_h,
+                     static_cast<uint32_t>(T), static_cast<uint32_t>(H), rows, mean, vscale, xi,
+                     xs, TP);
+  return check_launch(what);
+}
+
+}  // namespace solattn
+
+using namespace solattn;
+
+extern "C" int solattn_quant_rows(const uint16_t* x, int64_t sx_b, int64_t sx_t, int64_t sx_h,
+                                  int64_t B, int64_t T, int64_t H, int64_t D, const float* mean,
+                                  int8_t* xi, float* xs, int64_t TP, solattn_stream_t stream) {
+  clear_error();
+  return launch_quant(x, sx_b, sx_t, sx_h, B, T, H, D, mean, nullptr, xi, xs, TP,
+                      reinterpret_cast<hipStream_t>(stream), "quant_rows");
+}
+
+extern "C" int solattn_quant_v(const uint16_t* v, int64_t sv_b, int64_t sv_t, int64_t sv_h,
+                               int64_t B, int64_t T, int64_t H, int64_t D, const float* vscale,
+                               int8_t* vi, int64_t TP, solattn_stream_t stream) {
+  clear_error();
+  SOLATTN_REQUIRE(vscale != nullptr, SOLATTN_EINVAL, "quant_v: null vscale");
+  return launch_quant(v, sv_b, sv_t, sv_h, B, T, H, D, nullptr, vscale, vi, nullptr, TP,
+                      reinterpret_cast<hipStream_t>(stream), "quant_v");
+}

@@ -1,0 +1,216 @@
+/*
+ * solattn.h -- C ABI of libsolattn.so, the gfx950 (MI355X) implementation of
+ * Sol-Attn's sparse attention path.
+ *
+ * Conventions shared by every entry point:
+ *  - Device pointers are plain pointers into HBM; "bf16" buffers hold bfloat16
+ *    bit patterns (uint16_t). Strides are in ELEMENTS unless a name ends in
+ *    _bytes. Inputs q/k/v are BTHD ([batch, tokens, heads, head_dim]) with only
+ *    the last dim required to be contiguous; every other buffer is a dense
+ *    allocation in the layout written next to it.
+ *  - block is the routing block size in tokens (64 or 128); NT = ceil(T/block)
+ *    query/key blocks; npad is the block dim of kc/vc (>= NT, zero padded).
+ *  - Every function returns 0 on success or a negative SOLATTN_E* code and
+ *    records a message readable with solattn_last_error() (thread-local).
+ *  - The library never allocates device memory and never synchronises: every
+ *    launch goes on the hipStream_t passed in (NULL = the null stream).
+ *  - head_dim must be 128 on the device paths (the reference's only eligible
+ *    head size, /root/reference/__init__.py:41,178).
+ *
+ * Arithmetic contract (the CPU oracle restates the same operation order, so
+ * pooled keys, thresholds, routing lists and INT8 codes are bit-exact):
+ *  - pooled sums: for each (block, channel) four fp32 partial sums over rows
+ *    r = 0,4,8.. / 1,5,9.. / 2,6,.. / 3,7,.. taken in ascending order (rows past
+ *    T add 0.0f), combined as (p0 + p1) + (p2 + p3).
+ *  - kc = bf16_rne(sum / len); vc = bf16_rne(sum); qbar = sum / len (fp32).
+ *  - moments: 8 fp32 partials over blocks j = g (mod 8), ascending, combined
+ *    ((p0+p1)+(p2+p3)) + ((p4+p5)+(p6+p7)); no FMA.
+ *  - routing score R[i][j] = (fmaf chain over d of qbar_i[d] * kc_j[d]) * c,
+ *    c = scale * 1.4426950408889634f; thresholds as documented per function.
+ */
+#ifndef SOLATTN_H
+#define SOLATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* solattn_stream_t; /* == hipStream_t */
+
+enum {
+  SOLATTN_OK = 0,
+  SOLATTN_EINVAL = -1,    /* bad argument (shape, stride, null pointer) */
+  SOLATTN_EUNSUPPORTED = -2, /* valid but not implemented (e.g. head_dim != 128) */
+  SOLATTN_ELAUNCH = -3,   /* HIP launch error */
+  SOLATTN_ESIZE = -4      /* buffer too small */
+};
+
+enum { SOLATTN_CURVE_3D = 0, SOLATTN_CURVE_2D_FRAME = 1 };
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* solattn_last_error(void);
+/* ABI version: (major << 16) | minor. */
+int solattn_abi_version(void);
+
+/* ---------------------------------------------------------------- Morton --
+ * Host function (no device work). Z-order permutation of a frames x height x
+ * width latent grid laid out frame-major, then row-major, and its inverse.
+ * curve SOLATTN_CURVE_3D interleaves x, y, t bits; SOLATTN_CURVE_2D_FRAME keeps
+ * the frame index as the most significant key. roll != 0 rotates perm by roll
+ * places (torch.roll semantics) before the inverse is taken.
+ * perm/inverse: host int64 arrays of frames*height*width entries.
+ * Replaces: morton_perm, /root/reference/_morton.py:35-73, and the span roll of
+ * _perm_for, /root/reference/_morton_h3.py:42-61. */
+int solattn_morton_perm(int64_t frames, int64_t height, int64_t width, int curve,
+                        int64_t roll, int64_t* perm, int64_t* inverse);
+
+/* --------------------------------------------------------------- reorder --
+ * Row gather: dst[b, t, :] = src[b, index[t], :] for t < rows, b < batch.
+ * A row is row_bytes contiguous bytes (row_bytes % 16 == 0, 16-byte aligned
+ * rows). index: device int64 [rows], each entry in [0, src_rows).
+ * Replaces: the torch index_select / fancy-index gathers of the Morton hooks,
+ * /root/reference/_morton.py:113,128,148 and /root/reference/_morton_h3.py:349,373. */
+int solattn_reorder_rows(const void* src, int64_t src_rows, int64_t src_stride_b_bytes,
+                         int64_t src_stride_row_bytes, void* dst, int64_t dst_stride_b_bytes,
+                         int64_t dst_stride_row_bytes, int64_t batch, int64_t rows,
+                         int64_t row_bytes, const int64_t* index, solattn_stream_t stream);
+
+/* ------------------------------------------------------------------ pool --
+ * One pass over q, k and v per (batch, block, head):
+ *   kc[b, j, h, :] = bf16_rne(sum_k / len_j)      kc, vc: bf16 [B, npad, H, D]
+ *   vc[b, j, h, :] = bf16_rne(sum_v)              (rows j >= NT are not written)
+ *   qbar[b, h, j, :] = sum_q / len_j              qbar: fp32 [B, H, NT, D]
+ *   vamax_part[b, j, h, :] = max_r |v|            fp32 [B, NT, H, D], may be NULL
+ * Replaces: _reduce_kc_kernel / _reduce_vc_kernel / _reduce_kv,
+ * /root/reference/_preprocess.py:23-113,172-224, and the Q centroid of
+ * _diag_threshold_kernel (:144-149) / _q_quant_threshold_kernel
+ * (/root/reference/_fused_prep.py:320-334). */
+int solattn_pool(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
+                 const uint16_t* k, int64_t sk_b, int64_t sk_t, int64_t sk_h,
+                 const uint16_t* v, int64_t sv_b, int64_t sv_t, int64_t sv_h,
+                 int64_t B, int64_t T, int64_t H, int64_t D, int64_t block,
+                 uint16_t* kc, uint16_t* vc, int64_t npad, float* qbar,
+                 float* vamax_part, solattn_stream_t stream);
+
+/* --------------------------------------------------------------- moments --
+ * Per (b, h, d) over blocks j < NT, in ascending j:
+ *   mean = (sum_j kc) / NT
+ *   centre == 0 (BF16 path, /root/reference/_preprocess.py:241-243):
+ *     var = (sum_j (kc - mean)^2) / NT
+ *   centre == 1 (INT8 path, /root/reference/_fused_prep.py:77-81):
+ *     kc[b, j, h, d] = bf16_rne(kc - mean) (in place); var = (sum_j kc'^2) / NT
+ * kc_mean, kc_var: fp32 [B, H, D].
+ * If vamax_part != NULL also vscale[b, h, d] = max(max_j vamax_part * (1/127)f, 1e-8)
+ * (/root/reference/_fused_quant.py:102-105: torch divides by a scalar as a
+ * multiply by its fp32 reciprocal). */
+int solattn_moments(uint16_t* kc, int64_t npad, int64_t B, int64_t NT, int64_t H,
+                    int64_t D, int centre, float* kc_mean, float* kc_var,
+                    const float* vamax_part, float* vscale, solattn_stream_t stream);
+
+/* ----------------------------------------------------------------- route --
+ * Thresholds, routing decisions and per-query-block exact lists.
+ *   mode 0 (BF16, /root/reference/_preprocess.py:150-163):
+ *     mu  = (fmaf chain qbar*kc_mean) * c
+ *     var = (fmaf chain (qbar*qbar)*kc_var) * (c*c)
+ *     thr = mu + tau * sqrtf(fmaxf(var, 0) + 1e-6f)
+ *   mode 1 (INT8, /root/reference/_fused_prep.py:334-342, kc already centred):
+ *     thr = tau * sqrtf(var + 1e-6f)
+ *   R[i][j] = (fmaf chain qbar_i*kc_j) * c
+ *   exact(i, j) = i in [sink_q_lo, sink_q_hi) ? 1
+ *               : R > thr || |i - j| <= 1 || j in [sink_kv_lo, sink_kv_hi)
+ *   (the forward's rule, /root/reference/_tri_fwd.py:279-286).
+ * Outputs: thr fp32 [B, NT, H]; counts int32 [B, H, NT]; lists int16
+ * [B, H, NT, NT] (ascending exact j, first counts[] entries valid); mask
+ * uint32 [B, H, NT, ceil(NT/32)] (bit j%32 of word j/32 = exact). */
+int solattn_route(const float* qbar, const uint16_t* kc, int64_t npad, const float* kc_mean,
+                  const float* kc_var, int64_t B, int64_t T, int64_t H, int64_t D,
+                  int64_t block, float scale, float tau, int mode, int64_t sink_kv_lo,
+                  int64_t sink_kv_hi, int64_t sink_q_lo, int64_t sink_q_hi, float* thr,
+                  int32_t* counts, int16_t* lists, uint32_t* mask, solattn_stream_t stream);
+
+/* ----------------------------------------------------------------- quant --
+ * Per-token INT8 of a BTHD bf16 tensor, optionally smoothed by mean [B, H, D]:
+ *   y = x - mean; s = max|y| / 127; s = s > 1e-8 ? s : 1e-8
+ *   code = clamp(y/s >= 0 ? trunc(y/s + 0.5) : trunc(y/s - 0.5), -127, 127)
+ * xi: int8 [B, TP, H, D]; xs: fp32 [B, TP, H]; rows t >= T are not written.
+ * Replaces: _quant_kernel / quantize_bthd, /root/reference/_fused_quant.py:8-58
+ * (and the Q half of _q_quant_threshold_kernel, _fused_prep.py:325-331). */
+int solattn_quant_rows(const uint16_t* x, int64_t sx_b, int64_t sx_t, int64_t sx_h,
+                       int64_t B, int64_t T, int64_t H, int64_t D, const float* mean,
+                       int8_t* xi, float* xs, int64_t TP, solattn_stream_t stream);
+
+/* Per-channel INT8 of V with vscale fp32 [B, H, D]:
+ *   code = clamp(round_half_away(v / vscale[d]), -127, 127); vi: int8 [B, TP, H, D].
+ * Replaces: _quant_v_kernel / quantize_v_per_channel,
+ * /root/reference/_fused_quant.py:61-113. */
+int solattn_quant_v(const uint16_t* v, int64_t sv_b, int64_t sv_t, int64_t sv_h, int64_t B,
+                    int64_t T, int64_t H, int64_t D, const float* vscale, int8_t* vi,
+                    int64_t TP, solattn_stream_t stream);
+
+/* ------------------------------------------------------------- forwards --
+ * Sparse attention over exact blocks (flash attention on MFMA) plus the pooled
+ * branch (one pooled key kc_j and value vc_j per approximate block, softmax
+ * weight times len_j), one online softmax per query row.
+ * counts/mask come from solattn_route. o: bf16, element (b, t, h, d) at
+ * o + b*so_b + t*so_t + h*so_h + d; rows t >= T are not written.
+ * Replaces: _forward_ptr + sol_attn, /root/reference/_tri_fwd.py:215-410. */
+int solattn_fwd_bf16(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
+                     const uint16_t* k, int64_t sk_b, int64_t sk_t, int64_t sk_h,
+                     const uint16_t* v, int64_t sv_b, int64_t sv_t, int64_t sv_h,
+                     const uint16_t* kc, const uint16_t* vc, int64_t npad,
+                     const int32_t* counts, const int16_t* lists, const uint32_t* mask,
+                     int64_t B, int64_t T, int64_t H, int64_t D, int64_t block, float scale,
+                     uint16_t* o, int64_t so_b, int64_t so_t, int64_t so_h,
+                     solattn_stream_t stream);
+
+/* INT8 exact branch: S = int32(qi . ki) * (qs * c) * ks; int8_pv != 0 quantises
+ * P per row against the block max (pe = exp2(s - rowmax_blk), code =
+ * min(pe*127 + 0.5, 127)) and multiplies with vi, scaled by (beta/127)*vscale;
+ * int8_pv == 0 runs P.V in bf16 against v. The pooled branch is BF16 as above
+ * (q, kc, vc). qi/ki/vi int8 [B, TP, H, D]; qs/ks fp32 [B, TP, H].
+ * Replaces: _forward_int8_ptr + sol_attn_int8, /root/reference/_int8_fwd.py:208-432. */
+int solattn_fwd_int8(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
+                     const int8_t* qi, const float* qs, const int8_t* ki, const float* ks,
+                     const int8_t* vi, const float* vscale, const uint16_t* v, int64_t sv_b,
+                     int64_t sv_t, int64_t sv_h, int64_t TP, const uint16_t* kc,
+                     const uint16_t* vc, int64_t npad, const int32_t* counts,
+                     const int16_t* lists, const uint32_t* mask, int64_t B, int64_t T,
+                     int64_t H, int64_t D, int64_t block, float scale, int int8_pv,
+                     uint16_t* o, int64_t so_b, int64_t so_t, int64_t so_h,
+                     solattn_stream_t stream);
+
+/* ------------------------------------------------------ whole pipeline --
+ * sol_attn in one call: pool -> moments -> route -> fwd_bf16, with every
+ * intermediate carved out of a caller-owned device workspace of at least
+ * solattn_sol_attn_workspace_bytes(...) bytes (256-byte aligned base).
+ * Replaces: sol_attn, /root/reference/_tri_fwd.py:354-410. */
+int64_t solattn_sol_attn_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t D,
+                                         int64_t block, int int8);
+int solattn_sol_attn(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
+                     const uint16_t* k, int64_t sk_b, int64_t sk_t, int64_t sk_h,
+                     const uint16_t* v, int64_t sv_b, int64_t sv_t, int64_t sv_h,
+                     int64_t B, int64_t T, int64_t H, int64_t D, int64_t block,
+                     float scale, float tau, int64_t sink_kv_lo, int64_t sink_kv_hi,
+                     int64_t sink_q_lo, int64_t sink_q_hi, void* workspace,
+                     int64_t workspace_bytes, uint16_t* o, int64_t so_b, int64_t so_t,
+                     int64_t so_h, solattn_stream_t stream);
+
+/* sol_attn_int8 in one call: pool -> moments(centre) -> route(mode 1) ->
+ * quant(q, k smoothed, v) -> fwd_int8. Replaces: sol_attn_int8,
+ * /root/reference/_int8_fwd.py:379-432. */
+int solattn_sol_attn_int8(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
+                          const uint16_t* k, int64_t sk_b, int64_t sk_t, int64_t sk_h,
+                          const uint16_t* v, int64_t sv_b, int64_t sv_t, int64_t sv_h,
+                          int64_t B, int64_t T, int64_t H, int64_t D, int64_t block,
+                          float scale, float tau, int64_t sink_kv_lo, int64_t sink_kv_hi,
+                          int64_t sink_q_lo, int64_t sink_q_hi, int int8_pv,
+                          void* workspace, int64_t workspace_bytes, uint16_t* o,
+                          int64_t so_b, int64_t so_t, int64_t so_h,
+                          solattn_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SOLATTN_H */

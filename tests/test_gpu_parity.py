@@ -1,0 +1,169 @@
+"""GPU parity: every HIP kernel against the CPU oracle on seeded inputs.
+
+Integer/byte results (pooled keys, thresholds, routing lists, INT8 codes and
+scales, permutations) must match bit for bit; forward outputs must agree with
+the oracle's restatement of the reference loop within max-abs 2e-2 and cosine
+>= 0.9995 (BF16) / cosine >= 0.999 (INT8).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from _util import bits, compare_rows, cosine, randn_bf16, u32
+
+pytestmark = pytest.mark.gpu
+
+BF16_MAXABS, BF16_COS, INT8_COS = 2e-2, 0.9995, 0.999
+
+
+def _mods(pkg):
+    import importlib
+    n = pkg.__name__
+    return (importlib.import_module(f"{n}._preprocess"), importlib.import_module(f"{n}._tri_fwd"),
+            importlib.import_module(f"{n}._int8_fwd"), importlib.import_module(f"{n}._fused_prep"),
+            importlib.import_module(f"{n}._fused_quant"), importlib.import_module(f"{n}._morton"))
+
+
+CASES = [  # (B, T, H, block, tau, sink_kv, sink_q)
+    (1, 1000, 2, 64, 0.9, (0, 0), (0, 0)),
+    (2, 777, 3, 128, 0.5, (0, 2), (0, 0)),
+    (1, 4096, 4, 64, 1.3, (0, 3), (0, 3)),
+    (1, 2500, 2, 128, -1e30, (0, 0), (0, 0)),
+]
+
+
+@pytest.mark.parametrize("case", CASES)
+@pytest.mark.parametrize("int8", [False, True])
+def test_route_bit_exact(pkg, dev, case, int8):
+    prep = _mods(pkg)[0]
+    B, T, H, block, tau, skv, sq = case
+    print(f"[route] case={case} int8={int8}", flush=True)
+    q, k, v = (randn_bf16((B, T, H, 128), s) for s in (10, 11, 12))
+    r = prep.route(q.to(dev), k.to(dev), v.to(dev), scale=128 ** -0.5, tau=tau, block=block,
+                   int8=int8, v_absmax=int8, sink_blocks=skv, sink_q=sq)
+    ref = oracle.prepare(bits(q), bits(k), bits(v), block=block, tau=tau, int8=int8,
+                         sink_kv=skv, sink_q=sq)
+    NT = ref["NT"]
+    assert np.array_equal(bits(r.kc), ref["kc"])
+    assert np.array_equal(bits(r.vc), ref["vc"])
+    assert np.array_equal(r.qbar.cpu().numpy().view(np.uint32), ref["qbar"].view(np.uint32))
+    assert np.array_equal(r.kc_mean.cpu().numpy().view(np.uint32), ref["kc_mean"].view(np.uint32))
+    assert np.array_equal(r.kc_var.cpu().numpy().view(np.uint32), ref["kc_var"].view(np.uint32))
+    assert np.array_equal(r.threshold.cpu().numpy().view(np.uint32), ref["thr"].view(np.uint32))
+    assert np.array_equal(r.counts.cpu().numpy(), ref["counts"])
+    assert np.array_equal(u32(r.mask), ref["mask"])
+    lists = r.lists.cpu().numpy()
+    for b in range(B):
+        for h in range(H):
+            for i in range(NT):
+                n = ref["counts"][b, h, i]
+                assert np.array_equal(lists[b, h, i, :n], ref["lists"][b, h, i, :n])
+    if int8:
+        assert np.array_equal(r.vscale.cpu().numpy().view(np.uint32), ref["vscale"].view(np.uint32))
+
+
+@pytest.mark.parametrize("mean", [False, True])
+def test_quant_bit_exact(pkg, dev, mean):
+    fq = _mods(pkg)[4]
+    B, T, H = 2, 333, 3
+    x = randn_bf16((B, T, H, 128), 5, scale=3.0)
+    x[0, 7, 1] = 0  # all-zero row: scale floors at 1e-8
+    m = torch.randn(B, H, 128, generator=torch.Generator().manual_seed(6)) if mean else None
+    xi, xs = fq.quantize_bthd(x.to(dev), mean=None if m is None else m.reshape(B * H, 128).to(dev))
+    rxi, rxs = oracle.quant_rows(bits(x), None if m is None else m.numpy())
+    assert np.array_equal(xi.cpu().numpy(), rxi)
+    assert np.array_equal(xs.cpu().numpy().view(np.uint32), rxs.view(np.uint32))
+    vi, vsc = fq.quantize_v_per_channel(x.to(dev))
+    absmax = np.abs(oracle.bf16_to_f32(bits(x))).max(axis=1)
+    rsc = np.maximum(absmax * (np.float32(1) / np.float32(127)), np.float32(1e-8)).astype(np.float32)
+    assert np.array_equal(vsc.cpu().numpy().reshape(B, H, 128).view(np.uint32), rsc.view(np.uint32))
+    assert np.array_equal(vi.cpu().numpy(), oracle.quant_v(bits(x), rsc))
+
+
+def test_reorder_matches_index_select(pkg, dev):
+    mort = _mods(pkg)[5]
+    x = randn_bf16((2, 21 * 6 * 10, 3 * 128), 7).to(dev)
+    perm, inv = mort.morton_perm((21, 6, 10), dev, "3d")
+    rperm, rinv = oracle.morton_perm((21, 6, 10), "3d")
+    assert np.array_equal(perm.cpu().numpy(), rperm) and np.array_equal(inv.cpu().numpy(), rinv)
+    y = mort.reorder_tokens(x, perm, dim=1)
+    assert torch.equal(y, x.index_select(1, perm))
+    assert torch.equal(mort.reorder_tokens(y, inv, dim=1), x)
+    s = randn_bf16((500, 256), 8).to(dev)
+    idx = torch.randperm(500, generator=torch.Generator().manual_seed(1)).to(dev)
+    assert torch.equal(mort.reorder_tokens(s, idx, dim=0), s[idx])
+
+
+FWD_CASES = [  # (B, T, H, block, tau)
+    (1, 1000, 2, 64, 0.9),
+    (1, 2500, 2, 128, 0.9),
+    (2, 777, 3, 128, 0.3),
+    (1, 4096, 2, 64, 1.5),
+]
+
+
+def _rows(B, H, NT, limit=None, seed=0):
+    rows = [(b, h, i) for b in range(B) for h in range(H) for i in range(NT)]
+    if limit and len(rows) > limit:
+        rng = np.random.default_rng(seed)
+        rows = [rows[j] for j in sorted(rng.choice(len(rows), limit, replace=False))]
+    return rows
+
+
+@pytest.mark.parametrize("case", FWD_CASES)
+def test_fwd_bf16_vs_port(pkg, dev, case):
+    tri = _mods(pkg)[1]
+    B, T, H, block, tau = case
+    print(f"[fwd_bf16] case={case}", flush=True)
+    q, k, v = (randn_bf16((B, T, H, 128), s) for s in (20, 21, 22))
+    out = tri.sol_attn(q.to(dev), k.to(dev), v.to(dev), tau=tau, block=block)
+    torch.cuda.synchronize()
+    ref = oracle.prepare(bits(q), bits(k), bits(v), block=block, tau=tau)
+    rows = _rows(B, H, ref["NT"], limit=24)
+    port = oracle.forward_port(bits(q), bits(k), bits(v), ref, rows)
+    err, cos = compare_rows(out.float().cpu().numpy(), port, block)
+    print(f"[fwd_bf16] max|err|={err:.3e} cos={cos:.6f}", flush=True)
+    assert err < BF16_MAXABS and cos >= BF16_COS
+
+
+def test_fwd_bf16_all_exact_is_dense(pkg, dev):
+    """tau = -inf routes every block: the output is dense SDPA."""
+    tri = _mods(pkg)[1]
+    B, T, H = 1, 1500, 2
+    q, k, v = (randn_bf16((B, T, H, 128), s) for s in (30, 31, 32))
+    out = tri.sol_attn(q.to(dev), k.to(dev), v.to(dev), tau=-1e30, block=128)
+    ref = torch.nn.functional.scaled_dot_product_attention(
+        *(t.float().transpose(1, 2).to(dev) for t in (q, k, v))).transpose(1, 2)
+    err = (out.float() - ref).abs().max().item()
+    assert err < BF16_MAXABS
+    assert cosine(out.float().cpu().numpy(), ref.cpu().numpy()) >= BF16_COS
+
+
+@pytest.mark.parametrize("int8_pv", [True, False])
+@pytest.mark.parametrize("case", FWD_CASES[:3])
+def test_fwd_int8_vs_port(pkg, dev, case, int8_pv):
+    i8 = _mods(pkg)[2]
+    B, T, H, block, tau = case
+    print(f"[fwd_int8] case={case} int8_pv={int8_pv}", flush=True)
+    q, k, v = (randn_bf16((B, T, H, 128), s) for s in (40, 41, 42))
+    out = i8.sol_attn_int8(q.to(dev), k.to(dev), v.to(dev), tau=tau, block=block, int8_pv=int8_pv)
+    torch.cuda.synchronize()
+    ref = oracle.prepare(bits(q), bits(k), bits(v), block=block, tau=tau, int8=True, int8_pv=int8_pv)
+    rows = _rows(B, H, ref["NT"], limit=16)
+    port = oracle.forward_int8_port(bits(q), bits(v), ref, rows, int8_pv=int8_pv)
+    err, cos = compare_rows(out.float().cpu().numpy(), port, block)
+    print(f"[fwd_int8] max|err|={err:.3e} cos={cos:.6f}", flush=True)
+    assert cos >= INT8_COS
+
+
+def test_strided_qkv_view(pkg, dev):
+    """An interleaved qkv buffer goes in as strided views, no copies needed."""
+    tri = _mods(pkg)[1]
+    B, T, H = 1, 900, 2
+    qkv = randn_bf16((B, T, 3, H, 128), 50).to(dev)
+    q, k, v = qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2]
+    a = tri.sol_attn(q, k, v, tau=0.7, block=64)
+    b = tri.sol_attn(q.contiguous(), k.contiguous(), v.contiguous(), tau=0.7, block=64)
+    assert torch.equal(a, b)
