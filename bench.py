@@ -1,15 +1,32 @@
 """Benchmark of the Sol-Attn sparse attention path on one MI355X.
 
-(placeholder: the measurement driver follows; this module already provides the
-synthetic workloads shared with the tests)
+Workload (the "32K tokens" of the headline metric):
+B=1, H=24, D=128, N=32760 tokens from a 21x30x52 latent grid (smooth seeded
+field + 0.2 N(0,1) noise), Morton 3d reordered, routing block 128, tau=0.9.
+
+A step is one sparse-attention call (``sol_attn``: pool -> moments -> route ->
+BF16 forward) on inputs already resident in HBM. Prints ONE JSON line:
+value = dense-equivalent TFLOPS (4*B*H*N^2*D / time per call), ms_per_step =
+ms per call, plus the roofline of the dominant kernel (the forward, timed alone
+with HIP events on its stream) and the CPU baseline (the oracle's masked
+attention path, timed on a bounded sample on this host).
+
+    python bench.py [--steps K] [--warmup W] [--config 2] [--no-cpu] [--extra]
 """
 
 from __future__ import annotations
 
+import argparse
+import json
 import math
+import os
+import sys
+import time
 
 import torch
 import torch.nn.functional as F
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
 
 # Workloads of BASELINE.json. grid = latent (T, H, W); coarse = seeded grid
 # that is trilinearly upsampled into a smooth field; sigma = noise level.
@@ -25,6 +42,10 @@ CONFIGS = {
     4: dict(name="long_video_75k", B=1, H=40, D=128, grid=(21, 60, 60), coarse=(4, 8, 8), sigma=0.2,
             block=128, tau=0.9, dtype="bf16", morton=True, k_offset=0.0),
 }
+
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_INT8_TOPS = 5000.0     # MI355X dense int8 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 
 
 def smooth_field(B, H, D, grid, coarse, sigma, seed, device="cpu"):
@@ -42,12 +63,196 @@ def smooth_field(B, H, D, grid, coarse, sigma, seed, device="cpu"):
 def make_inputs(cfg, device="cpu", dtype=None):
     """(q, k, v) for a config dict (seeds 0, 1, 2), cast to the config's dtype."""
     B, H, D = cfg["B"], cfg["H"], cfg["D"]
-    q = smooth_field(B, H, D, cfg["grid"], cfg["coarse"], cfg["sigma"], 0, device)
-    k = smooth_field(B, H, D, cfg["grid"], cfg["coarse"], cfg["sigma"], 1, device)
-    v = smooth_field(B, H, D, cfg["grid"], cfg["coarse"], cfg["sigma"], 2, device)
-    if cfg.get("k_offset"):
-        g = torch.Generator().manual_seed(3)
-        k = k + (cfg["k_offset"] * torch.randn(1, 1, H, D, generator=g)).to(device)
     if dtype is None:
         dtype = torch.float32 if cfg["dtype"] == "fp32" else torch.bfloat16
-    return q.to(dtype), k.to(dtype), v.to(dtype)
+    out = []
+    for seed in (0, 1, 2):
+        t = smooth_field(B, H, D, cfg["grid"], cfg["coarse"], cfg["sigma"], seed, device)
+        if seed == 1 and cfg.get("k_offset"):
+            g = torch.Generator().manual_seed(3)
+            t = t + (cfg["k_offset"] * torch.randn(1, 1, H, D, generator=g)).to(device)
+        out.append(t.to(dtype))
+        del t
+    return tuple(out)
+
+
+def dense_flops(B, H, N, D):
+    return 4.0 * B * H * N * N * D
+
+
+def routed_flops(counts, mask, T, block, D):
+    """Algorithmic FLOPs of the forward on valid tokens:
+    4*D*sum_{b,h,i} len_i * (sum_{j exact} len_j + |approx(i)|)."""
+    NT = (T + block - 1) // block
+    lens = torch.full((NT,), float(block), dtype=torch.float64)
+    lens[-1] = T - (NT - 1) * block
+    j = torch.arange(NT)
+    words = mask.to(torch.int64)[..., j >> 5] & 0xFFFFFFFF
+    ex = ((words >> (j & 31)) & 1).bool()  # [B,H,NT,NT]
+    exact_tok = (ex.double() * lens).sum(-1)
+    n_approx = (~ex).sum(-1).double()
+    return float(4 * D * (lens * (exact_tok + n_approx)).sum())
+
+
+def time_cuda(fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def _pkg():
+    sys.path.insert(0, ROOT)
+    from __graft_entry__ import PKG_NAME, load_package
+    import importlib
+
+    load_package()
+    return {m: importlib.import_module(f"{PKG_NAME}.{m}")
+            for m in ("_tri_fwd", "_int8_fwd", "_preprocess", "_fused_prep", "_morton")}
+
+
+def cpu_baseline(cfg, q, k, v, budget_s=15.0):
+    """The oracle's masked-attention CPU path (torch fp32, augmented keys, one
+    query block at a time) on a bounded sample of query blocks; the oracle's C
+    routing runs on the full input. Extrapolated to ms per call."""
+    sys.path.insert(0, ROOT)
+    import numpy as np
+    import oracle  # test infrastructure: the CPU baseline leg only
+
+    threads = torch.get_num_threads()
+    bits = lambda t: t.contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
+    qb, kb, vb = bits(q), bits(k), bits(v)
+    t0 = time.perf_counter()
+    prep = oracle.prepare(qb, kb, vb, block=cfg["block"], tau=cfg["tau"])
+    t_prep = time.perf_counter() - t0
+    B, T, H, D = q.shape
+    NT = prep["NT"]
+    qf, kf, vf = (t.float().cpu() for t in (q, k, v))
+    rng = np.random.default_rng(0)
+    order = [(h, i) for h in range(H) for i in range(NT)]
+    rng.shuffle(order)
+    done, t_attn = 0, 0.0
+    while done < len(order) and t_attn < budget_s:
+        h, i = order[done]
+        t1 = time.perf_counter()
+        oracle.masked_attention_torch(qf, kf, vf, prep, heads=[h], qblocks=[i])
+        t_attn += time.perf_counter() - t1
+        done += 1
+    per_call_s = t_prep + t_attn * (len(order) / done)
+    return {
+        "value": round(per_call_s * 1e3, 1),
+        "unit": "ms/call",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"oracle C routing on the full input ({t_prep:.2f} s) + torch-fp32 masked "
+                   f"attention over [tokens; pooled keys] for {done} of {len(order)} "
+                   f"(head, query-block) pairs ({t_attn:.1f} s), scaled to the full call"),
+        "dense_equiv_tflops": round(dense_flops(B, H, T, D) / per_call_s / 1e12, 4),
+    }
+
+
+def _traffic():
+    """HBM bytes per forward launch from the committed rocprofv3 --pmc summary."""
+    path = os.path.join(ROOT, "profiles", "fwd_bf16_video32k_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get("bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", type=int, default=2)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--extra", action="store_true", help="also time INT8 (cfg 3) and cfg 4")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(heads shard with no communication; see the sharding notes).", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        sys.exit(2)
+
+    mods = _pkg()
+    dev = torch.device("cuda:0")
+    cfg = CONFIGS[args.config]
+    print(f"[bench] config {args.config} {cfg['name']}: generating inputs", file=sys.stderr, flush=True)
+    q, k, v = make_inputs(cfg, dev)
+    B, T, H, D = q.shape
+    block, tau = cfg["block"], cfg["tau"]
+    reorder_ms = None
+    if cfg["morton"]:
+        perm, inv = mods["_morton"].morton_perm(cfg["grid"], dev, "3d")
+        q, k, v = (mods["_morton"].reorder_tokens(t, perm, dim=1) for t in (q, k, v))
+        reorder_ms = time_cuda(lambda: mods["_morton"].reorder_tokens(q, perm, dim=1), 10, 2)
+    torch.cuda.synchronize()
+
+    sol_attn = mods["_tri_fwd"].sol_attn
+    step = lambda: sol_attn(q, k, v, tau=tau, block=block)
+    print("[bench] timing sol_attn", file=sys.stderr, flush=True)
+    ms = time_cuda(step, args.steps, args.warmup)
+
+    r = mods["_preprocess"].route(q, k, v, scale=D ** -0.5, tau=tau, block=block)
+    out = torch.empty_like(q)
+    fwd = lambda: mods["_tri_fwd"].forward_bf16(q, k, v, r, out=out)
+    fwd_ms = time_cuda(fwd, args.steps, args.warmup)
+    prep_ms = time_cuda(lambda: mods["_preprocess"].route(q, k, v, scale=D ** -0.5, tau=tau,
+                                                          block=block), args.steps, args.warmup)
+    counts = r.counts.cpu()
+    NT = counts.shape[-1]
+    density = float(counts.double().sum() / (B * H * NT * NT))
+    rflops = routed_flops(counts, r.mask.cpu(), T, block, D)
+    dflops = dense_flops(B, H, T, D)
+    achieved = rflops / (fwd_ms * 1e-3) / 1e12
+    line = {
+        "metric": "ms/attention call + dense-equiv TFLOPS at 32K tokens, % of MFMA peak",
+        "value": round(dflops / (ms * 1e-3) / 1e12, 2),
+        "unit": "TFLOPS (dense-equivalent, one sparse attention call)",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded smooth field + noise, Morton 3d reordered)",
+        "config": {"workload": f"cfg{args.config} {cfg['name']}: B{B} H{H} D{D} N{T} grid "
+                               f"{'x'.join(map(str, cfg['grid']))} block {block} tau {tau}",
+                   "global_batch": B, "seq_len": T, "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": _traffic(), "kernel": "fwd_bf16_kernel<128>",
+                     "algorithmic_flops_per_launch": rflops, "launch_ms": round(fwd_ms, 4)},
+        "routed_density": round(density, 4),
+        "prep_ms": round(prep_ms, 4),
+        "fwd_ms": round(fwd_ms, 4),
+        "dense_equiv_tflops_fwd_only": round(dflops / (fwd_ms * 1e-3) / 1e12, 2),
+        "reorder_ms_per_tensor": None if reorder_ms is None else round(reorder_ms, 4),
+        "reorder_GBps": None if reorder_ms is None else round(2 * q.numel() * 2 / (reorder_ms * 1e-3) / 1e9, 1),
+    }
+    del r, out
+    if args.extra:
+        i8 = mods["_int8_fwd"].sol_attn_int8
+        line["int8_ms"] = {str(t): round(time_cuda(lambda: i8(q, k, v, tau=t, block=block), args.steps,
+                                                   args.warmup), 4) for t in (0.8, 0.9, 0.95)}
+    if not args.no_cpu:
+        print("[bench] CPU baseline", file=sys.stderr, flush=True)
+        line["cpu_baseline"] = cpu_baseline(cfg, q, k, v, args.cpu_budget)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

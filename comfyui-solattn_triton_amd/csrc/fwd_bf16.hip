@@ -11,15 +11,16 @@
 // MFMA dataflow (v_mfma_f32_32x32x16_bf16): S^T = K . Q^T puts one query row
 // per lane column, so row max / sum need one cross-lane step (lane ^ 32) and
 // the S accumulator converts in place into the B operand of O^T += V^T . P^T.
-// V is transposed into LDS on the way in. Rows of K and Vt are padded so the
-// 16-byte (K) and 8-byte (Vt) LDS reads are bank-conflict free.
+// Tiles are copied global -> LDS directly (no VGPR staging, so two waves fit
+// per SIMD); V stays row-major and ds_read_tr16_b64 delivers it transposed as
+// the MFMA A operand. XOR-swizzled chunks keep the LDS reads conflict free.
 #include "common.hpp"
 #include "fwd_common.hpp"
 
 namespace solattn {
 
 template <int BLK>
-__global__ void __launch_bounds__(BLK * 2)
+__global__ void __launch_bounds__(BLK * 2, 2)
 fwd_bf16_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
                 const uint16_t* __restrict__ k, int64_t sk_b, int64_t sk_t, int64_t sk_h,
                 const uint16_t* __restrict__ v, int64_t sv_b, int64_t sv_t, int64_t sv_h,
@@ -28,7 +29,8 @@ fwd_bf16_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
                 const uint32_t* __restrict__ mask, int T, int H, int NT, int W, float c,
                 uint16_t* __restrict__ o, int64_t so_b, int64_t so_t, int64_t so_h) {
   constexpr int NTHREADS = BLK * 2;
-  __shared__ FwdShared<BLK> sh;
+  __shared__ SwzBuf buf[2];
+  __shared__ TileList tl;
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int col = lane & 31, half = lane >> 5;
@@ -37,8 +39,13 @@ fwd_bf16_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
   const int b = bh / H, h = bh % H;
   const int64_t row = static_cast<int64_t>(bh) * NT + qb;
 
-  const int ntiles = build_tile_list<BLK>(sh, counts, lists, mask, row, NT, W, T);
+  const int ntiles = build_tile_list<BLK>(tl, counts, lists, mask, row, NT, W, T);
   if (ntiles == 0) return;  // cannot happen for routed lists: the diagonal is exact
+
+  const KVSource src{k + b * sk_b + h * sk_h, sk_t, v + b * sv_b + h * sv_h, sv_t,
+                     kc + (static_cast<int64_t>(b) * npad * H + h) * kD,
+                     static_cast<int64_t>(H) * kD, vc + (static_cast<int64_t>(b) * npad * H + h) * kD};
+  issue_tile<BLK, NTHREADS>(buf[0], tl, 0, src, T, NT);
 
   // This wave's 32 query rows as the B operand of S^T = K Q^T.
   const int qrow = qb * BLK + wave * 32 + col;
@@ -53,29 +60,24 @@ fwd_bf16_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
     }
   }
 
-  const KVSource src{k + b * sk_b + h * sk_h, sk_t, v + b * sv_b + h * sv_h, sv_t,
-                     kc + (static_cast<int64_t>(b) * npad * H + h) * 128,
-                     static_cast<int64_t>(H) * 128, vc + (static_cast<int64_t>(b) * npad * H + h) * 128};
-
   SoftmaxState st;
   st.init();
-
-  TileRegs<NTHREADS> regs;
-  load_tile<BLK, NTHREADS>(regs, sh, 0, src, T, NT);
-  store_tile<NTHREADS>(regs, sh.buf[0]);
+  wait_tile_copies();
   __syncthreads();
 
   for (int n = 0; n < ntiles; ++n) {
-    if (n + 1 < ntiles) load_tile<BLK, NTHREADS>(regs, sh, n + 1, src, T, NT);
-    const TileDesc td = tile_desc<BLK>(sh, n, T, NT);
-    const TileBuf& tb = sh.buf[n & 1];
+    // Tile n+1 streams into the other buffer while tile n is computed; that
+    // buffer's last readers finished before the barrier that ended tile n-1.
+    if (n + 1 < ntiles) issue_tile<BLK, NTHREADS>(buf[(n + 1) & 1], tl, n + 1, src, T, NT);
+    const TileDesc td = tile_desc<BLK>(tl, n, T, NT);
+    const SwzBuf& tb = buf[n & 1];
 
     f32x16 s[2];
-    qk_bf16(tb, qreg, col, half, s);
+    qk_swz(tb, qreg, col, half, s);
     softmax_update<BLK>(st, s, td, c, half, NT, T);
-    pv_bf16(tb, s, col, half, st.acc);
+    pv_tr16(tb, s, lane, st.acc);
 
-    if (n + 1 < ntiles) store_tile<NTHREADS>(regs, sh.buf[(n + 1) & 1]);
+    wait_tile_copies();
     __syncthreads();
   }
 

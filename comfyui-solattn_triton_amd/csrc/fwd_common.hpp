@@ -1,11 +1,10 @@
 // Building blocks shared by the BF16 and INT8 Sol-Attn forwards on gfx950.
 //
 // A workgroup serves one query block (BLK rows, BLK/32 waves of 32 rows).
-// Its work is a sequence of 64-key tiles: first the pooled tiles (chunks of 64
-// pooled keys with at least one approximate block), then the exact tiles (64
-// tokens each, BLK/64 per exact block, ascending block order). Tiles are
-// staged in LDS, double buffered: K row-major [64][136] and V transposed
-// [128][68] (bf16 elements, padded rows).
+// Its work is a sequence of 64-key tiles: pooled tiles (chunks of 64 pooled
+// keys with at least one approximate block) and exact tiles (64 tokens each,
+// BLK/64 per exact block, ascending block order). Tiles are staged in LDS,
+// double buffered.
 #pragma once
 
 #include "common.hpp"
@@ -14,19 +13,14 @@ namespace solattn {
 
 constexpr int kKeys = 64;             // keys per tile
 constexpr int kD = 128;               // head dim
-constexpr int kKStride = kD + 8;      // bf16 per K row in LDS (272 B)
-constexpr int kVStride = kKeys + 4;   // bf16 per V^T row in LDS (136 B)
 constexpr int kMaxNT = 2048;          // query/key blocks per head
 constexpr int kMaxPool = kMaxNT / 64; // pooled tiles per query block
 
-struct TileBuf {
-  uint16_t k[kKeys * kKStride];
-  uint16_t vt[kD * kVStride];
-};
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void glb_void_t;
 
-template <int BLK>
-struct FwdShared {
-  TileBuf buf[2];
+// ----------------------------------------------------------------- tile list
+struct TileList {
   uint64_t pmask[kMaxPool];  // approximate-block mask of each pooled tile
   int16_t pchunk[kMaxPool];  // pooled tile -> chunk of 64 pooled keys
   int16_t blist[kMaxNT];     // exact key blocks, ascending
@@ -62,11 +56,11 @@ __device__ __forceinline__ void tile_coords(uint32_t w, uint32_t total, int NT, 
 }
 
 template <int BLK>
-__device__ int build_tile_list(FwdShared<BLK>& sh, const int32_t* __restrict__ counts,
+__device__ int build_tile_list(TileList& tl, const int32_t* __restrict__ counts,
                                const int16_t* __restrict__ lists, const uint32_t* __restrict__ mask,
                                int64_t row, int NT, int W, int T) {
   const int cnt = min(max(counts[row], 0), NT);
-  for (int e = threadIdx.x; e < cnt; e += blockDim.x) sh.blist[e] = lists[row * NT + e];
+  for (int e = threadIdx.x; e < cnt; e += blockDim.x) tl.blist[e] = lists[row * NT + e];
   if (threadIdx.x == 0) {
     const uint32_t* mrow = mask + row * W;
     int np = 0;
@@ -77,34 +71,35 @@ __device__ int build_tile_list(FwdShared<BLK>& sh, const int32_t* __restrict__ c
       const uint64_t valid = nvalid >= 64 ? ~0ull : ((1ull << nvalid) - 1ull);
       const uint64_t ap = ~ex & valid;
       if (ap) {
-        sh.pmask[np] = ap;
-        sh.pchunk[np] = static_cast<int16_t>(c);
+        tl.pmask[np] = ap;
+        tl.pchunk[np] = static_cast<int16_t>(c);
         ++np;
       }
     }
-    sh.npool = np;
+    tl.npool = np;
     constexpr int S = BLK / kKeys;
     int ne = cnt * S;
     const int tail = T - (NT - 1) * BLK;
     if (S == 2 && cnt > 0 && lists[row * NT + cnt - 1] == NT - 1 && tail <= kKeys) ne -= 1;
-    sh.nexact = ne;
+    tl.nexact = ne;
   }
   __syncthreads();
-  return sh.npool + sh.nexact;
+  return tl.npool + tl.nexact;
 }
 
+// Tile n: pooled tiles first (n < npool), then exact tiles.
 template <int BLK>
-__device__ __forceinline__ TileDesc tile_desc(const FwdShared<BLK>& sh, int n, int T, int NT) {
+__device__ __forceinline__ TileDesc tile_desc(const TileList& tl, int n, int T, int NT) {
   TileDesc td;
-  if (n < sh.npool) {
+  if (n < tl.npool) {
     td.pooled = 1;
-    td.first = sh.pchunk[n] * kKeys;
+    td.first = tl.pchunk[n] * kKeys;
     td.nvalid = min(kKeys, NT - td.first);
-    td.amask = sh.pmask[n];
+    td.amask = tl.pmask[n];
   } else {
     constexpr int S = BLK / kKeys;
-    const int e = n - sh.npool;
-    const int j = min(max(static_cast<int>(sh.blist[e / S]), 0), NT - 1);
+    const int e = n - tl.npool;
+    const int j = min(max(static_cast<int>(tl.blist[e / S]), 0), NT - 1);
     td.pooled = 0;
     td.first = j * BLK + (e % S) * kKeys;
     td.nvalid = max(0, min(kKeys, T - td.first));
@@ -113,81 +108,54 @@ __device__ __forceinline__ TileDesc tile_desc(const FwdShared<BLK>& sh, int n, i
   return td;
 }
 
-// Per-thread share of one tile on its way from HBM to LDS.
-template <int NTHREADS>
-struct TileRegs {
-  static constexpr int KCH = kKeys * kD / 8 / NTHREADS;  // 16-byte K chunks
-  static constexpr int VU = kKeys * kD / 32 / NTHREADS;  // 4-key x 8-channel V units
-  uint4 k[KCH];
-  uint4 v[VU][4];
+// ------------------------------------------------------------- direct tiles
+// K and V rows (64 keys x 128 bf16 = 16 chunks of 16 bytes) copied global ->
+// LDS without passing through VGPRs. Row-major, chunks XOR-swizzled:
+//   K: physical chunk = chunk ^ (row & 7)      (16-byte MFMA operand reads)
+//   V: physical chunk = chunk ^ 2*(row & 7)    (ds_read_tr16_b64 reads, which
+//      take 32 contiguous bytes = a chunk pair per row)
+struct SwzBuf {
+  uint16_t k[kKeys * kD];
+  uint16_t v[kKeys * kD];
 };
 
-__device__ __forceinline__ uint4 ld16(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
+__device__ __forceinline__ int swz_k(int row, int chunk) { return chunk ^ (row & 7); }
+__device__ __forceinline__ int swz_v(int row, int chunk) { return chunk ^ ((row & 7) << 1); }
 
+__device__ __forceinline__ void g2l16(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds((glb_void_t*)g, (lds_void_t*)lds, 16, 0, 0);
+}
+
+// Issue the copies of tile n into buf. Each instruction moves 64 lanes x 16 B
+// into 1 KiB of LDS at (wave base + 16 * lane); lane e of the tile fills
+// physical chunk e, so it fetches the logical chunk that lands there. Rows past
+// nvalid re-read row 0 of the tile (finite data, masked out of the softmax).
 template <int BLK, int NTHREADS>
-__device__ __forceinline__ void load_tile(TileRegs<NTHREADS>& r, const FwdShared<BLK>& sh, int n,
-                                          const KVSource& src, int T, int NT) {
-  const TileDesc td = tile_desc<BLK>(sh, n, T, NT);
+__device__ __forceinline__ void issue_tile(SwzBuf& buf, const TileList& tl, int n,
+                                           const KVSource& src, int T, int NT) {
+  const TileDesc td = tile_desc<BLK>(tl, n, T, NT);
   const uint16_t* kb = td.pooled ? src.kc : src.k;
   const uint16_t* vb = td.pooled ? src.vc : src.v;
   const int64_t ks = td.pooled ? src.skc : src.sk;
   const int64_t vs = td.pooled ? src.skc : src.sv;
-  const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+  const int wave_base = threadIdx.x & ~63;
 #pragma unroll
-  for (int u = 0; u < TileRegs<NTHREADS>::KCH; ++u) {
+  for (int u = 0; u < kKeys * 16 / NTHREADS; ++u) {
     const int e = threadIdx.x + NTHREADS * u;
-    const int row = e >> 4, cc = e & 15;
-    r.k[u] = row < td.nvalid ? ld16(kb + static_cast<int64_t>(td.first + row) * ks + cc * 8) : z;
-  }
-#pragma unroll
-  for (int u = 0; u < TileRegs<NTHREADS>::VU; ++u) {
-    const int e = threadIdx.x + NTHREADS * u;
-    const int kq = e & 15, dc = e >> 4;
-#pragma unroll
-    for (int x = 0; x < 4; ++x) {
-      const int row = 4 * kq + x;
-      r.v[u][x] = row < td.nvalid ? ld16(vb + static_cast<int64_t>(td.first + row) * vs + dc * 8) : z;
-    }
+    const int row = e >> 4, pc = e & 15;
+    const int srow = td.first + (row < td.nvalid ? row : 0);
+    const int lds_chunk = wave_base + NTHREADS * u;  // first chunk this wave writes
+    g2l16(kb + static_cast<int64_t>(srow) * ks + swz_k(row, pc) * 8, &buf.k[lds_chunk * 8]);
+    g2l16(vb + static_cast<int64_t>(srow) * vs + swz_v(row, pc) * 8, &buf.v[lds_chunk * 8]);
   }
 }
 
-__device__ __forceinline__ uint32_t word_of(const uint4& a, int w) {
-  return w == 0 ? a.x : (w == 1 ? a.y : (w == 2 ? a.z : a.w));
-}
-
-template <int NTHREADS>
-__device__ __forceinline__ void store_tile(const TileRegs<NTHREADS>& r, TileBuf& buf) {
-#pragma unroll
-  for (int u = 0; u < TileRegs<NTHREADS>::KCH; ++u) {
-    const int e = threadIdx.x + NTHREADS * u;
-    const int row = e >> 4, cc = e & 15;
-    *reinterpret_cast<uint4*>(&buf.k[row * kKStride + cc * 8]) = r.k[u];
-  }
-#pragma unroll
-  for (int u = 0; u < TileRegs<NTHREADS>::VU; ++u) {
-    const int e = threadIdx.x + NTHREADS * u;
-    const int kq = e & 15, dc = e >> 4;
-#pragma unroll
-    for (int el = 0; el < 8; ++el) {
-      const uint32_t a0 = word_of(r.v[u][0], el >> 1), a1 = word_of(r.v[u][1], el >> 1);
-      const uint32_t a2 = word_of(r.v[u][2], el >> 1), a3 = word_of(r.v[u][3], el >> 1);
-      uint2 p;
-      if ((el & 1) == 0) {
-        p.x = (a0 & 0xffffu) | (a1 << 16);
-        p.y = (a2 & 0xffffu) | (a3 << 16);
-      } else {
-        p.x = (a0 >> 16) | (a1 & 0xffff0000u);
-        p.y = (a2 >> 16) | (a3 & 0xffff0000u);
-      }
-      *reinterpret_cast<uint2*>(&buf.vt[(dc * 8 + el) * kVStride + 4 * kq]) = p;
-    }
-  }
-}
+__device__ __forceinline__ void wait_tile_copies() { __builtin_amdgcn_s_waitcnt(0); }
 
 // S^T (64 keys x 32 query rows of this wave) = K . Q^T. s[m] covers keys
 // 32m + 8(r/4) + 4*half + (r%4) for accumulator element r, query row `col`.
-__device__ __forceinline__ void qk_bf16(const TileBuf& tb, const bf16x8 (&qreg)[8], int col, int half,
-                                        f32x16 (&s)[2]) {
+__device__ __forceinline__ void qk_swz(const SwzBuf& tb, const bf16x8 (&qreg)[8], int col, int half,
+                                       f32x16 (&s)[2]) {
 #pragma unroll
   for (int m = 0; m < 2; ++m)
 #pragma unroll
@@ -196,13 +164,55 @@ __device__ __forceinline__ void qk_bf16(const TileBuf& tb, const bf16x8 (&qreg)[
   for (int cc = 0; cc < 8; ++cc) {
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
+      const int row = 32 * m + col;
       const bf16x8 a =
-          *reinterpret_cast<const bf16x8*>(&tb.k[(32 * m + col) * kKStride + cc * 16 + half * 8]);
+          *reinterpret_cast<const bf16x8*>(&tb.k[row * kD + swz_k(row, 2 * cc + half) * 8]);
       s[m] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qreg[cc], s[m], 0, 0, 0);
     }
   }
 }
 
+__device__ __forceinline__ bf16x4 tr16(const uint16_t* p) {
+  typedef short v4i16 __attribute__((ext_vector_type(4)));
+  const v4i16 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) v4i16*)(p));
+  return __builtin_bit_cast(bf16x4, r);
+}
+
+__device__ __forceinline__ bf16x8 to_bf16x8(const f32x16& s, int off) {
+  bf16x8 b;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) b[e] = static_cast<__bf16>(s[off + e]);
+  return b;
+}
+
+// O^T += V^T . P^T over the tile's 64 keys, 16 keys per MFMA step. V is
+// row-major in LDS; ds_read_tr16_b64 hands lane l the 4 keys
+// 16ks + 4*half + k (k = 0..3) of channel 32dt + (l % 32): within each 16-lane
+// group, lane s supplies row 16ks + 4*half + s/4, channels 4*(s%4) .. +3.
+__device__ __forceinline__ void pv_tr16(const SwzBuf& tb, const f32x16 (&p)[2], int lane,
+                                        f32x16 (&acc)[4]) {
+  const int g = lane >> 4, sl = lane & 15;
+  const int half = g >> 1;
+  const int sub = sl & 1;                       // 8-byte half of the 16-byte chunk
+  const int cpair = 2 * (g & 1) + ((sl & 3) >> 1);
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    const bf16x8 b = to_bf16x8(p[ks >> 1], 8 * (ks & 1));
+    const int row0 = 16 * ks + 4 * half + (sl >> 2);
+    const int row1 = row0 + 8;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      const int chunk = 4 * dt + cpair;
+      const bf16x4 lo = tr16(&tb.v[row0 * kD + swz_v(row0, chunk) * 8 + sub * 4]);
+      const bf16x4 hi = tr16(&tb.v[row1 * kD + swz_v(row1, chunk) * 8 + sub * 4]);
+      const bf16x8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[dt], 0, 0, 0);
+    }
+  }
+}
+
+// ------------------------------------------------------------ online softmax
 struct SoftmaxState {
   float m;          // running max, in the exp2 domain (score * c)
   float l;          // partial row sum over this lane's keys
@@ -273,30 +283,6 @@ __device__ __forceinline__ void softmax_update(SoftmaxState& st, f32x16 (&s)[2],
   st.m = m_new;
 }
 
-__device__ __forceinline__ bf16x8 to_bf16x8(const f32x16& s, int off) {
-  bf16x8 b;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) b[e] = static_cast<__bf16>(s[off + e]);
-  return b;
-}
-
-// O^T += V^T . P^T over the tile's 64 keys, 16 keys per MFMA step.
-__device__ __forceinline__ void pv_bf16(const TileBuf& tb, const f32x16 (&p)[2], int col, int half,
-                                        f32x16 (&acc)[4]) {
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    const bf16x8 b = to_bf16x8(p[ks >> 1], 8 * (ks & 1));
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-      const uint16_t* vrow = &tb.vt[(32 * dt + col) * kVStride + 16 * ks + 4 * half];
-      const bf16x4 lo = *reinterpret_cast<const bf16x4*>(vrow);
-      const bf16x4 hi = *reinterpret_cast<const bf16x4*>(vrow + 8);
-      const bf16x8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-      acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[dt], 0, 0, 0);
-    }
-  }
-}
-
 // o[qrow, :] = acc / l (bf16), rows past T skipped.
 __device__ __forceinline__ void store_output(const SoftmaxState& st, uint16_t* __restrict__ obase,
                                              int64_t so_t, int qrow, int T, int half) {
@@ -315,6 +301,121 @@ __device__ __forceinline__ void store_output(const SoftmaxState& st, uint16_t* _
     }
 }
 
+// ----------------------------------------------------- register-staged tiles
+// (INT8 forward): each thread loads its share into VGPRs, then writes it to LDS
+// with V transposed on the way. K row-major [64][136], V^T [128][68].
+constexpr int kKStride = kD + 8;      // bf16 per K row in LDS (272 B)
+constexpr int kVStride = kKeys + 4;   // bf16 per V^T row in LDS (136 B)
+
+struct TileBuf {
+  uint16_t k[kKeys * kKStride];
+  uint16_t vt[kD * kVStride];
+};
+
+template <int NTHREADS>
+struct TileRegs {
+  static constexpr int KCH = kKeys * kD / 8 / NTHREADS;  // 16-byte K chunks
+  static constexpr int VU = kKeys * kD / 32 / NTHREADS;  // 4-key x 8-channel V units
+  uint4 k[KCH];
+  uint4 v[VU][4];
+};
+
+__device__ __forceinline__ uint4 ld16(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
+
+template <int BLK, int NTHREADS>
+__device__ __forceinline__ void load_tile(TileRegs<NTHREADS>& r, const TileList& tl, int n,
+                                          const KVSource& src, int T, int NT) {
+  const TileDesc td = tile_desc<BLK>(tl, n, T, NT);
+  const uint16_t* kb = td.pooled ? src.kc : src.k;
+  const uint16_t* vb = td.pooled ? src.vc : src.v;
+  const int64_t ks = td.pooled ? src.skc : src.sk;
+  const int64_t vs = td.pooled ? src.skc : src.sv;
+  const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+  for (int u = 0; u < TileRegs<NTHREADS>::KCH; ++u) {
+    const int e = threadIdx.x + NTHREADS * u;
+    const int row = e >> 4, cc = e & 15;
+    r.k[u] = row < td.nvalid ? ld16(kb + static_cast<int64_t>(td.first + row) * ks + cc * 8) : z;
+  }
+#pragma unroll
+  for (int u = 0; u < TileRegs<NTHREADS>::VU; ++u) {
+    const int e = threadIdx.x + NTHREADS * u;
+    const int kq = e & 15, dc = e >> 4;
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+      const int row = 4 * kq + x;
+      r.v[u][x] = row < td.nvalid ? ld16(vb + static_cast<int64_t>(td.first + row) * vs + dc * 8) : z;
+    }
+  }
+}
+
+__device__ __forceinline__ uint32_t word_of(const uint4& a, int w) {
+  return w == 0 ? a.x : (w == 1 ? a.y : (w == 2 ? a.z : a.w));
+}
+
+template <int NTHREADS>
+__device__ __forceinline__ void store_tile(const TileRegs<NTHREADS>& r, TileBuf& buf) {
+#pragma unroll
+  for (int u = 0; u < TileRegs<NTHREADS>::KCH; ++u) {
+    const int e = threadIdx.x + NTHREADS * u;
+    const int row = e >> 4, cc = e & 15;
+    *reinterpret_cast<uint4*>(&buf.k[row * kKStride + cc * 8]) = r.k[u];
+  }
+#pragma unroll
+  for (int u = 0; u < TileRegs<NTHREADS>::VU; ++u) {
+    const int e = threadIdx.x + NTHREADS * u;
+    const int kq = e & 15, dc = e >> 4;
+#pragma unroll
+    for (int el = 0; el < 8; ++el) {
+      const uint32_t a0 = word_of(r.v[u][0], el >> 1), a1 = word_of(r.v[u][1], el >> 1);
+      const uint32_t a2 = word_of(r.v[u][2], el >> 1), a3 = word_of(r.v[u][3], el >> 1);
+      uint2 p;
+      if ((el & 1) == 0) {
+        p.x = (a0 & 0xffffu) | (a1 << 16);
+        p.y = (a2 & 0xffffu) | (a3 << 16);
+      } else {
+        p.x = (a0 >> 16) | (a1 & 0xffff0000u);
+        p.y = (a2 >> 16) | (a3 & 0xffff0000u);
+      }
+      *reinterpret_cast<uint2*>(&buf.vt[(dc * 8 + el) * kVStride + 4 * kq]) = p;
+    }
+  }
+}
+
+__device__ __forceinline__ void qk_bf16(const TileBuf& tb, const bf16x8 (&qreg)[8], int col, int half,
+                                        f32x16 (&s)[2]) {
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[m][r] = 0.f;
+#pragma unroll
+  for (int cc = 0; cc < 8; ++cc) {
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const bf16x8 a =
+          *reinterpret_cast<const bf16x8*>(&tb.k[(32 * m + col) * kKStride + cc * 16 + half * 8]);
+      s[m] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qreg[cc], s[m], 0, 0, 0);
+    }
+  }
+}
+
+__device__ __forceinline__ void pv_bf16(const TileBuf& tb, const f32x16 (&p)[2], int col, int half,
+                                        f32x16 (&acc)[4]) {
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    const bf16x8 b = to_bf16x8(p[ks >> 1], 8 * (ks & 1));
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      const uint16_t* vrow = &tb.vt[(32 * dt + col) * kVStride + 16 * ks + 4 * half];
+      const bf16x4 lo = *reinterpret_cast<const bf16x4*>(vrow);
+      const bf16x4 hi = *reinterpret_cast<const bf16x4*>(vrow + 8);
+      const bf16x8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[dt], 0, 0, 0);
+    }
+  }
+}
+
+// ------------------------------------------------------------ argument checks
 inline int check_fwd_common(const void* q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
                             const void* kc, const void* vc, int64_t npad, const int32_t* counts,
                             const int16_t* lists, const uint32_t* mask, int64_t B, int64_t T,

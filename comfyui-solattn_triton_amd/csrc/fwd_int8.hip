@@ -46,7 +46,7 @@ struct I8Source {
 
 // INT8 tiles first (n < nexact), then pooled tiles.
 template <int BLK>
-__device__ __forceinline__ TileDesc tile_desc_i8(const FwdShared<BLK>& sh, int n, int T, int NT) {
+__device__ __forceinline__ TileDesc tile_desc_i8(const TileList& sh, int n, int T, int NT) {
   if (n < sh.nexact) {
     // tile_desc() numbers exact tiles after the pooled ones
     return tile_desc<BLK>(sh, n + sh.npool, T, NT);
@@ -56,7 +56,7 @@ __device__ __forceinline__ TileDesc tile_desc_i8(const FwdShared<BLK>& sh, int n
 
 template <int BLK, int NTHREADS, bool INT8_PV>
 __device__ __forceinline__ void load_tile_i8(TileRegs<NTHREADS>& r, float& ksr,
-                                             const FwdShared<BLK>& sh, int n, const KVSource& src,
+                                             const TileList& sh, int n, const KVSource& src,
                                              const I8Source& is, int T, int NT) {
   const TileDesc td = tile_desc_i8<BLK>(sh, n, T, NT);
   if (td.pooled) {
@@ -184,7 +184,8 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
                 const uint32_t* __restrict__ mask, int T, int H, int NT, int W, float c,
                 uint16_t* __restrict__ o, int64_t so_b, int64_t so_t, int64_t so_h) {
   constexpr int NTHREADS = BLK * 2;
-  __shared__ FwdShared<BLK> sh;
+  __shared__ TileBuf tbufs[2];
+  __shared__ TileList sh;
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int col = lane & 31, half = lane >> 5;
@@ -237,13 +238,13 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
   TileRegs<NTHREADS> regs;
   float ksr = 0.f;
   load_tile_i8<BLK, NTHREADS, INT8_PV>(regs, ksr, sh, 0, src, is, T, NT);
-  store_tile_i8<BLK, NTHREADS, INT8_PV>(regs, ksr, 0 >= nexact, sh.buf[0]);
+  store_tile_i8<BLK, NTHREADS, INT8_PV>(regs, ksr, 0 >= nexact, tbufs[0]);
   __syncthreads();
 
   for (int n = 0; n < ntiles; ++n) {
     if (n + 1 < ntiles) load_tile_i8<BLK, NTHREADS, INT8_PV>(regs, ksr, sh, n + 1, src, is, T, NT);
     const TileDesc td = tile_desc_i8<BLK>(sh, n, T, NT);
-    const TileBuf& tb = sh.buf[n & 1];
+    const TileBuf& tb = tbufs[n & 1];
 
     if (td.pooled) {
       f32x16 s[2];
@@ -350,7 +351,7 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
     }
 
     if (n + 1 < ntiles)
-      store_tile_i8<BLK, NTHREADS, INT8_PV>(regs, ksr, n + 1 >= nexact, sh.buf[(n + 1) & 1]);
+      store_tile_i8<BLK, NTHREADS, INT8_PV>(regs, ksr, n + 1 >= nexact, tbufs[(n + 1) & 1]);
     __syncthreads();
   }
 

@@ -93,21 +93,33 @@ int or_morton_perm(int64_t frames, int64_t height, int64_t width, int curve, int
 /* ------------------------------------------------------------------ pool --
  * /root/reference/_preprocess.py:49-57 (kc = sum/len), :100 (vc = sum),
  * :106-113 (per-block |v| max), :140-149 (q centroid = sum/len).
- * x: bf16 BTHD with element strides; rows t >= T read as 0. */
-static float pooled_sum(const uint16_t* x, int64_t s_b, int64_t s_t, int64_t s_h, int64_t b,
-                        int64_t t0, int64_t T, int64_t h, int64_t d, int64_t block,
-                        float* amax) {
-  float p[4] = {0.f, 0.f, 0.f, 0.f};
-  float m = 0.f;
+ * x: bf16 BTHD with element strides; rows t >= T read as 0. For every
+ * (head, channel) four partials take rows r = g (mod 4) in ascending order and
+ * combine as (p0 + p1) + (p2 + p3); rows are streamed so the loop is cache-friendly. */
+static void pool_one(const uint16_t* x, int64_t s_b, int64_t s_t, int64_t s_h, int64_t b,
+                     int64_t t0, int64_t T, int64_t H, int64_t D, int64_t block, float* part,
+                     float* amax, float* out_sum) {
+  int64_t HD = H * D;
+  for (int64_t e = 0; e < 4 * HD; ++e) part[e] = 0.f;
+  if (amax)
+    for (int64_t e = 0; e < HD; ++e) amax[e] = 0.f;
   for (int64_t r = 0; r < block; ++r) {
     int64_t t = t0 + r;
-    float val = t < T ? bf2f(x[b * s_b + t * s_t + h * s_h + d]) : 0.f;
-    p[r & 3] = p[r & 3] + val;
-    float a = fabsf(val);
-    if (a > m) m = a;
+    float* p = part + (r & 3) * HD;
+    for (int64_t h = 0; h < H; ++h) {
+      const uint16_t* row = t < T ? x + b * s_b + t * s_t + h * s_h : NULL;
+      for (int64_t d = 0; d < D; ++d) {
+        float val = row ? bf2f(row[d]) : 0.f;
+        p[h * D + d] = p[h * D + d] + val;
+        if (amax) {
+          float a = fabsf(val);
+          if (a > amax[h * D + d]) amax[h * D + d] = a;
+        }
+      }
+    }
   }
-  if (amax) *amax = m;
-  return (p[0] + p[1]) + (p[2] + p[3]);
+  for (int64_t e = 0; e < HD; ++e)
+    out_sum[e] = (part[e] + part[HD + e]) + (part[2 * HD + e] + part[3 * HD + e]);
 }
 
 void or_pool(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h, const uint16_t* k,
@@ -116,25 +128,39 @@ void or_pool(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h, const 
              int64_t block, uint16_t* kc, uint16_t* vc, int64_t npad, float* qbar,
              float* vamax_part) {
   int64_t NT = (T + block - 1) / block;
-#pragma omp parallel for collapse(2) schedule(static)
-  for (int64_t b = 0; b < B; ++b)
-    for (int64_t j = 0; j < NT; ++j) {
-      int64_t t0 = j * block;
-      int64_t len = T - t0 < block ? T - t0 : block;
-      float flen = (float)len;
-      for (int64_t h = 0; h < H; ++h)
-        for (int64_t d = 0; d < D; ++d) {
-          float am;
-          float sk = pooled_sum(k, sk_b, sk_t, sk_h, b, t0, T, h, d, block, NULL);
-          float sv = pooled_sum(v, sv_b, sv_t, sv_h, b, t0, T, h, d, block, &am);
-          float sq = pooled_sum(q, sq_b, sq_t, sq_h, b, t0, T, h, d, block, NULL);
-          int64_t o = ((b * npad + j) * H + h) * D + d;
-          kc[o] = f2bf(sk / flen);
-          vc[o] = f2bf(sv);
-          qbar[((b * H + h) * NT + j) * D + d] = sq / flen;
-          if (vamax_part) vamax_part[((b * NT + j) * H + h) * D + d] = am;
-        }
-    }
+  int64_t HD = H * D;
+#pragma omp parallel
+  {
+    float* part = (float*)malloc(sizeof(float) * (size_t)(4 * HD));
+    float* sk = (float*)malloc(sizeof(float) * (size_t)HD);
+    float* sv = (float*)malloc(sizeof(float) * (size_t)HD);
+    float* sq = (float*)malloc(sizeof(float) * (size_t)HD);
+    float* am = (float*)malloc(sizeof(float) * (size_t)HD);
+#pragma omp for collapse(2) schedule(static)
+    for (int64_t b = 0; b < B; ++b)
+      for (int64_t j = 0; j < NT; ++j) {
+        int64_t t0 = j * block;
+        int64_t len = T - t0 < block ? T - t0 : block;
+        float flen = (float)len;
+        pool_one(k, sk_b, sk_t, sk_h, b, t0, T, H, D, block, part, NULL, sk);
+        pool_one(v, sv_b, sv_t, sv_h, b, t0, T, H, D, block, part, am, sv);
+        pool_one(q, sq_b, sq_t, sq_h, b, t0, T, H, D, block, part, NULL, sq);
+        for (int64_t h = 0; h < H; ++h)
+          for (int64_t d = 0; d < D; ++d) {
+            int64_t e = h * D + d;
+            int64_t o = ((b * npad + j) * H + h) * D + d;
+            kc[o] = f2bf(sk[e] / flen);
+            vc[o] = f2bf(sv[e]);
+            qbar[((b * H + h) * NT + j) * D + d] = sq[e] / flen;
+            if (vamax_part) vamax_part[((b * NT + j) * H + h) * D + d] = am[e];
+          }
+      }
+    free(part);
+    free(sk);
+    free(sv);
+    free(sq);
+    free(am);
+  }
 }
 
 /* Sums over blocks use 8 partials (blocks j = g mod 8, ascending) combined
