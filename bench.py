@@ -167,6 +167,38 @@ def _traffic():
         return None
 
 
+def run_kernel_only(args, mods, cfg, q, k, v):
+    """Launch one kernel ``--steps`` times for rocprofv3 (kernel trace or --pmc
+    passes), preceded by a 512 MiB copy whose bytes are known exactly."""
+    block, tau, D = cfg["block"], cfg["tau"], q.shape[-1]
+    src = torch.empty(256 << 20, dtype=torch.int16, device=q.device)
+    dst = torch.empty_like(src)
+    dst.copy_(src)  # calibration: 512 MiB read + 512 MiB written
+    torch.cuda.synchronize()
+    del src, dst
+    if args.kernel_only == "fwd":
+        r = mods["_preprocess"].route(q, k, v, scale=D ** -0.5, tau=tau, block=block)
+        out = torch.empty_like(q)
+        for _ in range(args.steps):
+            mods["_tri_fwd"].forward_bf16(q, k, v, r, out=out)
+    elif args.kernel_only == "fwd_int8":
+        fp = mods["_fused_prep"].fused_preprocess_routing(q, k, v, tau=tau, scale=D ** -0.5,
+                                                          block=block)
+        r, qi, qs, ki, ks, vi = fp
+        out = torch.empty_like(q)
+        for _ in range(args.steps):
+            mods["_int8_fwd"].forward_int8(q, v, r, qi, qs, ki, ks, vi, out=out)
+    elif args.kernel_only == "prep":
+        for _ in range(args.steps):
+            mods["_preprocess"].route(q, k, v, scale=D ** -0.5, tau=tau, block=block)
+    else:
+        perm, _ = mods["_morton"].morton_perm(cfg["grid"], q.device, "3d")
+        for _ in range(args.steps):
+            mods["_morton"].reorder_tokens(q, perm, dim=1)
+    torch.cuda.synchronize()
+    print(f"[bench] kernel-only {args.kernel_only} x{args.steps} done", file=sys.stderr, flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -176,6 +208,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--extra", action="store_true", help="also time INT8 (cfg 3) and cfg 4")
+    ap.add_argument("--kernel-only", choices=["fwd", "fwd_int8", "prep", "reorder"],
+                    help="profiling driver: run only this kernel --steps times (after a "
+                         "512 MiB device copy used to calibrate memory counters); no JSON")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -198,6 +233,10 @@ def main():
         q, k, v = (mods["_morton"].reorder_tokens(t, perm, dim=1) for t in (q, k, v))
         reorder_ms = time_cuda(lambda: mods["_morton"].reorder_tokens(q, perm, dim=1), 10, 2)
     torch.cuda.synchronize()
+
+    if args.kernel_only:
+        run_kernel_only(args, mods, cfg, q, k, v)
+        return
 
     sol_attn = mods["_tri_fwd"].sol_attn
     step = lambda: sol_attn(q, k, v, tau=tau, block=block)

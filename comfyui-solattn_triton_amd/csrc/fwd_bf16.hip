@@ -45,7 +45,9 @@ fwd_bf16_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
   const KVSource src{k + b * sk_b + h * sk_h, sk_t, v + b * sv_b + h * sv_h, sv_t,
                      kc + (static_cast<int64_t>(b) * npad * H + h) * kD,
                      static_cast<int64_t>(H) * kD, vc + (static_cast<int64_t>(b) * npad * H + h) * kD};
-  issue_tile<BLK, NTHREADS>(buf[0], tl, 0, src, T, NT);
+  TileOffsets<NTHREADS> off;
+  off.init(sk_t, sv_t);
+  issue_tile<BLK, NTHREADS>(buf[0], tl, 0, src, off, T, NT);
 
   // This wave's 32 query rows as the B operand of S^T = K Q^T.
   const int qrow = qb * BLK + wave * 32 + col;
@@ -68,7 +70,7 @@ fwd_bf16_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
   for (int n = 0; n < ntiles; ++n) {
     // Tile n+1 streams into the other buffer while tile n is computed; that
     // buffer's last readers finished before the barrier that ended tile n-1.
-    if (n + 1 < ntiles) issue_tile<BLK, NTHREADS>(buf[(n + 1) & 1], tl, n + 1, src, T, NT);
+    if (n + 1 < ntiles) issue_tile<BLK, NTHREADS>(buf[(n + 1) & 1], tl, n + 1, src, off, T, NT);
     const TileDesc td = tile_desc<BLK>(tl, n, T, NT);
     const SwzBuf& tb = buf[n & 1];
 

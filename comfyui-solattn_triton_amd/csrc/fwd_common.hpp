@@ -110,17 +110,20 @@ __device__ __forceinline__ TileDesc tile_desc(const TileList& tl, int n, int T, 
 
 // ------------------------------------------------------------- direct tiles
 // K and V rows (64 keys x 128 bf16 = 16 chunks of 16 bytes) copied global ->
-// LDS without passing through VGPRs. Row-major, chunks XOR-swizzled:
-//   K: physical chunk = chunk ^ (row & 7)      (16-byte MFMA operand reads)
-//   V: physical chunk = chunk ^ 2*(row & 7)    (ds_read_tr16_b64 reads, which
-//      take 32 contiguous bytes = a chunk pair per row)
+// LDS without passing through VGPRs. Rows are 256 bytes, one full sweep of the
+// 64 four-byte LDS banks, so only the chunk position picks the banks; chunks
+// are XOR-swizzled per row:
+//   K: physical chunk = chunk ^ (row & 15): a 16-byte operand read serves 16
+//      lanes = 16 rows of one chunk per cycle, all in different chunks;
+//   V: physical chunk = chunk ^ 4*(row & 3): a ds_read_tr16_b64 serves 32
+//      lanes = 4 rows x 4 consecutive chunks per cycle, all distinct.
 struct SwzBuf {
   uint16_t k[kKeys * kD];
   uint16_t v[kKeys * kD];
 };
 
-__device__ __forceinline__ int swz_k(int row, int chunk) { return chunk ^ (row & 7); }
-__device__ __forceinline__ int swz_v(int row, int chunk) { return chunk ^ ((row & 7) << 1); }
+__device__ __forceinline__ int swz_k(int row, int chunk) { return chunk ^ (row & 15); }
+__device__ __forceinline__ int swz_v(int row, int chunk) { return chunk ^ ((row & 3) << 2); }
 
 __device__ __forceinline__ void g2l16(const void* g, void* lds) {
   __builtin_amdgcn_global_load_lds((glb_void_t*)g, (lds_void_t*)lds, 16, 0, 0);
@@ -128,23 +131,53 @@ __device__ __forceinline__ void g2l16(const void* g, void* lds) {
 
 // Issue the copies of tile n into buf. Each instruction moves 64 lanes x 16 B
 // into 1 KiB of LDS at (wave base + 16 * lane); lane e of the tile fills
-// physical chunk e, so it fetches the logical chunk that lands there. Rows past
-// nvalid re-read row 0 of the tile (finite data, masked out of the softmax).
+// physical chunk e, so it fetches the logical chunk that lands there. Full
+// exact tiles use the per-lane byte offsets precomputed in TileOffsets (tile
+// base in SGPRs + 32-bit lane offset); pooled and ragged tiles compute theirs,
+// with rows past nvalid re-reading row 0 of the tile (finite data that the
+// softmax masks out).
+template <int NTHREADS>
+struct TileOffsets {
+  static constexpr int U = kKeys * 16 / NTHREADS;
+  uint32_t k[U], v[U];
+  __device__ __forceinline__ void init(int64_t sk, int64_t sv) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int e = threadIdx.x + NTHREADS * u;
+      const int row = e >> 4, pc = e & 15;
+      k[u] = static_cast<uint32_t>((row * sk + swz_k(row, pc) * 8) * 2);
+      v[u] = static_cast<uint32_t>((row * sv + swz_v(row, pc) * 8) * 2);
+    }
+  }
+};
+
 template <int BLK, int NTHREADS>
 __device__ __forceinline__ void issue_tile(SwzBuf& buf, const TileList& tl, int n,
-                                           const KVSource& src, int T, int NT) {
+                                           const KVSource& src, const TileOffsets<NTHREADS>& off,
+                                           int T, int NT) {
   const TileDesc td = tile_desc<BLK>(tl, n, T, NT);
+  const int wave_base = threadIdx.x & ~63;
+  if (!td.pooled && td.nvalid == kKeys) {
+    const char* kb = reinterpret_cast<const char*>(src.k + static_cast<int64_t>(td.first) * src.sk);
+    const char* vb = reinterpret_cast<const char*>(src.v + static_cast<int64_t>(td.first) * src.sv);
+#pragma unroll
+    for (int u = 0; u < TileOffsets<NTHREADS>::U; ++u) {
+      const int lds_chunk = wave_base + NTHREADS * u;  // first chunk this wave writes
+      g2l16(kb + off.k[u], &buf.k[lds_chunk * 8]);
+      g2l16(vb + off.v[u], &buf.v[lds_chunk * 8]);
+    }
+    return;
+  }
   const uint16_t* kb = td.pooled ? src.kc : src.k;
   const uint16_t* vb = td.pooled ? src.vc : src.v;
   const int64_t ks = td.pooled ? src.skc : src.sk;
   const int64_t vs = td.pooled ? src.skc : src.sv;
-  const int wave_base = threadIdx.x & ~63;
 #pragma unroll
-  for (int u = 0; u < kKeys * 16 / NTHREADS; ++u) {
+  for (int u = 0; u < TileOffsets<NTHREADS>::U; ++u) {
     const int e = threadIdx.x + NTHREADS * u;
     const int row = e >> 4, pc = e & 15;
     const int srow = td.first + (row < td.nvalid ? row : 0);
-    const int lds_chunk = wave_base + NTHREADS * u;  // first chunk this wave writes
+    const int lds_chunk = wave_base + NTHREADS * u;
     g2l16(kb + static_cast<int64_t>(srow) * ks + swz_k(row, pc) * 8, &buf.k[lds_chunk * 8]);
     g2l16(vb + static_cast<int64_t>(srow) * vs + swz_v(row, pc) * 8, &buf.v[lds_chunk * 8]);
   }
@@ -213,6 +246,8 @@ __device__ __forceinline__ void pv_tr16(const SwzBuf& tb, const f32x16 (&p)[2], 
 }
 
 // ------------------------------------------------------------ online softmax
+constexpr float kMaxSlack = 8.f;
+
 struct SoftmaxState {
   float m;          // running max, in the exp2 domain (score * c)
   float l;          // partial row sum over this lane's keys
@@ -247,7 +282,11 @@ __device__ __forceinline__ void softmax_update(SoftmaxState& st, f32x16 (&s)[2],
 #pragma unroll
     for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[m][r]);
   mx = fmaxf(mx, __shfl_xor(mx, 32));
-  const float m_new = fmaxf(st.m, mx * c);
+  // The running max moves only when the tile's max exceeds it by more than
+  // kMaxSlack (log2 units): p may then reach 2^kMaxSlack, harmless in bf16 P
+  // and fp32 sums, and the O rescale becomes rare.
+  const float m_tile = mx * c;
+  const float m_new = m_tile > st.m + kMaxSlack ? m_tile : st.m;
   const float alpha = st.m == m_new ? 1.f : __builtin_amdgcn_exp2f(st.m - m_new);
   const float neg = -m_new;
   float psum = 0.f;
@@ -454,6 +493,9 @@ inline int check_fwd_args(const void* q, int64_t sq_b, int64_t sq_t, int64_t sq_
                                 block, o, so_b, so_t, so_h, what))
     return rc;
   SOLATTN_REQUIRE(k && v, SOLATTN_EINVAL, "%s: null k/v", what);
+  // Lane offsets within a 64-row tile are kept in 32 bits.
+  SOLATTN_REQUIRE(sk_t >= 0 && sv_t >= 0 && sk_t < (1ll << 24) && sv_t < (1ll << 24),
+                  SOLATTN_EUNSUPPORTED, "%s: token strides beyond 2^24 elements", what);
   SOLATTN_REQUIRE(reinterpret_cast<uintptr_t>(k) % 16 == 0 && sk_b % 8 == 0 && sk_t % 8 == 0 &&
                       sk_h % 8 == 0 && reinterpret_cast<uintptr_t>(v) % 16 == 0 && sv_b % 8 == 0 &&
                       sv_t % 8 == 0 && sv_h % 8 == 0,

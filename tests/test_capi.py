@@ -1,0 +1,92 @@
+"""The C ABI without a GPU: the library loads, exports every symbol that
+include/solattn.h declares with the binding's signatures, rejects bad
+arguments with error codes (no device work is reached), and its host-side
+helpers (Morton, workspace sizing) answer correctly."""
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "solattn.h")
+
+
+def declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(solattn_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def capi(pkg):
+    import importlib
+    return importlib.import_module(f"{pkg.__name__}._capi")
+
+
+def test_exports_every_declared_symbol(capi):
+    names = declared()
+    assert len(names) >= 14
+    for name in names:
+        assert hasattr(capi.LIB, name), name
+    assert set(names) == set(capi.SIGNATURES), "binding and header disagree"
+
+
+def test_abi_version(capi):
+    assert capi.abi_version() >> 16 == 1
+
+
+def test_errors_are_reported(capi):
+    L = capi.LIB
+    null = None
+    # head_dim 64 on the device path: rejected before any launch
+    rc = L.solattn_pool(null, 0, 0, 0, null, 0, 0, 0, null, 0, 0, 0, 1, 100, 1, 64, 64,
+                        null, null, 64, null, null, null)
+    assert rc == -2 and b"head_dim" in L.solattn_last_error()
+    rc = L.solattn_fwd_bf16(*([null, 0, 0, 0] * 3), null, null, 64, null, null, null,
+                            1, 100, 1, 128, 96, 0.1, null, 0, 0, 0, null)
+    assert rc == -2 and b"block" in L.solattn_last_error()
+    rc = L.solattn_route(null, null, 1, null, null, 1, 10, 1, 128, 64, 0.1, 1.0, 0, 0, 0, 0, 0,
+                         null, null, null, null, null)
+    assert rc == -1
+    with pytest.raises(capi.SolAttnError, match="null pointer"):
+        capi.call("solattn_reorder_rows", null, 1, 0, 16, null, 0, 16, 1, 1, 16, null, null)
+    ws = L.solattn_sol_attn_workspace_bytes(1, 1000, 2, 128, 64, 0)
+    rc = L.solattn_sol_attn(*([null, 0, 0, 0] * 3), 1, 1000, 2, 128, 64, 0.1, 1.0, 0, 0, 0, 0,
+                            null, ws - 1, null, 0, 0, 0, null)
+    assert rc == -4 and b"workspace" in L.solattn_last_error()
+
+
+def test_workspace_bytes(capi):
+    L = capi.LIB
+    b0 = L.solattn_sol_attn_workspace_bytes(1, 32760, 24, 128, 128, 0)
+    b1 = L.solattn_sol_attn_workspace_bytes(1, 32760, 24, 128, 128, 1)
+    NT, npad = 256, 256
+    floor = 2 * npad * 24 * 128 * 2 + 24 * NT * NT * 2
+    assert b0 >= floor and b1 > b0 + 3 * 32760 * 24 * 128
+    assert b0 % 256 == 0
+    assert L.solattn_sol_attn_workspace_bytes(0, 10, 1, 128, 64, 0) == 0
+
+
+def test_host_morton(capi):
+    n = 3 * 4 * 5
+    perm = np.empty(n, np.int64)
+    inv = np.empty(n, np.int64)
+    rc = capi.LIB.solattn_morton_perm(3, 4, 5, 0, 0, perm.ctypes.data, inv.ctypes.data)
+    assert rc == 0
+    assert np.array_equal(np.sort(perm), np.arange(n)) and np.array_equal(perm[inv], np.arange(n))
+    assert capi.LIB.solattn_morton_perm(0, 4, 5, 0, 0, perm.ctypes.data, inv.ctypes.data) == -1
+    assert capi.LIB.solattn_morton_perm(3, 4, 5, 7, 0, perm.ctypes.data, inv.ctypes.data) == -1
+
+
+def test_product_does_not_import_oracle():
+    """The package never imports or loads the oracle."""
+    pkg_dir = os.path.join(ROOT, "comfyui-solattn_triton_amd")
+    banned = re.compile(r"^\s*(import\s+oracle|from\s+oracle)|liboracle|oracle\.\w+\(", re.M)
+    for dirpath, _, files in os.walk(pkg_dir):
+        for f in files:
+            if f.endswith((".py", ".hip", ".hpp", ".cpp")):
+                src = open(os.path.join(dirpath, f)).read()
+                assert not banned.search(src), f
