@@ -117,10 +117,7 @@ __device__ __forceinline__ TileDesc tile_desc(const TileList& tl, int n, int T, 
 //      lanes = 16 rows of one chunk per cycle, all in different chunks;
 //   V: physical chunk = chunk ^ 4*(row & 3): a ds_read_tr16_b64 serves 32
 //      lanes = 4 rows x 4 consecutive chunks per cycle, all distinct.
-struct SwzBuf {
-  uint16_t k[kKeys * kD];
-  uint16_t v[kKeys * kD];
-};
+constexpr int kTileElems = kKeys * kD;  // one K or V tile in LDS (16 KiB)
 
 __device__ __forceinline__ int swz_k(int row, int chunk) { return chunk ^ (row & 15); }
 __device__ __forceinline__ int swz_v(int row, int chunk) { return chunk ^ ((row & 3) << 2); }
@@ -151,35 +148,33 @@ struct TileOffsets {
   }
 };
 
+// Copy the K (kv == 0) or V (kv == 1) rows of tile n into an LDS tile.
 template <int BLK, int NTHREADS>
-__device__ __forceinline__ void issue_tile(SwzBuf& buf, const TileList& tl, int n,
+__device__ __forceinline__ void issue_half(uint16_t* dst, int kv, const TileList& tl, int n,
                                            const KVSource& src, const TileOffsets<NTHREADS>& off,
                                            int T, int NT) {
   const TileDesc td = tile_desc<BLK>(tl, n, T, NT);
   const int wave_base = threadIdx.x & ~63;
   if (!td.pooled && td.nvalid == kKeys) {
-    const char* kb = reinterpret_cast<const char*>(src.k + static_cast<int64_t>(td.first) * src.sk);
-    const char* vb = reinterpret_cast<const char*>(src.v + static_cast<int64_t>(td.first) * src.sv);
+    const char* base = kv == 0
+        ? reinterpret_cast<const char*>(src.k + static_cast<int64_t>(td.first) * src.sk)
+        : reinterpret_cast<const char*>(src.v + static_cast<int64_t>(td.first) * src.sv);
 #pragma unroll
     for (int u = 0; u < TileOffsets<NTHREADS>::U; ++u) {
       const int lds_chunk = wave_base + NTHREADS * u;  // first chunk this wave writes
-      g2l16(kb + off.k[u], &buf.k[lds_chunk * 8]);
-      g2l16(vb + off.v[u], &buf.v[lds_chunk * 8]);
+      g2l16(base + (kv == 0 ? off.k[u] : off.v[u]), dst + lds_chunk * 8);
     }
     return;
   }
-  const uint16_t* kb = td.pooled ? src.kc : src.k;
-  const uint16_t* vb = td.pooled ? src.vc : src.v;
-  const int64_t ks = td.pooled ? src.skc : src.sk;
-  const int64_t vs = td.pooled ? src.skc : src.sv;
+  const uint16_t* b = kv == 0 ? (td.pooled ? src.kc : src.k) : (td.pooled ? src.vc : src.v);
+  const int64_t stride = td.pooled ? src.skc : (kv == 0 ? src.sk : src.sv);
 #pragma unroll
   for (int u = 0; u < TileOffsets<NTHREADS>::U; ++u) {
     const int e = threadIdx.x + NTHREADS * u;
     const int row = e >> 4, pc = e & 15;
     const int srow = td.first + (row < td.nvalid ? row : 0);
-    const int lds_chunk = wave_base + NTHREADS * u;
-    g2l16(kb + static_cast<int64_t>(srow) * ks + swz_k(row, pc) * 8, &buf.k[lds_chunk * 8]);
-    g2l16(vb + static_cast<int64_t>(srow) * vs + swz_v(row, pc) * 8, &buf.v[lds_chunk * 8]);
+    const int chunk = kv == 0 ? swz_k(row, pc) : swz_v(row, pc);
+    g2l16(b + static_cast<int64_t>(srow) * stride + chunk * 8, dst + (wave_base + NTHREADS * u) * 8);
   }
 }
 
@@ -187,7 +182,7 @@ __device__ __forceinline__ void wait_tile_copies() { __builtin_amdgcn_s_waitcnt(
 
 // S^T (64 keys x 32 query rows of this wave) = K . Q^T. s[m] covers keys
 // 32m + 8(r/4) + 4*half + (r%4) for accumulator element r, query row `col`.
-__device__ __forceinline__ void qk_swz(const SwzBuf& tb, const bf16x8 (&qreg)[8], int col, int half,
+__device__ __forceinline__ void qk_swz(const uint16_t* kt, const bf16x8 (&qreg)[8], int col, int half,
                                        f32x16 (&s)[2]) {
 #pragma unroll
   for (int m = 0; m < 2; ++m)
@@ -199,7 +194,7 @@ __device__ __forceinline__ void qk_swz(const SwzBuf& tb, const bf16x8 (&qreg)[8]
     for (int m = 0; m < 2; ++m) {
       const int row = 32 * m + col;
       const bf16x8 a =
-          *reinterpret_cast<const bf16x8*>(&tb.k[row * kD + swz_k(row, 2 * cc + half) * 8]);
+          *reinterpret_cast<const bf16x8*>(&kt[row * kD + swz_k(row, 2 * cc + half) * 8]);
       s[m] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qreg[cc], s[m], 0, 0, 0);
     }
   }
@@ -223,7 +218,7 @@ __device__ __forceinline__ bf16x8 to_bf16x8(const f32x16& s, int off) {
 // row-major in LDS; ds_read_tr16_b64 hands lane l the 4 keys
 // 16ks + 4*half + k (k = 0..3) of channel 32dt + (l % 32): within each 16-lane
 // group, lane s supplies row 16ks + 4*half + s/4, channels 4*(s%4) .. +3.
-__device__ __forceinline__ void pv_tr16(const SwzBuf& tb, const f32x16 (&p)[2], int lane,
+__device__ __forceinline__ void pv_tr16(const uint16_t* vt, const f32x16 (&p)[2], int lane,
                                         f32x16 (&acc)[4]) {
   const int g = lane >> 4, sl = lane & 15;
   const int half = g >> 1;
@@ -237,8 +232,8 @@ __device__ __forceinline__ void pv_tr16(const SwzBuf& tb, const f32x16 (&p)[2], 
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
       const int chunk = 4 * dt + cpair;
-      const bf16x4 lo = tr16(&tb.v[row0 * kD + swz_v(row0, chunk) * 8 + sub * 4]);
-      const bf16x4 hi = tr16(&tb.v[row1 * kD + swz_v(row1, chunk) * 8 + sub * 4]);
+      const bf16x4 lo = tr16(&vt[row0 * kD + swz_v(row0, chunk) * 8 + sub * 4]);
+      const bf16x4 hi = tr16(&vt[row1 * kD + swz_v(row1, chunk) * 8 + sub * 4]);
       const bf16x8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
       acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[dt], 0, 0, 0);
     }
@@ -338,120 +333,6 @@ __device__ __forceinline__ void store_output(const SoftmaxState& st, uint16_t* _
       w.y = pack_bf16x2(st.acc[dt][4 * i + 2] * inv, st.acc[dt][4 * i + 3] * inv);
       *reinterpret_cast<uint2*>(orow + 32 * dt + 8 * i + 4 * half) = w;
     }
-}
-
-// ----------------------------------------------------- register-staged tiles
-// (INT8 forward): each thread loads its share into VGPRs, then writes it to LDS
-// with V transposed on the way. K row-major [64][136], V^T [128][68].
-constexpr int kKStride = kD + 8;      // bf16 per K row in LDS (272 B)
-constexpr int kVStride = kKeys + 4;   // bf16 per V^T row in LDS (136 B)
-
-struct TileBuf {
-  uint16_t k[kKeys * kKStride];
-  uint16_t vt[kD * kVStride];
-};
-
-template <int NTHREADS>
-struct TileRegs {
-  static constexpr int KCH = kKeys * kD / 8 / NTHREADS;  // 16-byte K chunks
-  static constexpr int VU = kKeys * kD / 32 / NTHREADS;  // 4-key x 8-channel V units
-  uint4 k[KCH];
-  uint4 v[VU][4];
-};
-
-__device__ __forceinline__ uint4 ld16(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
-
-template <int BLK, int NTHREADS>
-__device__ __forceinline__ void load_tile(TileRegs<NTHREADS>& r, const TileList& tl, int n,
-                                          const KVSource& src, int T, int NT) {
-  const TileDesc td = tile_desc<BLK>(tl, n, T, NT);
-  const uint16_t* kb = td.pooled ? src.kc : src.k;
-  const uint16_t* vb = td.pooled ? src.vc : src.v;
-  const int64_t ks = td.pooled ? src.skc : src.sk;
-  const int64_t vs = td.pooled ? src.skc : src.sv;
-  const uint4 z = make_uint4(0u, 0u, 0u, 0u);
-#pragma unroll
-  for (int u = 0; u < TileRegs<NTHREADS>::KCH; ++u) {
-    const int e = threadIdx.x + NTHREADS * u;
-    const int row = e >> 4, cc = e & 15;
-    r.k[u] = row < td.nvalid ? ld16(kb + static_cast<int64_t>(td.first + row) * ks + cc * 8) : z;
-  }
-#pragma unroll
-  for (int u = 0; u < TileRegs<NTHREADS>::VU; ++u) {
-    const int e = threadIdx.x + NTHREADS * u;
-    const int kq = e & 15, dc = e >> 4;
-#pragma unroll
-    for (int x = 0; x < 4; ++x) {
-      const int row = 4 * kq + x;
-      r.v[u][x] = row < td.nvalid ? ld16(vb + static_cast<int64_t>(td.first + row) * vs + dc * 8) : z;
-    }
-  }
-}
-
-__device__ __forceinline__ uint32_t word_of(const uint4& a, int w) {
-  return w == 0 ? a.x : (w == 1 ? a.y : (w == 2 ? a.z : a.w));
-}
-
-template <int NTHREADS>
-__device__ __forceinline__ void store_tile(const TileRegs<NTHREADS>& r, TileBuf& buf) {
-#pragma unroll
-  for (int u = 0; u < TileRegs<NTHREADS>::KCH; ++u) {
-    const int e = threadIdx.x + NTHREADS * u;
-    const int row = e >> 4, cc = e & 15;
-    *reinterpret_cast<uint4*>(&buf.k[row * kKStride + cc * 8]) = r.k[u];
-  }
-#pragma unroll
-  for (int u = 0; u < TileRegs<NTHREADS>::VU; ++u) {
-    const int e = threadIdx.x + NTHREADS * u;
-    const int kq = e & 15, dc = e >> 4;
-#pragma unroll
-    for (int el = 0; el < 8; ++el) {
-      const uint32_t a0 = word_of(r.v[u][0], el >> 1), a1 = word_of(r.v[u][1], el >> 1);
-      const uint32_t a2 = word_of(r.v[u][2], el >> 1), a3 = word_of(r.v[u][3], el >> 1);
-      uint2 p;
-      if ((el & 1) == 0) {
-        p.x = (a0 & 0xffffu) | (a1 << 16);
-        p.y = (a2 & 0xffffu) | (a3 << 16);
-      } else {
-        p.x = (a0 >> 16) | (a1 & 0xffff0000u);
-        p.y = (a2 >> 16) | (a3 & 0xffff0000u);
-      }
-      *reinterpret_cast<uint2*>(&buf.vt[(dc * 8 + el) * kVStride + 4 * kq]) = p;
-    }
-  }
-}
-
-__device__ __forceinline__ void qk_bf16(const TileBuf& tb, const bf16x8 (&qreg)[8], int col, int half,
-                                        f32x16 (&s)[2]) {
-#pragma unroll
-  for (int m = 0; m < 2; ++m)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) s[m][r] = 0.f;
-#pragma unroll
-  for (int cc = 0; cc < 8; ++cc) {
-#pragma unroll
-    for (int m = 0; m < 2; ++m) {
-      const bf16x8 a =
-          *reinterpret_cast<const bf16x8*>(&tb.k[(32 * m + col) * kKStride + cc * 16 + half * 8]);
-      s[m] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qreg[cc], s[m], 0, 0, 0);
-    }
-  }
-}
-
-__device__ __forceinline__ void pv_bf16(const TileBuf& tb, const f32x16 (&p)[2], int col, int half,
-                                        f32x16 (&acc)[4]) {
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    const bf16x8 b = to_bf16x8(p[ks >> 1], 8 * (ks & 1));
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-      const uint16_t* vrow = &tb.vt[(32 * dt + col) * kVStride + 16 * ks + 4 * half];
-      const bf16x4 lo = *reinterpret_cast<const bf16x4*>(vrow);
-      const bf16x4 hi = *reinterpret_cast<const bf16x4*>(vrow + 8);
-      const bf16x8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-      acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[dt], 0, 0, 0);
-    }
-  }
 }
 
 // ------------------------------------------------------------ argument checks
