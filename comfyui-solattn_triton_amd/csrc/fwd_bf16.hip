@@ -1,135 +1,287 @@
 // BF16 Sol-Attn forward on gfx950 MFMA.
 //
 // One workgroup per (batch, head, query block of BLK rows); each wave owns 32
-// query rows. Work is a list of 64-key tiles in LDS (double buffered):
+// query rows, two workgroups share a CU (two waves per SIMD). Work is a list
+// of 64-key tiles staged in LDS (double buffered):
 //   pooled tiles  64 pooled keys kc_j / values vc_j, masked to the approximate
 //                 blocks of this query block, softmax weight x len_j
 //                 (/root/reference/_tri_fwd.py:288-308);
 //   exact tiles   64 tokens of an exact block (/root/reference/_tri_fwd.py:310-340).
-// All tiles feed one online softmax per query row.
+// All tiles feed one online softmax per query row, which is exact under any
+// tile order (up to fp32 rounding): pooled tiles and the ragged exact tile run
+// first through a plain path; the full exact tiles then run through a
+// software pipeline whose step n
+//   * issues the copies of K(n+2) and V(n+1) (global -> LDS, no VGPR staging),
+//   * computes S(n+1) = K(n+1) Q^T (16 MFMAs) with the softmax VALU of tile n
+//     interleaved between them (row max, running max, exps packed to bf16,
+//     row sums by v_dot2),
+//   * accumulates O += P(n) V(n) (16 MFMAs), V operands read one step ahead.
 //
 // MFMA dataflow (v_mfma_f32_32x32x16_bf16): S^T = K . Q^T puts one query row
-// per lane column, so row max / sum need one cross-lane step (lane ^ 32) and
-// the S accumulator converts in place into the B operand of O^T += V^T . P^T.
-// Tiles are copied global -> LDS directly (no VGPR staging, so two waves fit
-// per SIMD); V stays row-major and ds_read_tr16_b64 delivers it transposed as
-// the MFMA A operand. XOR-swizzled chunks keep the LDS reads conflict free.
+// per lane column, so row max / sum need one cross-lane step (lanes 32 apart,
+// v_permlane32_swap) and the S accumulator converts in place into the B
+// operand of O^T += V^T . P^T. V stays row-major in LDS and ds_read_b64_tr_b16
+// delivers it transposed as the MFMA A operand. XOR-swizzled 16-byte chunks
+// keep the LDS reads conflict free (fwd_common.hpp).
 #include "common.hpp"
 #include "fwd_common.hpp"
 
 namespace solattn {
+namespace bf16fwd {
 
-// Two MFMA steps (d = 32*cc0 .. 32*cc0 + 31) of S^T = K . Q^T into s; the
-// first step starts from a zero accumulator (an inline constant operand).
-template <bool FIRST>
-__device__ __forceinline__ void qk_steps(const uint16_t* kt, const bf16x8 (&qreg)[8], int col,
-                                         int half, f32x16 (&s)[2], int cc0) {
+__device__ __forceinline__ f32x16 mfma(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// x combined with the value of the lane 32 apart (one v_permlane32_swap).
+__device__ __forceinline__ float xhalf_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xhalf_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// K operand of S^T = K . Q^T: key 32m + col, dims 16cc + 8half .. +7.
+__device__ __forceinline__ bf16x8 k_op(const uint16_t* kt, int m, int cc, int col, int half) {
+  const int row = 32 * m + col;
+  return *reinterpret_cast<const bf16x8*>(&kt[row * kD + swz_k(row, 2 * cc + half) * 8]);
+}
+
+// V^T operand of O^T += V^T . P^T for key step ks (16 keys) and channel tile
+// dt: lane l gets channel 32dt + l%32 of keys 16ks + 4*half + 8(e/4) + e%4,
+// matching the key order of the S accumulator (see pv_tr16).
+__device__ __forceinline__ bf16x8 v_op(const uint16_t* vt, int ks, int dt, int lane) {
+  const int g = lane >> 4, sl = lane & 15;
+  const int half = g >> 1;
+  const int sub = sl & 1;
+  const int chunk = 4 * dt + 2 * (g & 1) + ((sl & 3) >> 1);
+  const int row0 = 16 * ks + 4 * half + (sl >> 2);
+  const int row1 = row0 + 8;
+  const bf16x4 lo = tr16(&vt[row0 * kD + swz_v(row0, chunk) * 8 + sub * 4]);
+  const bf16x4 hi = tr16(&vt[row1 * kD + swz_v(row1, chunk) * 8 + sub * 4]);
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+__device__ __forceinline__ void qk_tile(const uint16_t* kt, const bf16x8 (&q)[8], int col, int half,
+                                        f32x16 (&s)[2]) {
   const f32x16 zero = {};
 #pragma unroll
-  for (int cc = cc0; cc < cc0 + 2; ++cc)
-#pragma unroll
-    for (int m = 0; m < 2; ++m) {
-      const int row = 32 * m + col;
-      const bf16x8 a =
-          *reinterpret_cast<const bf16x8*>(&kt[row * kD + swz_k(row, 2 * cc + half) * 8]);
-      s[m] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qreg[cc], (FIRST && cc == cc0) ? zero : s[m],
-                                                     0, 0, 0);
-    }
-}
-
-// Keys outside the tile's mask get -inf. Lane (col, half) holds key
-// 32m + 8i + 4*half + j in element 4i + j of s[m].
-__device__ __forceinline__ void mask_scores(f32x16 (&s)[2], uint64_t amask, int half) {
-#pragma unroll
-  for (int m = 0; m < 2; ++m) {
-    const uint32_t bits = static_cast<uint32_t>(amask >> (32 * m + 4 * half));
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        s[m][4 * i + j] = ((bits >> (8 * i + j)) & 1u) ? s[m][4 * i + j] : -INFINITY;
+  for (int cc = 0; cc < 8; ++cc) {
+    const bf16x8 a0 = k_op(kt, 0, cc, col, half);
+    const bf16x8 a1 = k_op(kt, 1, cc, col, half);
+    s[0] = mfma(a0, q[cc], cc == 0 ? zero : s[0]);
+    s[1] = mfma(a1, q[cc], cc == 0 ? zero : s[1]);
   }
 }
 
-// Row sum of a pooled tile: key j weighs len_j, i.e. BLK except the ragged
-// last block (/root/reference/_tri_fwd.py:302-307).
-template <int BLK>
-__device__ __forceinline__ float pooled_sum(const f32x16 (&p)[2], int first, int half, int NT, int T) {
-  const int kl_last = NT - 1 - first;
-  const float tail = static_cast<float>(T - (NT - 1) * BLK);
-  float sum = 0.f;
+// O^T += V^T . P^T over the tile's 16 (key step, channel tile) operands, each
+// read three operands ahead of its MFMA.
+__device__ __forceinline__ void pv_tile(const uint16_t* vt, const bf16x8 (&pb)[4], int lane,
+                                        f32x16 (&o)[4]) {
+  constexpr int L = 3;
+  bf16x8 va[16];
 #pragma unroll
-  for (int m = 0; m < 2; ++m)
+  for (int i = 0; i < L; ++i) va[i] = v_op(vt, i >> 2, i & 3, lane);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int kl = 32 * m + 8 * (r >> 2) + 4 * half + (r & 3);
-      sum = fmaf(p[m][r], kl == kl_last ? tail : static_cast<float>(BLK), sum);
-    }
-  return sum;
+  for (int i = 0; i < 16; ++i) {
+    if (i + L < 16) va[i + L] = v_op(vt, (i + L) >> 2, (i + L) & 3, lane);
+    o[i & 3] = mfma(va[i], pb[i >> 2], o[i & 3]);
+  }
 }
 
-__device__ __forceinline__ float max16(const f32x16& v, float mx) {
-#pragma unroll
-  for (int r = 0; r < 16; ++r) mx = fmaxf(mx, v[r]);
-  return mx;
+// Running-max update: the max moves only when the tile max exceeds it by more
+// than kMaxSlack (log2 units), so the O rescale is rare.
+__device__ __forceinline__ float new_max(float m_old, float m_tile, float& alpha) {
+  const float m_new = m_tile > m_old + kMaxSlack ? m_tile : m_old;
+  alpha = m_old == m_new ? 1.f : __builtin_amdgcn_exp2f(m_old - m_new);
+  return m_new;
 }
 
-__device__ __forceinline__ float exp16(f32x16& v, float c, float neg) {
-  float sum = 0.f;
+// p = exp2(s*c + neg) for elements [R0, R0 + 8) of s, packed to bf16 into pk;
+// the row sum accumulates the packed values (v_dot2 with ones).
+template <int R0>
+__device__ __forceinline__ float exp8(const f32x16& s, float c, float neg, bf16x8& pk, float sum) {
+  const bf16x2 ones = {static_cast<__bf16>(1.f), static_cast<__bf16>(1.f)};
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    v[r] = __builtin_amdgcn_exp2f(fmaf(v[r], c, neg));
-    sum += v[r];
+  for (int e = 0; e < 8; e += 2) {
+    bf16x2 two;
+    two[0] = static_cast<__bf16>(__builtin_amdgcn_exp2f(fmaf(s[R0 + e], c, neg)));
+    two[1] = static_cast<__bf16>(__builtin_amdgcn_exp2f(fmaf(s[R0 + e + 1], c, neg)));
+    pk[e] = two[0];
+    pk[e + 1] = two[1];
+    sum = __builtin_amdgcn_fdot2_f32_bf16(two, ones, sum, false);
   }
   return sum;
 }
 
-// One pipelined step: the QK MFMAs of tile n+1 (into sn) are interleaved with
-// the softmax of tile n (in sc), then P.V of tile n. On entry K(n+1) and V(n)
-// are in LDS; this step starts the copies of K(n+2) and V(n+1) into the
-// buffers freed by step n-1.
-template <int BLK, int NTHREADS>
-__device__ __forceinline__ void fwd_step(int n, int ntiles, f32x16 (&sc)[2], f32x16 (&sn)[2],
-                                         SoftmaxState& st, uint16_t (*kbuf)[kTileElems],
-                                         uint16_t (*vbuf)[kTileElems], const TileList& tl,
-                                         const KVSource& src, const TileOffsets<NTHREADS>& off,
-                                         const bf16x8 (&qreg)[8], int lane, float c, int T, int NT) {
-  const int col = lane & 31, half = lane >> 5;
-  if (n + 2 < ntiles) issue_half<BLK, NTHREADS>(kbuf[n & 1], 0, tl, n + 2, src, off, T, NT);
-  if (n + 1 < ntiles) issue_half<BLK, NTHREADS>(vbuf[(n + 1) & 1], 1, tl, n + 1, src, off, T, NT);
-  const TileDesc td = tile_desc<BLK>(tl, n, T, NT);
-  const uint16_t* kt = kbuf[(n + 1) & 1];
-
-  if (td.amask != ~0ull) mask_scores(sc, td.amask, half);
-
-  qk_steps<true>(kt, qreg, col, half, sn, 0);
-  float mx = max16(sc[0], -INFINITY);
-  qk_steps<false>(kt, qreg, col, half, sn, 2);
-  mx = max16(sc[1], mx);
-  mx = fmaxf(mx, __shfl_xor(mx, 32));
-  // The running max moves only when the tile's max exceeds it by more than
-  // kMaxSlack (log2 units), so the O rescale is rare.
-  const float m_tile = mx * c;
-  const float m_new = m_tile > st.m + kMaxSlack ? m_tile : st.m;
-  const float alpha = st.m == m_new ? 1.f : __builtin_amdgcn_exp2f(st.m - m_new);
-  const float neg = -m_new;
-  qk_steps<false>(kt, qreg, col, half, sn, 4);
-  float psum = exp16(sc[0], c, neg);
-  qk_steps<false>(kt, qreg, col, half, sn, 6);
-  psum += exp16(sc[1], c, neg);
-  if (td.pooled) psum = pooled_sum<BLK>(sc, td.first, half, NT, T);
-  st.l = fmaf(st.l, alpha, psum);
+__device__ __forceinline__ void rescale(SoftmaxState& st, float alpha) {
   if (__any(alpha != 1.f)) {
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) st.acc[dt][r] *= alpha;
   }
-  st.m = m_new;
+}
 
-  pv_tr16(vbuf[n & 1], sc, lane, st.acc);
-  wait_tile_copies();
-  __syncthreads();
+// Softmax and P.V of one tile whose scores are in s: the plain path (pooled,
+// ragged and last tiles). Masked keys get -inf; pooled keys weigh len_j in the
+// row sum (/root/reference/_tri_fwd.py:302-307); P is rounded to bf16 for the
+// MFMA and, for exact tiles, summed as rounded (as on the pipelined path).
+template <int BLK>
+__device__ __forceinline__ void finish_tile(SoftmaxState& st, f32x16 (&s)[2], const uint16_t* vt,
+                                            const TileDesc& td, float c, int lane, int NT, int T) {
+  const int half = lane >> 5;
+  if (td.amask != ~0ull) {
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const uint32_t bits = static_cast<uint32_t>(td.amask >> (32 * m + 4 * half));
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        s[m][r] = ((bits >> (8 * (r >> 2) + (r & 3))) & 1u) ? s[m][r] : -INFINITY;
+    }
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[m][r]);
+  float alpha;
+  st.m = new_max(st.m, xhalf_max(mx) * c, alpha);
+  const float neg = -st.m;
+  bf16x8 pb[4];
+  float psum = 0.f;
+  if (td.pooled) {
+    const int kl_last = NT - 1 - td.first;
+    const float tail = static_cast<float>(T - (NT - 1) * BLK);
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int kl = 32 * m + 8 * (r >> 2) + 4 * half + (r & 3);
+        const float p = __builtin_amdgcn_exp2f(fmaf(s[m][r], c, neg));
+        pb[2 * m + (r >> 3)][r & 7] = static_cast<__bf16>(p);
+        psum = fmaf(p, kl == kl_last ? tail : static_cast<float>(BLK), psum);
+      }
+  } else {
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      psum = exp8<0>(s[m], c, neg, pb[2 * m], psum);
+      psum = exp8<8>(s[m], c, neg, pb[2 * m + 1], psum);
+    }
+  }
+  st.l = fmaf(st.l, alpha, psum);
+  rescale(st, alpha);
+  pv_tile(vt, pb, lane, st.acc);
+}
+
+// Pipelined step over full exact tile n (scores in sc): S(n+1) from the K tile
+// kn goes to sn, interleaved with the softmax of tile n; then P(n) . V(n).
+__device__ __forceinline__ void fast_step(SoftmaxState& st, f32x16 (&sc)[2], f32x16 (&sn)[2],
+                                          const uint16_t* kn, const uint16_t* vt,
+                                          const bf16x8 (&q)[8], float c, int lane) {
+  const int col = lane & 31, half = lane >> 5;
+  const f32x16 zero = {};
+  bf16x8 pb[4];
+  bf16x8 ka[8][2];
+  float mx = -INFINITY, alpha = 1.f, neg = 0.f, psum = 0.f;
+  ka[0][0] = k_op(kn, 0, 0, col, half);
+  ka[0][1] = k_op(kn, 1, 0, col, half);
+#pragma unroll
+  for (int cc = 0; cc < 8; ++cc) {
+    if (cc + 1 < 8) {
+      ka[cc + 1][0] = k_op(kn, 0, cc + 1, col, half);
+      ka[cc + 1][1] = k_op(kn, 1, cc + 1, col, half);
+    }
+    sn[0] = mfma(ka[cc][0], q[cc], cc == 0 ? zero : sn[0]);
+    sn[1] = mfma(ka[cc][1], q[cc], cc == 0 ? zero : sn[1]);
+    // softmax of tile n, spread over the 8 MFMA pairs
+    if (cc == 0) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[0][r]);
+    } else if (cc == 1) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[1][r]);
+      st.m = new_max(st.m, xhalf_max(mx) * c, alpha);
+      neg = -st.m;
+    } else if (cc == 2) {
+      psum = exp8<0>(sc[0], c, neg, pb[0], psum);
+    } else if (cc == 3) {
+      psum = exp8<8>(sc[0], c, neg, pb[1], psum);
+    } else if (cc == 4) {
+      psum = exp8<0>(sc[1], c, neg, pb[2], psum);
+    } else if (cc == 5) {
+      psum = exp8<8>(sc[1], c, neg, pb[3], psum);
+    }
+  }
+  st.l = fmaf(st.l, alpha, psum);
+  rescale(st, alpha);
+  pv_tile(vt, pb, lane, st.acc);
+}
+
+// Per-lane byte offsets of the 16-byte chunks this lane copies into a K or V
+// tile. Copy u covers rows 16u/P .. : lanes repeat their swizzle every P
+// copies (P = 256 / NTHREADS), so the offset of copy u is
+// off[u % P] + (u / P) * (rows per P copies) * row stride, the second term
+// wave-uniform.
+template <int NTHREADS>
+struct CopyOffsets {
+  static constexpr int U = kKeys * 16 / NTHREADS;  // copies per lane per K or V tile
+  static constexpr int P = 256 / NTHREADS;
+  uint32_t k[P], v[P];
+  __device__ __forceinline__ void init(int64_t sk, int64_t sv) {
+#pragma unroll
+    for (int u = 0; u < P; ++u) {
+      const int e = threadIdx.x + NTHREADS * u;
+      const int row = e >> 4, pc = e & 15;
+      k[u] = static_cast<uint32_t>((row * sk + swz_k(row, pc) * 8) * 2);
+      v[u] = static_cast<uint32_t>((row * sv + swz_v(row, pc) * 8) * 2);
+    }
+  }
+};
+
+// Copies of a full exact tile whose first row is at `base` (row stride `stride`
+// elements), into LDS tile dst.
+template <int NTHREADS>
+__device__ __forceinline__ void issue_full(uint16_t* dst, const uint16_t* base, int64_t stride,
+                                           const uint32_t (&off)[CopyOffsets<NTHREADS>::P]) {
+  using CO = CopyOffsets<NTHREADS>;
+  const int wave_base = static_cast<int>(threadIdx.x) & ~63;
+  const char* b = reinterpret_cast<const char*>(base);
+#pragma unroll
+  for (int u = 0; u < CO::U; ++u) {
+    const char* row_base = b + static_cast<int64_t>(u / CO::P) * 16 * stride * 2;
+    g2l16_s(row_base, off[u % CO::P], dst + (wave_base + NTHREADS * u) * 8);
+  }
+}
+
+// s_waitcnt vmcnt(N): all but the N newest copies have landed (vmcnt is bits
+// [3:0] and [15:14]; expcnt and lgkmcnt stay at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0f70);
+}
+
+// Tile n of this kernel's order: pooled tiles, the ragged exact tile (if any),
+// then the full exact tiles in ascending key order.
+template <int BLK>
+__device__ __forceinline__ TileDesc desc(const TileList& tl, int n, int nrag, int T, int NT) {
+  int std_n;
+  if (n < tl.npool) std_n = n;
+  else if (n < tl.npool + nrag) std_n = tl.npool + tl.nexact - 1;
+  else std_n = n - nrag;
+  return tile_desc<BLK>(tl, std_n, T, NT);
+}
+
+// First token row of full exact tile n (n >= npool + nrag), wave-uniform.
+template <int BLK>
+__device__ __forceinline__ int fast_first(const TileList& tl, int n, int nrag) {
+  constexpr int S = BLK / kKeys;
+  const int e = n - tl.npool - nrag;
+  const int j = tl.blist[e / S];
+  return __builtin_amdgcn_readfirstlane(j * BLK + (e % S) * kKeys);
 }
 
 template <int BLK>
@@ -142,6 +294,7 @@ fwd_bf16_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
                 const uint32_t* __restrict__ mask, int T, int H, int NT, int W, float c,
                 uint16_t* __restrict__ o, int64_t so_b, int64_t so_t, int64_t so_h) {
   constexpr int NTHREADS = BLK * 2;
+  constexpr int kCopiesPerTile = 2 * CopyOffsets<NTHREADS>::U;
   __shared__ __align__(16) uint16_t kbuf[2][kTileElems];
   __shared__ __align__(16) uint16_t vbuf[2][kTileElems];
   __shared__ TileList tl;
@@ -155,15 +308,36 @@ fwd_bf16_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
 
   const int ntiles = build_tile_list<BLK>(tl, counts, lists, mask, row, NT, W, T);
   if (ntiles == 0) return;  // cannot happen for routed lists: the diagonal is exact
+  // The last exact tile is ragged when block NT-1 is exact and T is not a
+  // multiple of 64 (exact blocks are listed in ascending order).
+  const int cnt = min(max(counts[row], 0), NT);
+  const int nrag = (tl.nexact > 0 && tl.blist[cnt - 1] == NT - 1 && (T % kKeys) != 0) ? 1 : 0;
+  const int nplain = tl.npool + nrag;
 
   const KVSource src{k + b * sk_b + h * sk_h, sk_t, v + b * sv_b + h * sv_h, sv_t,
                      kc + (static_cast<int64_t>(b) * npad * H + h) * kD,
                      static_cast<int64_t>(H) * kD, vc + (static_cast<int64_t>(b) * npad * H + h) * kD};
-  TileOffsets<NTHREADS> off;
+  CopyOffsets<NTHREADS> off;
   off.init(sk_t, sv_t);
-  issue_half<BLK, NTHREADS>(kbuf[0], 0, tl, 0, src, off, T, NT);
-  issue_half<BLK, NTHREADS>(vbuf[0], 1, tl, 0, src, off, T, NT);
-  if (ntiles > 1) issue_half<BLK, NTHREADS>(kbuf[1], 0, tl, 1, src, off, T, NT);
+  const auto issue_k = [&](int n, int buf) {
+    const int first = fast_first<BLK>(tl, n, nrag);
+    issue_full<NTHREADS>(kbuf[buf], src.k + static_cast<int64_t>(first) * src.sk, src.sk, off.k);
+  };
+  const auto issue_v = [&](int n, int buf) {
+    const int first = fast_first<BLK>(tl, n, nrag);
+    issue_full<NTHREADS>(vbuf[buf], src.v + static_cast<int64_t>(first) * src.sv, src.sv, off.v);
+  };
+  const auto issue_tile = [&](int n, int buf) {
+    if (n >= nplain) {
+      issue_k(n, buf);
+      issue_v(n, buf);
+    } else {
+      const TileDesc td = desc<BLK>(tl, n, nrag, T, NT);
+      issue_generic<NTHREADS>(kbuf[buf], 0, td, src);
+      issue_generic<NTHREADS>(vbuf[buf], 1, td, src);
+    }
+  };
+  issue_tile(0, 0);
 
   // This wave's 32 query rows as the B operand of S^T = K Q^T.
   const int qrow = qb * BLK + wave * 32 + col;
@@ -180,22 +354,76 @@ fwd_bf16_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
 
   SoftmaxState st;
   st.init();
-  wait_tile_copies();
-  __syncthreads();
-  f32x16 sa[2], sb[2];
-  qk_swz(kbuf[0], qreg, col, half, sa);
-  __syncthreads();  // kbuf[0] is refilled (K of tile 2) by the first step
 
-  // Unrolled by two so the S buffers swap roles without register copies.
-  for (int n = 0; n < ntiles; n += 2) {
-    fwd_step<BLK, NTHREADS>(n, ntiles, sa, sb, st, kbuf, vbuf, tl, src, off, qreg, lane, c, T, NT);
-    if (n + 1 < ntiles)
-      fwd_step<BLK, NTHREADS>(n + 1, ntiles, sb, sa, st, kbuf, vbuf, tl, src, off, qreg, lane, c, T, NT);
+  // ---- plain tiles (pooled, ragged): tile n+1 is copied while tile n computes
+  for (int n = 0; n < nplain; ++n) {
+    if (n + 1 < ntiles) {
+      issue_tile(n + 1, (n + 1) & 1);
+      wait_vmcnt<kCopiesPerTile>();  // tile n landed; tile n+1 stays in flight
+    } else {
+      wait_tile_copies();
+    }
+    __syncthreads();
+    f32x16 s[2];
+    qk_tile(kbuf[n & 1], qreg, col, half, s);
+    finish_tile<BLK>(st, s, vbuf[n & 1], desc<BLK>(tl, n, nrag, T, NT), c, lane, NT, T);
+    __syncthreads();
   }
 
-  store_output(st, o + b * so_b + h * so_h, so_t, qrow, T, half);
+  // ---- full exact tiles, pipelined; tile F is in buffer F & 1 (or in flight)
+  const int F = nplain;
+  if (F < ntiles) {
+    wait_tile_copies();
+    __syncthreads();
+    if (F + 1 < ntiles) issue_k(F + 1, (F + 1) & 1);
+    f32x16 sa[2], sb[2];
+    qk_tile(kbuf[F & 1], qreg, col, half, sa);
+    wait_tile_copies();
+    __syncthreads();  // kbuf[F & 1] is refilled (K of tile F+2) by the first step
+
+    int n = F;
+    // Step n computes S(n+1) and needs n + 1 < ntiles. K(n+2) of the last
+    // step is clamped to the last tile: a redundant copy into a buffer that
+    // nothing reads afterwards, which keeps the loop free of branches.
+    const auto step = [&](f32x16 (&sc)[2], f32x16 (&sn)[2]) {
+      issue_k(min(n + 2, ntiles - 1), n & 1);
+      issue_v(n + 1, (n + 1) & 1);
+      fast_step(st, sc, sn, kbuf[(n + 1) & 1], vbuf[n & 1], qreg, c, lane);
+      wait_tile_copies();
+      __syncthreads();
+      ++n;
+    };
+    // Pairs of steps, so the S buffers swap roles without register copies.
+    while (n + 2 < ntiles) {
+      step(sa, sb);
+      step(sb, sa);
+    }
+    const TileDesc full{0, 0, kKeys, ~0ull};
+    if (n + 1 < ntiles) {
+      step(sa, sb);
+      finish_tile<BLK>(st, sb, vbuf[n & 1], full, c, lane, NT, T);
+    } else {
+      finish_tile<BLK>(st, sa, vbuf[n & 1], full, c, lane, NT, T);
+    }
+  }
+
+  // ---- O / l, rows past T skipped
+  const float inv = 1.f / xhalf_sum(st.l);
+  if (qrow < T) {
+    uint16_t* orow = o + b * so_b + h * so_h + static_cast<int64_t>(qrow) * so_t;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uint2 w;
+        w.x = pack_bf16x2(st.acc[dt][4 * i] * inv, st.acc[dt][4 * i + 1] * inv);
+        w.y = pack_bf16x2(st.acc[dt][4 * i + 2] * inv, st.acc[dt][4 * i + 3] * inv);
+        *reinterpret_cast<uint2*>(orow + 32 * dt + 8 * i + 4 * half) = w;
+      }
+  }
 }
 
+}  // namespace bf16fwd
 }  // namespace solattn
 
 using namespace solattn;
@@ -219,12 +447,12 @@ extern "C" int solattn_fwd_bf16(const uint16_t* q, int64_t sq_b, int64_t sq_t, i
   const uint32_t grid = static_cast<uint32_t>(B * H * NT);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (block == 128) {
-    hipLaunchKernelGGL(fwd_bf16_kernel<128>, dim3(grid), dim3(256), 0, s,
+    hipLaunchKernelGGL(bf16fwd::fwd_bf16_kernel<128>, dim3(grid), dim3(256), 0, s,
                        q, sq_b, sq_t, sq_h, k, sk_b, sk_t, sk_h, v, sv_b, sv_t, sv_h, kc, vc, npad,
                        counts, lists, mask, static_cast<int>(T), static_cast<int>(H),
                        static_cast<int>(NT), W, c, o, so_b, so_t, so_h);
   } else {
-    hipLaunchKernelGGL(fwd_bf16_kernel<64>, dim3(grid), dim3(128), 0, s, q,
+    hipLaunchKernelGGL(bf16fwd::fwd_bf16_kernel<64>, dim3(grid), dim3(128), 0, s, q,
                        sq_b, sq_t, sq_h, k, sk_b, sk_t, sk_h, v, sv_b, sv_t, sv_h, kc, vc, npad,
                        counts, lists, mask, static_cast<int>(T), static_cast<int>(H),
                        static_cast<int>(NT), W, c, o, so_b, so_t, so_h);

@@ -122,8 +122,25 @@ constexpr int kTileElems = kKeys * kD;  // one K or V tile in LDS (16 KiB)
 __device__ __forceinline__ int swz_k(int row, int chunk) { return chunk ^ (row & 15); }
 __device__ __forceinline__ int swz_v(int row, int chunk) { return chunk ^ ((row & 3) << 2); }
 
+// Global -> LDS copies (global_load_lds_*): lane i's bytes land at
+// lds + size * i, lds wave-uniform (M0). They are issued through inline asm so
+// that the compiler does not make later, unrelated LDS reads wait for them;
+// every consumer orders them itself: s_waitcnt vmcnt, then a barrier.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)p)));
+}
+// 16 bytes per lane from a per-lane address.
 __device__ __forceinline__ void g2l16(const void* g, void* lds) {
-  __builtin_amdgcn_global_load_lds((glb_void_t*)g, (lds_void_t*)lds, 16, 0, 0);
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(lds_addr(lds)) : "memory");
+}
+// 16 bytes per lane from a wave-uniform base plus a 32-bit lane offset.
+__device__ __forceinline__ void g2l16_s(const void* base, uint32_t off, void* lds) {
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds_addr(lds)) : "memory");
+}
+// 4 bytes per lane from a per-lane address.
+__device__ __forceinline__ void g2l4(const void* g, void* lds) {
+  asm volatile("global_load_lds_dword %0, off" ::"v"(g), "{m0}"(lds_addr(lds)) : "memory");
 }
 
 // Issue the copies of tile n into buf. Each instruction moves 64 lanes x 16 B
@@ -148,14 +165,32 @@ struct TileOffsets {
   }
 };
 
-// Copy the K (kv == 0) or V (kv == 1) rows of tile n into an LDS tile.
-template <int BLK, int NTHREADS>
-__device__ __forceinline__ void issue_half(uint16_t* dst, int kv, const TileList& tl, int n,
-                                           const KVSource& src, const TileOffsets<NTHREADS>& off,
-                                           int T, int NT) {
-  const TileDesc td = tile_desc<BLK>(tl, n, T, NT);
+// Copy the K (kv == 0) or V (kv == 1) rows of the tile `td` into an LDS tile,
+// each lane computing its own source rows: rows past nvalid re-read row 0 of
+// the tile (finite data that the softmax masks out).
+template <int NTHREADS>
+__device__ __forceinline__ void issue_generic(uint16_t* dst, int kv, const TileDesc& td,
+                                              const KVSource& src) {
+  constexpr int U = kKeys * 16 / NTHREADS;
   const int wave_base = threadIdx.x & ~63;
+  const uint16_t* b = kv == 0 ? (td.pooled ? src.kc : src.k) : (td.pooled ? src.vc : src.v);
+  const int64_t stride = td.pooled ? src.skc : (kv == 0 ? src.sk : src.sv);
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int e = threadIdx.x + NTHREADS * u;
+    const int row = e >> 4, pc = e & 15;
+    const int srow = td.first + (row < td.nvalid ? row : 0);
+    const int chunk = kv == 0 ? swz_k(row, pc) : swz_v(row, pc);
+    g2l16(b + static_cast<int64_t>(srow) * stride + chunk * 8, dst + (wave_base + NTHREADS * u) * 8);
+  }
+}
+
+// As issue_generic, with full exact tiles taking the precomputed lane offsets.
+template <int NTHREADS>
+__device__ __forceinline__ void issue_desc(uint16_t* dst, int kv, const TileDesc& td,
+                                           const KVSource& src, const TileOffsets<NTHREADS>& off) {
   if (!td.pooled && td.nvalid == kKeys) {
+    const int wave_base = threadIdx.x & ~63;
     const char* base = kv == 0
         ? reinterpret_cast<const char*>(src.k + static_cast<int64_t>(td.first) * src.sk)
         : reinterpret_cast<const char*>(src.v + static_cast<int64_t>(td.first) * src.sv);
@@ -166,16 +201,15 @@ __device__ __forceinline__ void issue_half(uint16_t* dst, int kv, const TileList
     }
     return;
   }
-  const uint16_t* b = kv == 0 ? (td.pooled ? src.kc : src.k) : (td.pooled ? src.vc : src.v);
-  const int64_t stride = td.pooled ? src.skc : (kv == 0 ? src.sk : src.sv);
-#pragma unroll
-  for (int u = 0; u < TileOffsets<NTHREADS>::U; ++u) {
-    const int e = threadIdx.x + NTHREADS * u;
-    const int row = e >> 4, pc = e & 15;
-    const int srow = td.first + (row < td.nvalid ? row : 0);
-    const int chunk = kv == 0 ? swz_k(row, pc) : swz_v(row, pc);
-    g2l16(b + static_cast<int64_t>(srow) * stride + chunk * 8, dst + (wave_base + NTHREADS * u) * 8);
-  }
+  issue_generic<NTHREADS>(dst, kv, td, src);
+}
+
+// Copy the K (kv == 0) or V (kv == 1) rows of tile n (pooled tiles first) into an LDS tile.
+template <int BLK, int NTHREADS>
+__device__ __forceinline__ void issue_half(uint16_t* dst, int kv, const TileList& tl, int n,
+                                           const KVSource& src, const TileOffsets<NTHREADS>& off,
+                                           int T, int NT) {
+  issue_desc<NTHREADS>(dst, kv, tile_desc<BLK>(tl, n, T, NT), src, off);
 }
 
 __device__ __forceinline__ void wait_tile_copies() { __builtin_amdgcn_s_waitcnt(0); }

@@ -30,10 +30,6 @@ __device__ __forceinline__ int swz_vi(int row, int chunk) {
   return chunk ^ (2 * (((row >> 1) & 1) | (((row >> 3) & 1) << 1)));
 }
 
-__device__ __forceinline__ void g2l4(const void* g, void* lds) {
-  __builtin_amdgcn_global_load_lds((glb_void_t*)g, (lds_void_t*)lds, 4, 0, 0);
-}
-
 struct I8Source {
   const int8_t* ki;  // rows of this batch/head, stride srow bytes
   const float* ks;   // stride H floats
