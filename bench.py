@@ -285,8 +285,10 @@ def main():
     del r, out
     if args.extra:
         i8 = mods["_int8_fwd"].sol_attn_int8
-        line["int8_ms"] = {str(t): round(time_cuda(lambda: i8(q, k, v, tau=t, block=block), args.steps,
-                                                   args.warmup), 4) for t in (0.8, 0.9, 0.95)}
+        # int8 QK, bf16 P.V; the reference's default int8 P.V beside it
+        for key, pv in (("int8_ms", False), ("int8_pv_ms", True)):
+            line[key] = {str(t): round(time_cuda(lambda: i8(q, k, v, tau=t, block=block, int8_pv=pv),
+                                                 args.steps, args.warmup), 4) for t in (0.8, 0.9, 0.95)}
     if not args.no_cpu:
         print("[bench] CPU baseline", file=sys.stderr, flush=True)
         line["cpu_baseline"] = cpu_baseline(cfg, q, k, v, args.cpu_budget)

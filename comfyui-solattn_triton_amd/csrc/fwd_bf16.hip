@@ -29,153 +29,6 @@
 namespace solattn {
 namespace bf16fwd {
 
-__device__ __forceinline__ f32x16 mfma(const bf16x8& a, const bf16x8& b, const f32x16& c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-}
-
-// x combined with the value of the lane 32 apart (one v_permlane32_swap).
-__device__ __forceinline__ float xhalf_max(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float xhalf_sum(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
-// K operand of S^T = K . Q^T: key 32m + col, dims 16cc + 8half .. +7.
-__device__ __forceinline__ bf16x8 k_op(const uint16_t* kt, int m, int cc, int col, int half) {
-  const int row = 32 * m + col;
-  return *reinterpret_cast<const bf16x8*>(&kt[row * kD + swz_k(row, 2 * cc + half) * 8]);
-}
-
-// V^T operand of O^T += V^T . P^T for key step ks (16 keys) and channel tile
-// dt: lane l gets channel 32dt + l%32 of keys 16ks + 4*half + 8(e/4) + e%4,
-// matching the key order of the S accumulator (see pv_tr16).
-__device__ __forceinline__ bf16x8 v_op(const uint16_t* vt, int ks, int dt, int lane) {
-  const int g = lane >> 4, sl = lane & 15;
-  const int half = g >> 1;
-  const int sub = sl & 1;
-  const int chunk = 4 * dt + 2 * (g & 1) + ((sl & 3) >> 1);
-  const int row0 = 16 * ks + 4 * half + (sl >> 2);
-  const int row1 = row0 + 8;
-  const bf16x4 lo = tr16(&vt[row0 * kD + swz_v(row0, chunk) * 8 + sub * 4]);
-  const bf16x4 hi = tr16(&vt[row1 * kD + swz_v(row1, chunk) * 8 + sub * 4]);
-  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-}
-
-__device__ __forceinline__ void qk_tile(const uint16_t* kt, const bf16x8 (&q)[8], int col, int half,
-                                        f32x16 (&s)[2]) {
-  const f32x16 zero = {};
-#pragma unroll
-  for (int cc = 0; cc < 8; ++cc) {
-    const bf16x8 a0 = k_op(kt, 0, cc, col, half);
-    const bf16x8 a1 = k_op(kt, 1, cc, col, half);
-    s[0] = mfma(a0, q[cc], cc == 0 ? zero : s[0]);
-    s[1] = mfma(a1, q[cc], cc == 0 ? zero : s[1]);
-  }
-}
-
-// O^T += V^T . P^T over the tile's 16 (key step, channel tile) operands, each
-// read three operands ahead of its MFMA.
-__device__ __forceinline__ void pv_tile(const uint16_t* vt, const bf16x8 (&pb)[4], int lane,
-                                        f32x16 (&o)[4]) {
-  constexpr int L = 3;
-  bf16x8 va[16];
-#pragma unroll
-  for (int i = 0; i < L; ++i) va[i] = v_op(vt, i >> 2, i & 3, lane);
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    if (i + L < 16) va[i + L] = v_op(vt, (i + L) >> 2, (i + L) & 3, lane);
-    o[i & 3] = mfma(va[i], pb[i >> 2], o[i & 3]);
-  }
-}
-
-// Running-max update: the max moves only when the tile max exceeds it by more
-// than kMaxSlack (log2 units), so the O rescale is rare.
-__device__ __forceinline__ float new_max(float m_old, float m_tile, float& alpha) {
-  const float m_new = m_tile > m_old + kMaxSlack ? m_tile : m_old;
-  alpha = m_old == m_new ? 1.f : __builtin_amdgcn_exp2f(m_old - m_new);
-  return m_new;
-}
-
-// p = exp2(s*c + neg) for elements [R0, R0 + 8) of s, packed to bf16 into pk;
-// the row sum accumulates the packed values (v_dot2 with ones).
-template <int R0>
-__device__ __forceinline__ float exp8(const f32x16& s, float c, float neg, bf16x8& pk, float sum) {
-  const bf16x2 ones = {static_cast<__bf16>(1.f), static_cast<__bf16>(1.f)};
-#pragma unroll
-  for (int e = 0; e < 8; e += 2) {
-    bf16x2 two;
-    two[0] = static_cast<__bf16>(__builtin_amdgcn_exp2f(fmaf(s[R0 + e], c, neg)));
-    two[1] = static_cast<__bf16>(__builtin_amdgcn_exp2f(fmaf(s[R0 + e + 1], c, neg)));
-    pk[e] = two[0];
-    pk[e + 1] = two[1];
-    sum = __builtin_amdgcn_fdot2_f32_bf16(two, ones, sum, false);
-  }
-  return sum;
-}
-
-__device__ __forceinline__ void rescale(SoftmaxState& st, float alpha) {
-  if (__any(alpha != 1.f)) {
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) st.acc[dt][r] *= alpha;
-  }
-}
-
-// Softmax and P.V of one tile whose scores are in s: the plain path (pooled,
-// ragged and last tiles). Masked keys get -inf; pooled keys weigh len_j in the
-// row sum (/root/reference/_tri_fwd.py:302-307); P is rounded to bf16 for the
-// MFMA and, for exact tiles, summed as rounded (as on the pipelined path).
-template <int BLK>
-__device__ __forceinline__ void finish_tile(SoftmaxState& st, f32x16 (&s)[2], const uint16_t* vt,
-                                            const TileDesc& td, float c, int lane, int NT, int T) {
-  const int half = lane >> 5;
-  if (td.amask != ~0ull) {
-#pragma unroll
-    for (int m = 0; m < 2; ++m) {
-      const uint32_t bits = static_cast<uint32_t>(td.amask >> (32 * m + 4 * half));
-#pragma unroll
-      for (int r = 0; r < 16; ++r)
-        s[m][r] = ((bits >> (8 * (r >> 2) + (r & 3))) & 1u) ? s[m][r] : -INFINITY;
-    }
-  }
-  float mx = -INFINITY;
-#pragma unroll
-  for (int m = 0; m < 2; ++m)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[m][r]);
-  float alpha;
-  st.m = new_max(st.m, xhalf_max(mx) * c, alpha);
-  const float neg = -st.m;
-  bf16x8 pb[4];
-  float psum = 0.f;
-  if (td.pooled) {
-    const int kl_last = NT - 1 - td.first;
-    const float tail = static_cast<float>(T - (NT - 1) * BLK);
-#pragma unroll
-    for (int m = 0; m < 2; ++m)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int kl = 32 * m + 8 * (r >> 2) + 4 * half + (r & 3);
-        const float p = __builtin_amdgcn_exp2f(fmaf(s[m][r], c, neg));
-        pb[2 * m + (r >> 3)][r & 7] = static_cast<__bf16>(p);
-        psum = fmaf(p, kl == kl_last ? tail : static_cast<float>(BLK), psum);
-      }
-  } else {
-#pragma unroll
-    for (int m = 0; m < 2; ++m) {
-      psum = exp8<0>(s[m], c, neg, pb[2 * m], psum);
-      psum = exp8<8>(s[m], c, neg, pb[2 * m + 1], psum);
-    }
-  }
-  st.l = fmaf(st.l, alpha, psum);
-  rescale(st, alpha);
-  pv_tile(vt, pb, lane, st.acc);
-}
-
 // Pipelined step over full exact tile n (scores in sc): S(n+1) from the K tile
 // kn goes to sn, interleaved with the softmax of tile n; then P(n) . V(n).
 __device__ __forceinline__ void fast_step(SoftmaxState& st, f32x16 (&sc)[2], f32x16 (&sn)[2],
@@ -194,8 +47,8 @@ __device__ __forceinline__ void fast_step(SoftmaxState& st, f32x16 (&sc)[2], f32
       ka[cc + 1][0] = k_op(kn, 0, cc + 1, col, half);
       ka[cc + 1][1] = k_op(kn, 1, cc + 1, col, half);
     }
-    sn[0] = mfma(ka[cc][0], q[cc], cc == 0 ? zero : sn[0]);
-    sn[1] = mfma(ka[cc][1], q[cc], cc == 0 ? zero : sn[1]);
+    sn[0] = mfma_bf16(ka[cc][0], q[cc], cc == 0 ? zero : sn[0]);
+    sn[1] = mfma_bf16(ka[cc][1], q[cc], cc == 0 ? zero : sn[1]);
     // softmax of tile n, spread over the 8 MFMA pairs
     if (cc == 0) {
 #pragma unroll
@@ -220,68 +73,13 @@ __device__ __forceinline__ void fast_step(SoftmaxState& st, f32x16 (&sc)[2], f32
   pv_tile(vt, pb, lane, st.acc);
 }
 
-// Per-lane byte offsets of the 16-byte chunks this lane copies into a K or V
-// tile. Copy u covers rows 16u/P .. : lanes repeat their swizzle every P
-// copies (P = 256 / NTHREADS), so the offset of copy u is
-// off[u % P] + (u / P) * (rows per P copies) * row stride, the second term
-// wave-uniform.
-template <int NTHREADS>
-struct CopyOffsets {
-  static constexpr int U = kKeys * 16 / NTHREADS;  // copies per lane per K or V tile
-  static constexpr int P = 256 / NTHREADS;
-  uint32_t k[P], v[P];
-  __device__ __forceinline__ void init(int64_t sk, int64_t sv) {
-#pragma unroll
-    for (int u = 0; u < P; ++u) {
-      const int e = threadIdx.x + NTHREADS * u;
-      const int row = e >> 4, pc = e & 15;
-      k[u] = static_cast<uint32_t>((row * sk + swz_k(row, pc) * 8) * 2);
-      v[u] = static_cast<uint32_t>((row * sv + swz_v(row, pc) * 8) * 2);
-    }
-  }
-};
-
-// Copies of a full exact tile whose first row is at `base` (row stride `stride`
-// elements), into LDS tile dst.
-template <int NTHREADS>
-__device__ __forceinline__ void issue_full(uint16_t* dst, const uint16_t* base, int64_t stride,
-                                           const uint32_t (&off)[CopyOffsets<NTHREADS>::P]) {
-  using CO = CopyOffsets<NTHREADS>;
-  const int wave_base = static_cast<int>(threadIdx.x) & ~63;
-  const char* b = reinterpret_cast<const char*>(base);
-#pragma unroll
-  for (int u = 0; u < CO::U; ++u) {
-    const char* row_base = b + static_cast<int64_t>(u / CO::P) * 16 * stride * 2;
-    g2l16_s(row_base, off[u % CO::P], dst + (wave_base + NTHREADS * u) * 8);
-  }
-}
-
-// s_waitcnt vmcnt(N): all but the N newest copies have landed (vmcnt is bits
-// [3:0] and [15:14]; expcnt and lgkmcnt stay at their maxima).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0f70);
-}
-
-// Tile n of this kernel's order: pooled tiles, the ragged exact tile (if any),
-// then the full exact tiles in ascending key order.
+// Tile n of this kernel's order: pooled tiles, the ragged exact tile (if
+// any), then the full exact tiles in ascending key order.
 template <int BLK>
 __device__ __forceinline__ TileDesc desc(const TileList& tl, int n, int nrag, int T, int NT) {
-  int std_n;
-  if (n < tl.npool) std_n = n;
-  else if (n < tl.npool + nrag) std_n = tl.npool + tl.nexact - 1;
-  else std_n = n - nrag;
-  return tile_desc<BLK>(tl, std_n, T, NT);
-}
-
-// First token row of full exact tile n (n >= npool + nrag), wave-uniform.
-template <int BLK>
-__device__ __forceinline__ int fast_first(const TileList& tl, int n, int nrag) {
-  constexpr int S = BLK / kKeys;
-  const int e = n - tl.npool - nrag;
-  const int j = tl.blist[e / S];
-  return __builtin_amdgcn_readfirstlane(j * BLK + (e % S) * kKeys);
+  if (n < tl.npool) return pooled_desc(tl, n, NT);
+  if (n < tl.npool + nrag) return exact_desc<BLK>(tl, tl.nexact - 1, T, NT);
+  return exact_desc<BLK>(tl, n - tl.npool - nrag, T, NT);
 }
 
 template <int BLK>
@@ -310,8 +108,7 @@ fwd_bf16_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
   if (ntiles == 0) return;  // cannot happen for routed lists: the diagonal is exact
   // The last exact tile is ragged when block NT-1 is exact and T is not a
   // multiple of 64 (exact blocks are listed in ascending order).
-  const int cnt = min(max(counts[row], 0), NT);
-  const int nrag = (tl.nexact > 0 && tl.blist[cnt - 1] == NT - 1 && (T % kKeys) != 0) ? 1 : 0;
+  const int nrag = ragged_tiles(tl, counts, row, NT, T);
   const int nplain = tl.npool + nrag;
 
   const KVSource src{k + b * sk_b + h * sk_h, sk_t, v + b * sv_b + h * sv_h, sv_t,
@@ -320,11 +117,11 @@ fwd_bf16_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
   CopyOffsets<NTHREADS> off;
   off.init(sk_t, sv_t);
   const auto issue_k = [&](int n, int buf) {
-    const int first = fast_first<BLK>(tl, n, nrag);
+    const int first = exact_first<BLK>(tl, n - nplain);
     issue_full<NTHREADS>(kbuf[buf], src.k + static_cast<int64_t>(first) * src.sk, src.sk, off.k);
   };
   const auto issue_v = [&](int n, int buf) {
-    const int first = fast_first<BLK>(tl, n, nrag);
+    const int first = exact_first<BLK>(tl, n - nplain);
     issue_full<NTHREADS>(vbuf[buf], src.v + static_cast<int64_t>(first) * src.sv, src.sv, off.v);
   };
   const auto issue_tile = [&](int n, int buf) {
@@ -407,20 +204,7 @@ fwd_bf16_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
     }
   }
 
-  // ---- O / l, rows past T skipped
-  const float inv = 1.f / xhalf_sum(st.l);
-  if (qrow < T) {
-    uint16_t* orow = o + b * so_b + h * so_h + static_cast<int64_t>(qrow) * so_t;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        uint2 w;
-        w.x = pack_bf16x2(st.acc[dt][4 * i] * inv, st.acc[dt][4 * i + 1] * inv);
-        w.y = pack_bf16x2(st.acc[dt][4 * i + 2] * inv, st.acc[dt][4 * i + 3] * inv);
-        *reinterpret_cast<uint2*>(orow + 32 * dt + 8 * i + 4 * half) = w;
-      }
-  }
+  store_rows(st, o + b * so_b + h * so_h, so_t, qrow, T, half);
 }
 
 }  // namespace bf16fwd

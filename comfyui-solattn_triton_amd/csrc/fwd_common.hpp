@@ -1,10 +1,16 @@
 // Building blocks shared by the BF16 and INT8 Sol-Attn forwards on gfx950.
 //
-// A workgroup serves one query block (BLK rows, BLK/32 waves of 32 rows).
-// Its work is a sequence of 64-key tiles: pooled tiles (chunks of 64 pooled
-// keys with at least one approximate block) and exact tiles (64 tokens each,
-// BLK/64 per exact block, ascending block order). Tiles are staged in LDS,
-// double buffered.
+// A workgroup serves one query block (BLK rows, BLK/32 waves of 32 rows, two
+// workgroups per CU). Its work is a sequence of 64-key tiles: pooled tiles
+// (chunks of 64 pooled keys with at least one approximate block) and exact
+// tiles (64 tokens each, BLK/64 per exact block, ascending block order).
+// Tiles are copied global -> LDS (double buffered) and consumed by MFMA:
+//   S^T = K . Q^T (v_mfma_f32_32x32x16_bf16): lane l holds query row l%32 and
+//     keys 32m + 8(r/4) + 4(l/32) + r%4 in element r of tile m, so row max and
+//     sum need one exchange between lanes 32 apart;
+//   O^T += V^T . P^T: the S accumulator converts in place into the B operand;
+//     V stays row-major in LDS and ds_read_b64_tr_b16 delivers V^T with the
+//     matching key order.
 #pragma once
 
 #include "common.hpp"
@@ -15,9 +21,7 @@ constexpr int kKeys = 64;             // keys per tile
 constexpr int kD = 128;               // head dim
 constexpr int kMaxNT = 2048;          // query/key blocks per head
 constexpr int kMaxPool = kMaxNT / 64; // pooled tiles per query block
-
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((address_space(1))) void glb_void_t;
+constexpr float kMaxSlack = 8.f;      // lazy running max (log2 units)
 
 // ----------------------------------------------------------------- tile list
 struct TileList {
@@ -87,35 +91,52 @@ __device__ int build_tile_list(TileList& tl, const int32_t* __restrict__ counts,
   return tl.npool + tl.nexact;
 }
 
-// Tile n: pooled tiles first (n < npool), then exact tiles.
-template <int BLK>
-__device__ __forceinline__ TileDesc tile_desc(const TileList& tl, int n, int T, int NT) {
+// The last exact tile is ragged when block NT-1 is exact and T is not a
+// multiple of 64 (exact blocks are listed in ascending order).
+__device__ __forceinline__ int ragged_tiles(const TileList& tl, const int32_t* __restrict__ counts,
+                                            int64_t row, int NT, int T) {
+  const int cnt = min(max(counts[row], 0), NT);
+  return (tl.nexact > 0 && tl.blist[cnt - 1] == NT - 1 && (T % kKeys) != 0) ? 1 : 0;
+}
+
+// Pooled tile p.
+__device__ __forceinline__ TileDesc pooled_desc(const TileList& tl, int p, int NT) {
   TileDesc td;
-  if (n < tl.npool) {
-    td.pooled = 1;
-    td.first = tl.pchunk[n] * kKeys;
-    td.nvalid = min(kKeys, NT - td.first);
-    td.amask = tl.pmask[n];
-  } else {
-    constexpr int S = BLK / kKeys;
-    const int e = n - tl.npool;
-    const int j = min(max(static_cast<int>(tl.blist[e / S]), 0), NT - 1);
-    td.pooled = 0;
-    td.first = j * BLK + (e % S) * kKeys;
-    td.nvalid = max(0, min(kKeys, T - td.first));
-    td.amask = td.nvalid >= kKeys ? ~0ull : ((1ull << td.nvalid) - 1ull);
-  }
+  td.pooled = 1;
+  td.first = tl.pchunk[p] * kKeys;
+  td.nvalid = min(kKeys, NT - td.first);
+  td.amask = tl.pmask[p];
   return td;
 }
 
-// ------------------------------------------------------------- direct tiles
-// K and V rows (64 keys x 128 bf16 = 16 chunks of 16 bytes) copied global ->
-// LDS without passing through VGPRs. Rows are 256 bytes, one full sweep of the
-// 64 four-byte LDS banks, so only the chunk position picks the banks; chunks
-// are XOR-swizzled per row:
+// Exact tile e (list order).
+template <int BLK>
+__device__ __forceinline__ TileDesc exact_desc(const TileList& tl, int e, int T, int NT) {
+  constexpr int S = BLK / kKeys;
+  const int j = min(max(static_cast<int>(tl.blist[e / S]), 0), NT - 1);
+  TileDesc td;
+  td.pooled = 0;
+  td.first = j * BLK + (e % S) * kKeys;
+  td.nvalid = max(0, min(kKeys, T - td.first));
+  td.amask = td.nvalid >= kKeys ? ~0ull : ((1ull << td.nvalid) - 1ull);
+  return td;
+}
+
+// First token row of full exact tile e (list order), wave-uniform.
+template <int BLK>
+__device__ __forceinline__ int exact_first(const TileList& tl, int e) {
+  constexpr int S = BLK / kKeys;
+  const int j = tl.blist[e / S];
+  return __builtin_amdgcn_readfirstlane(j * BLK + (e % S) * kKeys);
+}
+
+// ------------------------------------------------------------- LDS copies
+// K and V rows (64 keys x 128 bf16 = 16 chunks of 16 bytes) land in LDS rows
+// of 256 bytes, one full sweep of the 64 four-byte banks, so only the chunk
+// position picks the banks; chunks are XOR-swizzled per row:
 //   K: physical chunk = chunk ^ (row & 15): a 16-byte operand read serves 16
 //      lanes = 16 rows of one chunk per cycle, all in different chunks;
-//   V: physical chunk = chunk ^ 4*(row & 3): a ds_read_tr16_b64 serves 32
+//   V: physical chunk = chunk ^ 4*(row & 3): a ds_read_b64_tr_b16 serves 32
 //      lanes = 4 rows x 4 consecutive chunks per cycle, all distinct.
 constexpr int kTileElems = kKeys * kD;  // one K or V tile in LDS (16 KiB)
 
@@ -142,32 +163,24 @@ __device__ __forceinline__ void g2l16_s(const void* base, uint32_t off, void* ld
 __device__ __forceinline__ void g2l4(const void* g, void* lds) {
   asm volatile("global_load_lds_dword %0, off" ::"v"(g), "{m0}"(lds_addr(lds)) : "memory");
 }
+// 4 bytes per lane from a wave-uniform base plus a 32-bit lane offset.
+__device__ __forceinline__ void g2l4_s(const void* base, uint32_t off, void* lds) {
+  asm volatile("global_load_lds_dword %0, %1" ::"v"(off), "s"(base), "{m0}"(lds_addr(lds)) : "memory");
+}
 
-// Issue the copies of tile n into buf. Each instruction moves 64 lanes x 16 B
-// into 1 KiB of LDS at (wave base + 16 * lane); lane e of the tile fills
-// physical chunk e, so it fetches the logical chunk that lands there. Full
-// exact tiles use the per-lane byte offsets precomputed in TileOffsets (tile
-// base in SGPRs + 32-bit lane offset); pooled and ragged tiles compute theirs,
-// with rows past nvalid re-reading row 0 of the tile (finite data that the
-// softmax masks out).
-template <int NTHREADS>
-struct TileOffsets {
-  static constexpr int U = kKeys * 16 / NTHREADS;
-  uint32_t k[U], v[U];
-  __device__ __forceinline__ void init(int64_t sk, int64_t sv) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int e = threadIdx.x + NTHREADS * u;
-      const int row = e >> 4, pc = e & 15;
-      k[u] = static_cast<uint32_t>((row * sk + swz_k(row, pc) * 8) * 2);
-      v[u] = static_cast<uint32_t>((row * sv + swz_v(row, pc) * 8) * 2);
-    }
-  }
-};
+__device__ __forceinline__ void wait_tile_copies() { __builtin_amdgcn_s_waitcnt(0); }
 
-// Copy the K (kv == 0) or V (kv == 1) rows of the tile `td` into an LDS tile,
-// each lane computing its own source rows: rows past nvalid re-read row 0 of
-// the tile (finite data that the softmax masks out).
+// s_waitcnt vmcnt(N): all but the N newest copies have landed (vmcnt is bits
+// [3:0] and [15:14]; expcnt and lgkmcnt stay at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0f70);
+}
+
+// Copy the K (kv == 0) or V (kv == 1) rows of the bf16 tile `td` into an LDS
+// tile, each lane computing its own source rows: rows past nvalid re-read row
+// 0 of the tile (finite data that the softmax masks out). U copies per lane.
 template <int NTHREADS>
 __device__ __forceinline__ void issue_generic(uint16_t* dst, int kv, const TileDesc& td,
                                               const KVSource& src) {
@@ -185,53 +198,44 @@ __device__ __forceinline__ void issue_generic(uint16_t* dst, int kv, const TileD
   }
 }
 
-// As issue_generic, with full exact tiles taking the precomputed lane offsets.
+// Per-lane byte offsets of the 16-byte chunks this lane copies into a full
+// bf16 K or V tile. Copy u covers rows (NTHREADS/16)u ..; lanes repeat their
+// swizzle every P copies (P = 256 / NTHREADS), so the offset of copy u is
+// off[u % P] + (u / P) * 16 * row stride, the second term wave-uniform.
 template <int NTHREADS>
-__device__ __forceinline__ void issue_desc(uint16_t* dst, int kv, const TileDesc& td,
-                                           const KVSource& src, const TileOffsets<NTHREADS>& off) {
-  if (!td.pooled && td.nvalid == kKeys) {
-    const int wave_base = threadIdx.x & ~63;
-    const char* base = kv == 0
-        ? reinterpret_cast<const char*>(src.k + static_cast<int64_t>(td.first) * src.sk)
-        : reinterpret_cast<const char*>(src.v + static_cast<int64_t>(td.first) * src.sv);
+struct CopyOffsets {
+  static constexpr int U = kKeys * 16 / NTHREADS;  // copies per lane per K or V tile
+  static constexpr int P = 256 / NTHREADS;
+  uint32_t k[P], v[P];
+  __device__ __forceinline__ void init(int64_t sk, int64_t sv) {
 #pragma unroll
-    for (int u = 0; u < TileOffsets<NTHREADS>::U; ++u) {
-      const int lds_chunk = wave_base + NTHREADS * u;  // first chunk this wave writes
-      g2l16(base + (kv == 0 ? off.k[u] : off.v[u]), dst + lds_chunk * 8);
-    }
-    return;
-  }
-  issue_generic<NTHREADS>(dst, kv, td, src);
-}
-
-// Copy the K (kv == 0) or V (kv == 1) rows of tile n (pooled tiles first) into an LDS tile.
-template <int BLK, int NTHREADS>
-__device__ __forceinline__ void issue_half(uint16_t* dst, int kv, const TileList& tl, int n,
-                                           const KVSource& src, const TileOffsets<NTHREADS>& off,
-                                           int T, int NT) {
-  issue_desc<NTHREADS>(dst, kv, tile_desc<BLK>(tl, n, T, NT), src, off);
-}
-
-__device__ __forceinline__ void wait_tile_copies() { __builtin_amdgcn_s_waitcnt(0); }
-
-// S^T (64 keys x 32 query rows of this wave) = K . Q^T. s[m] covers keys
-// 32m + 8(r/4) + 4*half + (r%4) for accumulator element r, query row `col`.
-__device__ __forceinline__ void qk_swz(const uint16_t* kt, const bf16x8 (&qreg)[8], int col, int half,
-                                       f32x16 (&s)[2]) {
-#pragma unroll
-  for (int m = 0; m < 2; ++m)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) s[m][r] = 0.f;
-#pragma unroll
-  for (int cc = 0; cc < 8; ++cc) {
-#pragma unroll
-    for (int m = 0; m < 2; ++m) {
-      const int row = 32 * m + col;
-      const bf16x8 a =
-          *reinterpret_cast<const bf16x8*>(&kt[row * kD + swz_k(row, 2 * cc + half) * 8]);
-      s[m] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qreg[cc], s[m], 0, 0, 0);
+    for (int u = 0; u < P; ++u) {
+      const int e = threadIdx.x + NTHREADS * u;
+      const int row = e >> 4, pc = e & 15;
+      k[u] = static_cast<uint32_t>((row * sk + swz_k(row, pc) * 8) * 2);
+      v[u] = static_cast<uint32_t>((row * sv + swz_v(row, pc) * 8) * 2);
     }
   }
+};
+
+// Copies of a full bf16 tile whose first row is at `base` (row stride
+// `stride` elements) into LDS tile dst.
+template <int NTHREADS>
+__device__ __forceinline__ void issue_full(uint16_t* dst, const uint16_t* base, int64_t stride,
+                                           const uint32_t (&off)[CopyOffsets<NTHREADS>::P]) {
+  using CO = CopyOffsets<NTHREADS>;
+  const int wave_base = static_cast<int>(threadIdx.x) & ~63;
+  const char* b = reinterpret_cast<const char*>(base);
+#pragma unroll
+  for (int u = 0; u < CO::U; ++u) {
+    const char* row_base = b + static_cast<int64_t>(u / CO::P) * 16 * stride * 2;
+    g2l16_s(row_base, off[u % CO::P], dst + (wave_base + NTHREADS * u) * 8);
+  }
+}
+
+// ------------------------------------------------------------ bf16 MFMA tiles
+__device__ __forceinline__ f32x16 mfma_bf16(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
 __device__ __forceinline__ bf16x4 tr16(const uint16_t* p) {
@@ -241,42 +245,57 @@ __device__ __forceinline__ bf16x4 tr16(const uint16_t* p) {
   return __builtin_bit_cast(bf16x4, r);
 }
 
-__device__ __forceinline__ bf16x8 to_bf16x8(const f32x16& s, int off) {
-  bf16x8 b;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) b[e] = static_cast<__bf16>(s[off + e]);
-  return b;
+// K operand of S^T = K . Q^T: key 32m + col, dims 16cc + 8half .. +7.
+__device__ __forceinline__ bf16x8 k_op(const uint16_t* kt, int m, int cc, int col, int half) {
+  const int row = 32 * m + col;
+  return *reinterpret_cast<const bf16x8*>(&kt[row * kD + swz_k(row, 2 * cc + half) * 8]);
 }
 
-// O^T += V^T . P^T over the tile's 64 keys, 16 keys per MFMA step. V is
-// row-major in LDS; ds_read_tr16_b64 hands lane l the 4 keys
-// 16ks + 4*half + k (k = 0..3) of channel 32dt + (l % 32): within each 16-lane
-// group, lane s supplies row 16ks + 4*half + s/4, channels 4*(s%4) .. +3.
-__device__ __forceinline__ void pv_tr16(const uint16_t* vt, const f32x16 (&p)[2], int lane,
-                                        f32x16 (&acc)[4]) {
+// V^T operand of O^T += V^T . P^T for key step ks (16 keys) and channel tile
+// dt: lane l gets channel 32dt + l%32 of keys 16ks + 8(e/4) + 4(l/32) + e%4,
+// the key order of S accumulator elements 8(ks%2) .. +7 of tile ks/2. Within
+// a 16-lane group, lane s of the ds_read_b64_tr_b16 supplies row
+// 16ks + 4(l/32) + s/4 (+8 for the second read), channels 4(s%4) .. +3.
+__device__ __forceinline__ bf16x8 v_op(const uint16_t* vt, int ks, int dt, int lane) {
   const int g = lane >> 4, sl = lane & 15;
   const int half = g >> 1;
-  const int sub = sl & 1;                       // 8-byte half of the 16-byte chunk
-  const int cpair = 2 * (g & 1) + ((sl & 3) >> 1);
+  const int sub = sl & 1;
+  const int chunk = 4 * dt + 2 * (g & 1) + ((sl & 3) >> 1);
+  const int row0 = 16 * ks + 4 * half + (sl >> 2);
+  const int row1 = row0 + 8;
+  const bf16x4 lo = tr16(&vt[row0 * kD + swz_v(row0, chunk) * 8 + sub * 4]);
+  const bf16x4 hi = tr16(&vt[row1 * kD + swz_v(row1, chunk) * 8 + sub * 4]);
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+__device__ __forceinline__ void qk_tile(const uint16_t* kt, const bf16x8 (&q)[8], int col, int half,
+                                        f32x16 (&s)[2]) {
+  const f32x16 zero = {};
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    const bf16x8 b = to_bf16x8(p[ks >> 1], 8 * (ks & 1));
-    const int row0 = 16 * ks + 4 * half + (sl >> 2);
-    const int row1 = row0 + 8;
+  for (int cc = 0; cc < 8; ++cc) {
+    const bf16x8 a0 = k_op(kt, 0, cc, col, half);
+    const bf16x8 a1 = k_op(kt, 1, cc, col, half);
+    s[0] = mfma_bf16(a0, q[cc], cc == 0 ? zero : s[0]);
+    s[1] = mfma_bf16(a1, q[cc], cc == 0 ? zero : s[1]);
+  }
+}
+
+// O^T += V^T . P^T over the tile's 16 (key step, channel tile) operands, each
+// read three operands ahead of its MFMA.
+__device__ __forceinline__ void pv_tile(const uint16_t* vt, const bf16x8 (&pb)[4], int lane,
+                                        f32x16 (&o)[4]) {
+  constexpr int L = 3;
+  bf16x8 va[16];
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-      const int chunk = 4 * dt + cpair;
-      const bf16x4 lo = tr16(&vt[row0 * kD + swz_v(row0, chunk) * 8 + sub * 4]);
-      const bf16x4 hi = tr16(&vt[row1 * kD + swz_v(row1, chunk) * 8 + sub * 4]);
-      const bf16x8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-      acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[dt], 0, 0, 0);
-    }
+  for (int i = 0; i < L; ++i) va[i] = v_op(vt, i >> 2, i & 3, lane);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    if (i + L < 16) va[i + L] = v_op(vt, (i + L) >> 2, (i + L) & 3, lane);
+    o[i & 3] = mfma_bf16(va[i], pb[i >> 2], o[i & 3]);
   }
 }
 
 // ------------------------------------------------------------ online softmax
-constexpr float kMaxSlack = 8.f;
-
 struct SoftmaxState {
   float m;          // running max, in the exp2 domain (score * c)
   float l;          // partial row sum over this lane's keys
@@ -291,71 +310,107 @@ struct SoftmaxState {
   }
 };
 
-// Online softmax over one tile: p = exp2(s*c - m_new) replaces s in place.
-// Pooled keys carry weight len_j in the row sum (/root/reference/_tri_fwd.py:302-307).
-template <int BLK>
-__device__ __forceinline__ void softmax_update(SoftmaxState& st, f32x16 (&s)[2], const TileDesc& td,
-                                               float c, int half, int NT, int T) {
-  if (td.amask != ~0ull) {
+// x combined with the value of the lane 32 apart (one v_permlane32_swap).
+__device__ __forceinline__ float xhalf_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xhalf_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Running-max update: the max moves only when the tile max exceeds it by more
+// than kMaxSlack (log2 units), so p may reach 2^kMaxSlack (harmless in bf16 P
+// and fp32 sums) and the O rescale is rare.
+__device__ __forceinline__ float new_max(float m_old, float m_tile, float& alpha) {
+  const float m_new = m_tile > m_old + kMaxSlack ? m_tile : m_old;
+  alpha = m_old == m_new ? 1.f : __builtin_amdgcn_exp2f(m_old - m_new);
+  return m_new;
+}
+
+// p = exp2(s*c + neg) for elements [R0, R0 + 8) of s, packed to bf16 into pk;
+// the row sum accumulates the packed values (v_dot2 with ones).
+template <int R0>
+__device__ __forceinline__ float exp8(const f32x16& s, float c, float neg, bf16x8& pk, float sum) {
+  const bf16x2 ones = {static_cast<__bf16>(1.f), static_cast<__bf16>(1.f)};
 #pragma unroll
-    for (int m = 0; m < 2; ++m)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int kl = 32 * m + 8 * (r >> 2) + 4 * half + (r & 3);
-        if (!((td.amask >> kl) & 1ull)) s[m][r] = -INFINITY;
-      }
+  for (int e = 0; e < 8; e += 2) {
+    bf16x2 two;
+    two[0] = static_cast<__bf16>(__builtin_amdgcn_exp2f(fmaf(s[R0 + e], c, neg)));
+    two[1] = static_cast<__bf16>(__builtin_amdgcn_exp2f(fmaf(s[R0 + e + 1], c, neg)));
+    pk[e] = two[0];
+    pk[e + 1] = two[1];
+    sum = __builtin_amdgcn_fdot2_f32_bf16(two, ones, sum, false);
   }
-  float mx = -INFINITY;
-#pragma unroll
-  for (int m = 0; m < 2; ++m)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[m][r]);
-  mx = fmaxf(mx, __shfl_xor(mx, 32));
-  // The running max moves only when the tile's max exceeds it by more than
-  // kMaxSlack (log2 units): p may then reach 2^kMaxSlack, harmless in bf16 P
-  // and fp32 sums, and the O rescale becomes rare.
-  const float m_tile = mx * c;
-  const float m_new = m_tile > st.m + kMaxSlack ? m_tile : st.m;
-  const float alpha = st.m == m_new ? 1.f : __builtin_amdgcn_exp2f(st.m - m_new);
-  const float neg = -m_new;
-  float psum = 0.f;
-  if (td.pooled) {
-    const int tail = T - (NT - 1) * BLK;
-#pragma unroll
-    for (int m = 0; m < 2; ++m)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int kl = 32 * m + 8 * (r >> 2) + 4 * half + (r & 3);
-        const float p = __builtin_amdgcn_exp2f(fmaf(s[m][r], c, neg));
-        s[m][r] = p;
-        const float w = (td.first + kl == NT - 1) ? static_cast<float>(tail) : static_cast<float>(BLK);
-        psum = fmaf(p, w, psum);
-      }
-  } else {
-#pragma unroll
-    for (int m = 0; m < 2; ++m)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = __builtin_amdgcn_exp2f(fmaf(s[m][r], c, neg));
-        s[m][r] = p;
-        psum += p;
-      }
-  }
-  st.l = fmaf(st.l, alpha, psum);
+  return sum;
+}
+
+__device__ __forceinline__ void rescale(SoftmaxState& st, float alpha) {
   if (__any(alpha != 1.f)) {
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) st.acc[dt][r] *= alpha;
   }
-  st.m = m_new;
 }
 
-// o[qrow, :] = acc / l (bf16), rows past T skipped.
-__device__ __forceinline__ void store_output(const SoftmaxState& st, uint16_t* __restrict__ obase,
-                                             int64_t so_t, int qrow, int T, int half) {
-  const float l = st.l + __shfl_xor(st.l, 32);
-  const float inv = 1.f / l;
+// Softmax and P.V of one bf16 tile whose scores are in s (the plain path:
+// pooled, ragged and last tiles). Masked keys get -inf; pooled keys weigh
+// len_j in the row sum (/root/reference/_tri_fwd.py:302-307); P is rounded to
+// bf16 for the MFMA and, for exact tiles, summed as rounded (as on the
+// pipelined path).
+template <int BLK>
+__device__ __forceinline__ void finish_tile(SoftmaxState& st, f32x16 (&s)[2], const uint16_t* vt,
+                                            const TileDesc& td, float c, int lane, int NT, int T) {
+  const int half = lane >> 5;
+  if (td.amask != ~0ull) {
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const uint32_t bits = static_cast<uint32_t>(td.amask >> (32 * m + 4 * half));
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        s[m][r] = ((bits >> (8 * (r >> 2) + (r & 3))) & 1u) ? s[m][r] : -INFINITY;
+    }
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[m][r]);
+  float alpha;
+  st.m = new_max(st.m, xhalf_max(mx) * c, alpha);
+  const float neg = -st.m;
+  bf16x8 pb[4];
+  float psum = 0.f;
+  if (td.pooled) {
+    const int kl_last = NT - 1 - td.first;
+    const float tail = static_cast<float>(T - (NT - 1) * BLK);
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int kl = 32 * m + 8 * (r >> 2) + 4 * half + (r & 3);
+        const float p = __builtin_amdgcn_exp2f(fmaf(s[m][r], c, neg));
+        pb[2 * m + (r >> 3)][r & 7] = static_cast<__bf16>(p);
+        psum = fmaf(p, kl == kl_last ? tail : static_cast<float>(BLK), psum);
+      }
+  } else {
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      psum = exp8<0>(s[m], c, neg, pb[2 * m], psum);
+      psum = exp8<8>(s[m], c, neg, pb[2 * m + 1], psum);
+    }
+  }
+  st.l = fmaf(st.l, alpha, psum);
+  rescale(st, alpha);
+  pv_tile(vt, pb, lane, st.acc);
+}
+
+// O row qrow = acc / l in bf16 (rows past T skipped).
+__device__ __forceinline__ void store_rows(const SoftmaxState& st, uint16_t* __restrict__ obase,
+                                           int64_t so_t, int qrow, int T, int half) {
+  const float inv = 1.f / xhalf_sum(st.l);
   if (qrow >= T) return;
   uint16_t* orow = obase + static_cast<int64_t>(qrow) * so_t;
 #pragma unroll

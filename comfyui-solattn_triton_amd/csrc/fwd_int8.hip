@@ -1,22 +1,27 @@
 // INT8 Sol-Attn forward on gfx950 MFMA (/root/reference/_int8_fwd.py:208-372).
 //
-// Exact tiles: S = int32(qi . ki) * ((qs * c) * ks) on v_mfma_i32_32x32x32_i8.
+// Exact tiles: S = int32(qi . ki) * (qs*c * ks) on v_mfma_i32_32x32x32_i8.
 //   INT8_PV: P is quantised per row against the tile's own max,
-//     pe = exp2(s - bmax), code = min(pe*127 + 0.5, 127), and multiplied with
+//     pe = exp2(s - bmax), code = round(pe * 127), and multiplied with
 //     per-channel int8 V on the i8 MFMA; the row factor beta/127 (beta =
-//     exp2(bmax - m)) is applied per tile, the channel scale vscale[d] once at
-//     the end of the exact phase (it is the same for every tile).
+//     exp2(bmax - m)) is applied per tile, the channel scale vscale[d] once
+//     after the exact tiles (it is the same for every tile).
 //   otherwise: P.V in bf16 against the bf16 V, as in the BF16 forward.
-// Pooled tiles run afterwards in bf16 on the centred kc and vc. Tile order is
-// free: the online softmax is exact under reordering, up to fp32 rounding.
+// Pooled tiles run last in bf16 on the centred kc and vc. The online softmax
+// is exact under any tile order, up to fp32 rounding.
 //
-// Tiles are copied global -> LDS directly (double buffered). int8 K and V stay
-// row-major (128-byte rows, XOR-swizzled 16-byte chunks); ds_read_b64_tr_b8
-// delivers V transposed as the MFMA A operand.
+// Tile order: the ragged exact tile (if any) through a plain path, the full
+// exact tiles through a pipeline (step n: copies of K(n+2) and V(n+1); the i8
+// MFMAs of S(n+1) interleaved with the softmax of tile n; P(n).V(n), then the
+// conversion of S(n+1) to fp32 scores while tile n+1's ks are in LDS), then
+// the pooled tiles. Tiles are copied global -> LDS directly: int8 K and V rows
+// of 128 bytes with XOR-swizzled 16-byte chunks, ks behind the K rows;
+// ds_read_b64_tr_b8 delivers int8 V transposed as the MFMA A operand.
 #include "common.hpp"
 #include "fwd_common.hpp"
 
 namespace solattn {
+namespace int8fwd {
 
 constexpr int kI8Row = kD;                  // bytes per int8 K / V row
 constexpr int kKsOffset = kKeys * kI8Row;   // ks[64] after the int8 K rows (bytes)
@@ -30,59 +35,8 @@ __device__ __forceinline__ int swz_vi(int row, int chunk) {
   return chunk ^ (2 * (((row >> 1) & 1) | (((row >> 3) & 1) << 1)));
 }
 
-struct I8Source {
-  const int8_t* ki;  // rows of this batch/head, stride srow bytes
-  const float* ks;   // stride H floats
-  const int8_t* vi;
-  const uint16_t* v;  // bf16 V (INT8_PV off)
-  int64_t sv;
-  int64_t srow;
-  int H;
-};
-
-// Tile n: the exact tiles first (n < nexact), then the pooled tiles.
-template <int BLK>
-__device__ __forceinline__ TileDesc tile_desc_i8(const TileList& tl, int n, int T, int NT) {
-  return n < tl.nexact ? tile_desc<BLK>(tl, n + tl.npool, T, NT) : tile_desc<BLK>(tl, n - tl.nexact, T, NT);
-}
-
-template <int BLK, int NTHREADS, bool INT8_PV>
-__device__ __forceinline__ void issue_i8(uint16_t* kdst, uint16_t* vdst, const TileList& tl, int n,
-                                         const KVSource& src, const I8Source& is,
-                                         const TileOffsets<NTHREADS>& off, int T, int NT) {
-  if (n >= tl.nexact) {
-    issue_half<BLK, NTHREADS>(kdst, 0, tl, n - tl.nexact, src, off, T, NT);
-    issue_half<BLK, NTHREADS>(vdst, 1, tl, n - tl.nexact, src, off, T, NT);
-    return;
-  }
-  const TileDesc td = tile_desc_i8<BLK>(tl, n, T, NT);
-  const int wave_base = threadIdx.x & ~63;
-  char* kb = reinterpret_cast<char*>(kdst);
-  char* vb = reinterpret_cast<char*>(vdst);
-  // ks[64] (stride H floats) by 4-byte copies, behind the int8 rows.
-  if (threadIdx.x < kKeys) {
-    const int row = static_cast<int>(threadIdx.x) < td.nvalid ? static_cast<int>(threadIdx.x) : 0;
-    g2l4(is.ks + static_cast<int64_t>(td.first + row) * is.H, kb + kKsOffset);
-  }
-#pragma unroll
-  for (int u = 0; u < kKeys * 8 / NTHREADS; ++u) {
-    const int e = threadIdx.x + NTHREADS * u;
-    const int row = e >> 3, pc = e & 7;
-    const int64_t srow = td.first + (row < td.nvalid ? row : 0);
-    const int lds = (wave_base + NTHREADS * u) * 16;
-    g2l16(is.ki + srow * is.srow + swz_ki(row, pc) * 16, kb + lds);
-    if constexpr (INT8_PV) g2l16(is.vi + srow * is.srow + swz_vi(row, pc) * 16, vb + lds);
-  }
-  if constexpr (!INT8_PV) issue_half<BLK, NTHREADS>(vdst, 1, tl, n + tl.npool, src, off, T, NT);
-}
-
-__device__ __forceinline__ uint32_t quant_p4(float a, float b, float c, float d) {
-  // min(pe*127 + 0.5, 127) truncated: pe is in [0, 1]
-  const uint32_t qa = static_cast<uint32_t>(fminf(fmaf(a, 127.f, 0.5f), 127.f));
-  const uint32_t qb = static_cast<uint32_t>(fminf(fmaf(b, 127.f, 0.5f), 127.f));
-  const uint32_t qc = static_cast<uint32_t>(fminf(fmaf(c, 127.f, 0.5f), 127.f));
-  const uint32_t qd = static_cast<uint32_t>(fminf(fmaf(d, 127.f, 0.5f), 127.f));
-  return qa | (qb << 8) | (qc << 16) | (qd << 24);
+__device__ __forceinline__ i32x16 mfma_i8(const i32x4& a, const i32x4& b, const i32x16& c) {
+  return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
 }
 
 __device__ __forceinline__ i32x2 tr8(const char* p) {
@@ -91,106 +45,263 @@ __device__ __forceinline__ i32x2 tr8(const char* p) {
   return __builtin_bit_cast(i32x2, r);
 }
 
-// One exact int8 tile: S^T = Ki . Qi^T, online softmax, P.V.
-template <bool INT8_PV>
-__device__ __forceinline__ void exact_i8(SoftmaxState& st, const uint16_t* kt16, const uint16_t* vt16,
-                                         const i32x4 (&qireg)[4], float qsl, const TileDesc& td,
-                                         int lane) {
-  const int col = lane & 31, half = lane >> 5;
-  const char* kt = reinterpret_cast<const char*>(kt16);
-  i32x16 si[2];
-  const i32x16 zero = {};
-#pragma unroll
-  for (int cc = 0; cc < 4; ++cc)
-#pragma unroll
-    for (int m = 0; m < 2; ++m) {
-      const int row = 32 * m + col;
-      const i32x4 a = *reinterpret_cast<const i32x4*>(kt + row * kI8Row + swz_ki(row, 2 * cc + half) * 16);
-      si[m] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, qireg[cc], cc == 0 ? zero : si[m], 0, 0, 0);
-    }
-  // s = int32 * (qs*c * ks): the reference's exact_scores (/root/reference/_int8_fwd.py:328-330).
+// int8 K operand: key 32m + col, dims 32cc + 16half .. +15.
+__device__ __forceinline__ i32x4 ki_op(const char* kt, int m, int cc, int col, int half) {
+  const int row = 32 * m + col;
+  return *reinterpret_cast<const i32x4*>(kt + row * kI8Row + swz_ki(row, 2 * cc + half) * 16);
+}
+
+// s[m][r] = int32 score * ks[key]: the reference's exact_scores without the
+// query factor qs*c, which multiplies later (it is positive, so it commutes
+// with the row max) (/root/reference/_int8_fwd.py:328-330).
+__device__ __forceinline__ void scale_scores(const char* kt, const i32x16 (&si)[2], int half,
+                                             f32x16 (&s)[2]) {
   const float* ksl = reinterpret_cast<const float*>(kt + kKsOffset);
-  f32x16 s[2];
-  float mx = -INFINITY;
 #pragma unroll
-  for (int m = 0; m < 2; ++m) {
-    const uint32_t bits = static_cast<uint32_t>(td.amask >> (32 * m + 4 * half));
+  for (int m = 0; m < 2; ++m)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float4 k4 = *reinterpret_cast<const float4*>(ksl + 32 * m + 8 * i + 4 * half);
-      const float kk[4] = {k4.x, k4.y, k4.z, k4.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float v = static_cast<float>(si[m][4 * i + j]) * (qsl * kk[j]);
-        s[m][4 * i + j] = ((bits >> (8 * i + j)) & 1u) ? v : -INFINITY;
-        mx = fmaxf(mx, s[m][4 * i + j]);
-      }
+      s[m][4 * i + 0] = static_cast<float>(si[m][4 * i + 0]) * k4.x;
+      s[m][4 * i + 1] = static_cast<float>(si[m][4 * i + 1]) * k4.y;
+      s[m][4 * i + 2] = static_cast<float>(si[m][4 * i + 2]) * k4.z;
+      s[m][4 * i + 3] = static_cast<float>(si[m][4 * i + 3]) * k4.w;
     }
-  }
-  const float bmax = fmaxf(mx, __shfl_xor(mx, 32));
-  const float m_new = bmax > st.m + kMaxSlack ? bmax : st.m;
-  const float alpha = st.m == m_new ? 1.f : __builtin_amdgcn_exp2f(st.m - m_new);
-  if (__any(alpha != 1.f)) {
+}
+
+__device__ __forceinline__ void qk_i8_tile(const char* kt, const i32x4 (&qi)[4], int col, int half,
+                                           i32x16 (&si)[2]) {
+  const i32x16 zero = {};
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) st.acc[dt][r] *= alpha;
+  for (int cc = 0; cc < 4; ++cc) {
+    const i32x4 a0 = ki_op(kt, 0, cc, col, half);
+    const i32x4 a1 = ki_op(kt, 1, cc, col, half);
+    si[0] = mfma_i8(a0, qi[cc], cc == 0 ? zero : si[0]);
+    si[1] = mfma_i8(a1, qi[cc], cc == 0 ? zero : si[1]);
   }
+}
+
+// ---------------------------------------------------------- INT8 P . V path
+// p_e = exp2(s*qsl - bmax) in [0, 1] for the 16 scores of key tile m, codes
+// round(p_e * 127) (v_cvt_pk_u8_f32: nearest, ties to even) packed 4 per
+// dword in element order; returns the fp32 sum of p_e.
+__device__ __forceinline__ float probs_i8(const f32x16& s, float qsl, float negb, i32x4& pi) {
+  float sum = 0.f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    uint32_t d = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float pe = __builtin_amdgcn_exp2f(fmaf(s[4 * w + j], qsl, negb));
+      sum += pe;
+      d = __builtin_amdgcn_cvt_pk_u8_f32(pe * 127.f, j, d);
+    }
+    pi[w] = static_cast<int>(d);
+  }
+  return sum;
+}
+
+// O^T += (Vi^T . Pi^T) * f: lane (channel 32dt + col, half) takes keys
+// 32ks + 8i + 4half + j (i, j < 4) of the int8 V tile from two ds_read_tr8:
+// within a 16-lane group, lane s supplies key (s >> 1) of the 8 keys read,
+// channels 8(s & 1) .. +7.
+__device__ __forceinline__ void pv_i8(const char* vt, const i32x4 (&pi)[2], float f, int lane,
+                                      f32x16 (&acc)[4]) {
+  const i32x16 zero = {};
+  const int g = lane >> 4, sl = lane & 15, half = lane >> 5;
+  const int kk = sl >> 1;
+  const int key_in = 8 * (kk >> 2) + 4 * half + (kk & 3);
+  const auto tile = [&](int dt) {
+    const int chunk = 2 * dt + (g & 1);
+    i32x16 pv;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int r0 = 32 * ks + key_in, r1 = r0 + 16;
+      const i32x2 lo = tr8(vt + r0 * kI8Row + swz_vi(r0, chunk) * 16 + 8 * (sl & 1));
+      const i32x2 hi = tr8(vt + r1 * kI8Row + swz_vi(r1, chunk) * 16 + 8 * (sl & 1));
+      const i32x4 a = {lo[0], lo[1], hi[0], hi[1]};
+      pv = mfma_i8(a, pi[ks], ks == 0 ? zero : pv);
+    }
+    return pv;
+  };
+  // The MFMAs of channel tile dt+1 run while tile dt is converted. The empty
+  // asm pins each converted tile in place: left to itself the compiler issues
+  // all eight MFMAs first and sinks the conversions, holding four int32
+  // accumulators (64 VGPRs) at once.
+  i32x16 pv[2];
+  pv[0] = tile(0);
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) {
+    if (dt + 1 < 4) pv[(dt + 1) & 1] = tile(dt + 1);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[dt][r] = fmaf(static_cast<float>(pv[dt & 1][r]), f, acc[dt][r]);
+    asm volatile("" : "+v"(acc[dt]));
+  }
+}
+
+// Softmax + P.V of an exact tile whose scaled scores are in s (masked keys
+// already -inf): /root/reference/_int8_fwd.py:333-368.
+template <bool INT8_PV>
+__device__ __forceinline__ void exact_softmax_pv(SoftmaxState& st, f32x16 (&s)[2], const void* vt,
+                                                 float qsl, int lane) {
+  float mx = -INFINITY;
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[m][r]);
+  const float bmax = xhalf_max(mx) * qsl;
+  float alpha;
+  st.m = new_max(st.m, bmax, alpha);
   if constexpr (INT8_PV) {
-    // P against the tile max: pe in [0, 1], beta carries it to the running max
-    // (/root/reference/_int8_fwd.py:348-353).
-    const float beta = __builtin_amdgcn_exp2f(bmax - m_new);
+    const float beta = __builtin_amdgcn_exp2f(bmax - st.m);
+    i32x4 pi[2];
+    float psum = probs_i8(s[0], qsl, -bmax, pi[0]);
+    psum += probs_i8(s[1], qsl, -bmax, pi[1]);
+    st.l = fmaf(st.l, alpha, beta * psum);
+    rescale(st, alpha);
+    pv_i8(static_cast<const char*>(vt), pi, beta * (1.f / 127.f), lane, st.acc);
+  } else {
+    const float neg = -st.m;
+    bf16x8 pb[4];
     float psum = 0.f;
-    i32x4 pb[2];
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        s[m][r] = __builtin_amdgcn_exp2f(s[m][r] - bmax);
-        psum += s[m][r];
-      }
-#pragma unroll
-      for (int w = 0; w < 4; ++w)
-        pb[m][w] = static_cast<int>(quant_p4(s[m][4 * w], s[m][4 * w + 1], s[m][4 * w + 2], s[m][4 * w + 3]));
+      psum = exp8<0>(s[m], qsl, neg, pb[2 * m], psum);
+      psum = exp8<8>(s[m], qsl, neg, pb[2 * m + 1], psum);
     }
-    st.l = fmaf(st.l, alpha, beta * psum);
-    const float f = beta * (1.f / 127.f);
-    // O^T += Vi^T . Pi^T: lane (channel 32dt + col, half) takes keys
-    // 32ks + 8i + 4*half + j (i, j < 4) from two ds_read_tr8: within a 16-lane
-    // group, lane s supplies key (s >> 1) of the 8 keys, channels 8*(s & 1)..+7.
-    const char* vt = reinterpret_cast<const char*>(vt16);
-    const int g = lane >> 4, sl = lane & 15;
-    const int kk = sl >> 1;                       // key index within the 8 read
-    const int key_in = 8 * (kk >> 2) + 4 * half + (kk & 3);
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-      const int chunk = 2 * dt + (g & 1);         // 16-byte chunk of channels 32dt + 16(g&1)
-      i32x16 pv;
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const int r0 = 32 * ks + key_in, r1 = r0 + 16;
-        const i32x2 lo = tr8(vt + r0 * kI8Row + swz_vi(r0, chunk) * 16 + 8 * (sl & 1));
-        const i32x2 hi = tr8(vt + r1 * kI8Row + swz_vi(r1, chunk) * 16 + 8 * (sl & 1));
-        const i32x4 a = {lo[0], lo[1], hi[0], hi[1]};
-        pv = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, pb[ks], ks == 0 ? zero : pv, 0, 0, 0);
-      }
-#pragma unroll
-      for (int r = 0; r < 16; ++r) st.acc[dt][r] = fmaf(static_cast<float>(pv[r]), f, st.acc[dt][r]);
-    }
-  } else {
-    float psum = 0.f;
-    const float neg = -m_new;
-#pragma unroll
-    for (int m = 0; m < 2; ++m)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        s[m][r] = __builtin_amdgcn_exp2f(s[m][r] + neg);
-        psum += s[m][r];
-      }
     st.l = fmaf(st.l, alpha, psum);
-    pv_tr16(vt16, s, lane, st.acc);
+    rescale(st, alpha);
+    pv_tile(static_cast<const uint16_t*>(vt), pb, lane, st.acc);
   }
-  st.m = m_new;
+}
+
+// Pipelined step over full exact tile n (scaled scores in sc): the i8 MFMAs
+// of S(n+1) from the K tile kn are interleaved with the softmax of tile n;
+// then P(n).V(n) and the conversion of S(n+1) into sn (ks of tile n+1 from kn).
+template <bool INT8_PV>
+__device__ __forceinline__ void fast_step(SoftmaxState& st, f32x16 (&sc)[2], f32x16 (&sn)[2],
+                                          const char* kn, const void* vt, const i32x4 (&qi)[4],
+                                          float qsl, int lane) {
+  const int col = lane & 31, half = lane >> 5;
+  const i32x16 zero = {};
+  i32x16 si[2];
+  i32x4 ka[4][2];
+  float mx = -INFINITY, alpha = 1.f, bmax = 0.f, neg = 0.f, psum = 0.f;
+  bf16x8 pb[4];
+  i32x4 pi[2];
+  ka[0][0] = ki_op(kn, 0, 0, col, half);
+  ka[0][1] = ki_op(kn, 1, 0, col, half);
+#pragma unroll
+  for (int cc = 0; cc < 4; ++cc) {
+    if (cc + 1 < 4) {
+      ka[cc + 1][0] = ki_op(kn, 0, cc + 1, col, half);
+      ka[cc + 1][1] = ki_op(kn, 1, cc + 1, col, half);
+    }
+    si[0] = mfma_i8(ka[cc][0], qi[cc], cc == 0 ? zero : si[0]);
+    si[1] = mfma_i8(ka[cc][1], qi[cc], cc == 0 ? zero : si[1]);
+    if (cc == 0) {
+#pragma unroll
+      for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[m][r]);
+      bmax = xhalf_max(mx) * qsl;
+      st.m = new_max(st.m, bmax, alpha);
+      neg = -st.m;
+    } else if (cc == 1) {
+      if constexpr (INT8_PV) {
+        psum = probs_i8(sc[0], qsl, -bmax, pi[0]);
+      } else {
+        psum = exp8<0>(sc[0], qsl, neg, pb[0], psum);
+        psum = exp8<8>(sc[0], qsl, neg, pb[1], psum);
+      }
+    } else if (cc == 2) {
+      if constexpr (INT8_PV) {
+        psum += probs_i8(sc[1], qsl, -bmax, pi[1]);
+      } else {
+        psum = exp8<0>(sc[1], qsl, neg, pb[2], psum);
+        psum = exp8<8>(sc[1], qsl, neg, pb[3], psum);
+      }
+    }
+  }
+  float beta = 1.f;
+  if constexpr (INT8_PV) {
+    beta = __builtin_amdgcn_exp2f(bmax - st.m);
+    st.l = fmaf(st.l, alpha, beta * psum);
+  } else {
+    st.l = fmaf(st.l, alpha, psum);
+  }
+  rescale(st, alpha);
+  if constexpr (INT8_PV) {
+    scale_scores(kn, si, half, sn);  // frees the int32 scores before the P.V accumulators
+    pv_i8(static_cast<const char*>(vt), pi, beta * (1.f / 127.f), lane, st.acc);
+  } else {
+    pv_tile(static_cast<const uint16_t*>(vt), pb, lane, st.acc);
+    scale_scores(kn, si, half, sn);
+  }
+}
+
+// ------------------------------------------------------------------ copies
+struct I8Source {
+  const int8_t* ki;  // rows of this batch/head, stride srow bytes
+  const float* ks;   // stride H floats
+  const int8_t* vi;
+  int64_t srow;
+  int H;
+};
+
+// Per-lane byte offsets of this lane's 16-byte chunk of an int8 tile (copy u
+// adds (NTHREADS/8) u rows; the swizzles repeat, so one offset per tile kind).
+template <int NTHREADS>
+struct I8Offsets {
+  static constexpr int U = kKeys * 8 / NTHREADS;  // copies per lane per int8 tile
+  static constexpr int kKsPerWave = kKeys / (NTHREADS / 64);
+  uint32_t k, v, ks;  // ks: this lane's key of the tile (waves copy kKsPerWave each) x H x 4
+  __device__ __forceinline__ void init(int64_t srow, int H) {
+    const int row = threadIdx.x >> 3, pc = threadIdx.x & 7;
+    k = static_cast<uint32_t>(row * srow + swz_ki(row, pc) * 16);
+    v = static_cast<uint32_t>(row * srow + swz_vi(row, pc) * 16);
+    const int key = kKsPerWave * (threadIdx.x >> 6) + (threadIdx.x & 63);
+    ks = static_cast<uint32_t>(key * H * 4);
+  }
+};
+
+// int8 rows [first, first + 64) (rows past nvalid re-read row 0 when !FULL)
+// of ki (or vi) into an LDS tile; with KS also the 64 ks, each wave copying
+// 64 / nwaves of them.
+template <int NTHREADS, bool FULL, bool KS>
+__device__ __forceinline__ void issue_i8(char* dst, const int8_t* rows, const I8Source& is, int first,
+                                         int nvalid, uint32_t off, uint32_t ks_off, bool is_v) {
+  constexpr int U = I8Offsets<NTHREADS>::U;
+  const int wave_base = static_cast<int>(threadIdx.x) & ~63;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    char* d = dst + (wave_base + NTHREADS * u) * 16;
+    if constexpr (FULL) {
+      const char* base = reinterpret_cast<const char*>(rows) +
+                         static_cast<int64_t>(first + u * (NTHREADS / 8)) * is.srow;
+      g2l16_s(base, off, d);
+    } else {
+      const int e = threadIdx.x + NTHREADS * u;
+      const int row = e >> 3, pc = e & 7;
+      const int srow = first + (row < nvalid ? row : 0);
+      const int chunk = is_v ? swz_vi(row, pc) : swz_ki(row, pc);
+      g2l16(reinterpret_cast<const char*>(rows) + static_cast<int64_t>(srow) * is.srow + chunk * 16, d);
+    }
+  }
+  if constexpr (KS) {
+    constexpr int kpw = I8Offsets<NTHREADS>::kKsPerWave;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (lane < kpw) {
+      char* d = dst + kKsOffset + 4 * kpw * wave;
+      if constexpr (FULL) {
+        g2l4_s(is.ks + static_cast<int64_t>(first) * is.H, ks_off, d);
+      } else {
+        const int key = kpw * wave + lane;
+        const int r = key < nvalid ? key : 0;
+        g2l4(is.ks + static_cast<int64_t>(first + r) * is.H, d);
+      }
+    }
+  }
 }
 
 template <int BLK, bool INT8_PV>
@@ -218,62 +329,155 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
 
   const int ntiles = build_tile_list<BLK>(tl, counts, lists, mask, row, NT, W, T);
   if (ntiles == 0) return;  // cannot happen for routed lists: the diagonal is exact
-  const int nexact = tl.nexact;
+  const int nrag = ragged_tiles(tl, counts, row, NT, T);
+  const int nexact = tl.nexact;       // tiles [0, nexact): ragged first, then full
+  const int nfast = nexact - nrag;    // tiles [nexact, ntiles): pooled
 
   const int64_t bhD = (static_cast<int64_t>(b) * npad * H + h) * kD;
-  const KVSource src{nullptr, 0, INT8_PV ? nullptr : v + b * sv_b + h * sv_h, sv_t, kc + bhD,
+  const KVSource src{nullptr, 0, v + b * sv_b + h * sv_h, sv_t, kc + bhD,
                      static_cast<int64_t>(H) * kD, vc + bhD};
   const I8Source is{ki + (static_cast<int64_t>(b) * TP * H + h) * kD,
                     ks + static_cast<int64_t>(b) * TP * H + h,
-                    INT8_PV ? vi + (static_cast<int64_t>(b) * TP * H + h) * kD : nullptr,
-                    INT8_PV ? nullptr : v + b * sv_b + h * sv_h,
-                    sv_t,
-                    static_cast<int64_t>(H) * kD,
-                    H};
-  TileOffsets<NTHREADS> off;
-  off.init(0, sv_t);
-  issue_i8<BLK, NTHREADS, INT8_PV>(kbuf[0], vbuf[0], tl, 0, src, is, off, T, NT);
+                    vi + (static_cast<int64_t>(b) * TP * H + h) * kD,
+                    static_cast<int64_t>(H) * kD, H};
+  I8Offsets<NTHREADS> ioff;
+  ioff.init(is.srow, H);
+  CopyOffsets<NTHREADS> boff;
+  boff.init(0, sv_t);
+
+  // Exact tile n of this kernel's order: n < nrag is the ragged one (list
+  // tile nexact - 1), then list tiles 0 .. nfast-1.
+  const auto exact_tile = [&](int n) {
+    return exact_desc<BLK>(tl, n < nrag ? nexact - 1 : n - nrag, T, NT);
+  };
+  const auto issue_exact_full = [&](int n, char* kd, void* vd, bool with_k, bool with_v) {
+    const int first = exact_first<BLK>(tl, n - nrag);
+    if (with_k) issue_i8<NTHREADS, true, true>(kd, is.ki, is, first, kKeys, ioff.k, ioff.ks, false);
+    if (with_v) {
+      if constexpr (INT8_PV)
+        issue_i8<NTHREADS, true, false>(static_cast<char*>(vd), is.vi, is, first, kKeys, ioff.v, 0, true);
+      else
+        issue_full<NTHREADS>(static_cast<uint16_t*>(vd), src.v + static_cast<int64_t>(first) * src.sv,
+                             src.sv, boff.v);
+    }
+  };
+  const auto issue_tile = [&](int n, int buf) {
+    char* kd = reinterpret_cast<char*>(kbuf[buf]);
+    if (n >= nexact) {
+      const TileDesc td = pooled_desc(tl, n - nexact, NT);
+      issue_generic<NTHREADS>(kbuf[buf], 0, td, src);
+      issue_generic<NTHREADS>(vbuf[buf], 1, td, src);
+    } else if (n >= nrag) {
+      issue_exact_full(n, kd, vbuf[buf], true, true);
+    } else {
+      const TileDesc td = exact_tile(n);
+      issue_i8<NTHREADS, false, true>(kd, is.ki, is, td.first, td.nvalid, 0, 0, false);
+      if constexpr (INT8_PV)
+        issue_i8<NTHREADS, false, false>(reinterpret_cast<char*>(vbuf[buf]), is.vi, is, td.first,
+                                          td.nvalid, 0, 0, true);
+      else
+        issue_generic<NTHREADS>(vbuf[buf], 1, td, src);
+    }
+  };
+  issue_tile(0, 0);
 
   const int qrow = qb * BLK + wave * 32 + col;
   const bool qvalid = qrow < T;
   SoftmaxState st;
   st.init();
-  int n = 0;
+
+  // ---- exact tiles (int8 Q: 16 VGPRs)
   if (nexact > 0) {
-    // Exact phase: int8 Q (16 VGPRs) only.
     i32x4 qireg[4];
     float qsl = 0.f;
-    const int64_t qoff = (static_cast<int64_t>(b) * TP + qrow) * H + h;
-    const int8_t* qip = qi + qoff * kD + half * 16;
+    {
+      const int64_t qoff = (static_cast<int64_t>(b) * TP + qrow) * H + h;
+      const int8_t* qip = qi + qoff * kD + half * 16;
 #pragma unroll
-    for (int cc = 0; cc < 4; ++cc) {
-      uint4 r = make_uint4(0u, 0u, 0u, 0u);
-      if (qvalid) r = *reinterpret_cast<const uint4*>(qip + cc * 32);
-      qireg[cc] = __builtin_bit_cast(i32x4, r);
+      for (int cc = 0; cc < 4; ++cc) {
+        uint4 r = make_uint4(0u, 0u, 0u, 0u);
+        if (qvalid) r = *reinterpret_cast<const uint4*>(qip + cc * 32);
+        qireg[cc] = __builtin_bit_cast(i32x4, r);
+      }
+      if (qvalid) qsl = qs[qoff] * c;
     }
-    if (qvalid) qsl = qs[qoff] * c;
-    wait_tile_copies();
-    __syncthreads();
-    for (; n < nexact; ++n) {
-      if (n + 1 < ntiles)
-        issue_i8<BLK, NTHREADS, INT8_PV>(kbuf[(n + 1) & 1], vbuf[(n + 1) & 1], tl, n + 1, src, is,
-                                         off, T, NT);
-      const TileDesc td = tile_desc_i8<BLK>(tl, n, T, NT);
-      exact_i8<INT8_PV>(st, kbuf[n & 1], vbuf[n & 1], qireg, qsl, td, lane);
+    // ragged tile: plain, masked
+    if (nrag) {
       wait_tile_copies();
+      __syncthreads();
+      if (1 < ntiles) issue_tile(1, 1);
+      const TileDesc td = exact_tile(0);
+      i32x16 si[2];
+      f32x16 s[2];
+      const char* kt = reinterpret_cast<const char*>(kbuf[0]);
+      qk_i8_tile(kt, qireg, col, half, si);
+      scale_scores(kt, si, half, s);
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        const uint32_t bits = static_cast<uint32_t>(td.amask >> (32 * m + 4 * half));
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          s[m][r] = ((bits >> (8 * (r >> 2) + (r & 3))) & 1u) ? s[m][r] : -INFINITY;
+      }
+      exact_softmax_pv<INT8_PV>(st, s, vbuf[0], qsl, lane);
+      __syncthreads();
+    }
+    // full exact tiles, pipelined (tile F = nrag was issued into buffers F & 1)
+    const int F = nrag;
+    if (nfast > 0) {
+      const int E = nexact;  // one past the last full exact tile
+      wait_tile_copies();
+      __syncthreads();
+      if (F + 1 < E)
+        issue_exact_full(F + 1, reinterpret_cast<char*>(kbuf[(F + 1) & 1]), nullptr, true, false);
+      f32x16 sa[2], sb[2];
+      {
+        i32x16 si[2];
+        const char* kt = reinterpret_cast<const char*>(kbuf[F & 1]);
+        qk_i8_tile(kt, qireg, col, half, si);
+        scale_scores(kt, si, half, sa);
+      }
+      wait_tile_copies();
+      __syncthreads();  // kbuf[F & 1] is refilled (K of tile F+2) by the first step
+      int n = F;
+      // Step n needs n + 1 < E. K(n+2) of the last step is clamped to the
+      // last full tile: a redundant copy into a buffer nothing reads afterwards.
+      const auto step = [&](f32x16 (&sc)[2], f32x16 (&sn)[2]) {
+        issue_exact_full(min(n + 2, E - 1), reinterpret_cast<char*>(kbuf[n & 1]), nullptr, true, false);
+        issue_exact_full(n + 1, nullptr, vbuf[(n + 1) & 1], false, true);
+        fast_step<INT8_PV>(st, sc, sn, reinterpret_cast<const char*>(kbuf[(n + 1) & 1]), vbuf[n & 1],
+                           qireg, qsl, lane);
+        wait_tile_copies();
+        __syncthreads();
+        ++n;
+      };
+      while (n + 2 < E) {
+        step(sa, sb);
+        step(sb, sa);
+      }
+      if (n + 1 < E) {
+        step(sa, sb);
+        exact_softmax_pv<INT8_PV>(st, sb, vbuf[n & 1], qsl, lane);
+      } else {
+        exact_softmax_pv<INT8_PV>(st, sa, vbuf[n & 1], qsl, lane);
+      }
       __syncthreads();
     }
     if constexpr (INT8_PV) {
-      // Exact phase done: the per-channel V scale is the same for every tile.
+      // The per-channel V scale, common to every exact tile. The empty asm
+      // keeps its 64 loads here: hoisted above the exact tiles they would
+      // hold 64 VGPRs through the whole pipeline.
       const float* vsc = vscale + static_cast<int64_t>(bh) * kD;
+      asm volatile("" : "+s"(vsc));
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) st.acc[dt][r] *= vsc[32 * dt + 8 * (r >> 2) + 4 * half + (r & 3)];
     }
   }
-  if (n < ntiles) {
-    // Pooled phase: bf16 Q against the centred kc / vc.
+
+  // ---- pooled tiles (bf16 Q: 32 VGPRs)
+  if (nexact < ntiles) {
     bf16x8 qreg[8];
     const uint16_t* qp = q + b * sq_b + static_cast<int64_t>(qrow) * sq_t + h * sq_h + half * 8;
 #pragma unroll
@@ -282,25 +486,19 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
       if (qvalid) r = *reinterpret_cast<const uint4*>(qp + cc * 16);
       qreg[cc] = __builtin_bit_cast(bf16x8, r);
     }
-    if (n == 0) {
-      wait_tile_copies();
+    if (nexact > 0) issue_tile(nexact, nexact & 1);  // every earlier copy has landed
+    for (int n = nexact; n < ntiles; ++n) {
+      wait_tile_copies();  // tile n: the only copies in flight
       __syncthreads();
-    }
-    for (; n < ntiles; ++n) {
-      if (n + 1 < ntiles)
-        issue_i8<BLK, NTHREADS, INT8_PV>(kbuf[(n + 1) & 1], vbuf[(n + 1) & 1], tl, n + 1, src, is,
-                                         off, T, NT);
-      const TileDesc td = tile_desc_i8<BLK>(tl, n, T, NT);
+      if (n + 1 < ntiles) issue_tile(n + 1, (n + 1) & 1);
       f32x16 s[2];
-      qk_swz(kbuf[n & 1], qreg, col, half, s);
-      softmax_update<BLK>(st, s, td, c, half, NT, T);
-      pv_tr16(vbuf[n & 1], s, lane, st.acc);
-      wait_tile_copies();
+      qk_tile(kbuf[n & 1], qreg, col, half, s);
+      finish_tile<BLK>(st, s, vbuf[n & 1], pooled_desc(tl, n - nexact, NT), c, lane, NT, T);
       __syncthreads();
     }
   }
-
-  store_output(st, o + b * so_b + h * so_h, so_t, qrow, T, half);
+  wait_tile_copies();
+  store_rows(st, o + b * so_b + h * so_h, so_t, qrow, T, half);
 }
 
 template <int BLK, bool PV>
@@ -316,6 +514,7 @@ void launch_i8(uint32_t grid, hipStream_t s, const uint16_t* q, int64_t sq_b, in
                      counts, lists, mask, T, H, NT, W, c, o, so_b, so_t, so_h);
 }
 
+}  // namespace int8fwd
 }  // namespace solattn
 
 using namespace solattn;
@@ -338,12 +537,14 @@ extern "C" int solattn_fwd_int8(const uint16_t* q, int64_t sq_b, int64_t sq_t, i
   SOLATTN_REQUIRE(reinterpret_cast<uintptr_t>(qi) % 16 == 0 && reinterpret_cast<uintptr_t>(ki) % 16 == 0 &&
                       reinterpret_cast<uintptr_t>(ks) % 4 == 0,
                   SOLATTN_EINVAL, "fwd_int8: qi/ki must be 16-byte aligned");
+  // Lane offsets within a 64-row int8 tile are kept in 32 bits.
+  SOLATTN_REQUIRE(H * D < (1ll << 24), SOLATTN_EUNSUPPORTED, "fwd_int8: H*D beyond 2^24");
   if (int8_pv) {
     SOLATTN_REQUIRE(vi && vscale && reinterpret_cast<uintptr_t>(vi) % 16 == 0, SOLATTN_EINVAL,
                     "fwd_int8: int8_pv needs 16-byte aligned vi and vscale");
   } else {
     SOLATTN_REQUIRE(v && reinterpret_cast<uintptr_t>(v) % 16 == 0 && sv_b % 8 == 0 &&
-                        sv_t % 8 == 0 && sv_h % 8 == 0 && sv_t < (1ll << 24),
+                        sv_t % 8 == 0 && sv_h % 8 == 0 && sv_t >= 0 && sv_t < (1ll << 24),
                     SOLATTN_EINVAL, "fwd_int8: bf16 v must be 16-byte aligned with strides multiple of 8");
   }
   const int64_t NT = cdiv(T, block);
@@ -356,11 +557,11 @@ extern "C" int solattn_fwd_int8(const uint16_t* q, int64_t sq_b, int64_t sq_t, i
       counts, lists, mask, static_cast<int>(T), static_cast<int>(H), static_cast<int>(NT), W, c, o, \
       so_b, so_t, so_h
   if (block == 128) {
-    if (int8_pv) launch_i8<128, true>(SOLATTN_I8_ARGS);
-    else launch_i8<128, false>(SOLATTN_I8_ARGS);
+    if (int8_pv) int8fwd::launch_i8<128, true>(SOLATTN_I8_ARGS);
+    else int8fwd::launch_i8<128, false>(SOLATTN_I8_ARGS);
   } else {
-    if (int8_pv) launch_i8<64, true>(SOLATTN_I8_ARGS);
-    else launch_i8<64, false>(SOLATTN_I8_ARGS);
+    if (int8_pv) int8fwd::launch_i8<64, true>(SOLATTN_I8_ARGS);
+    else int8fwd::launch_i8<64, false>(SOLATTN_I8_ARGS);
   }
 #undef SOLATTN_I8_ARGS
   return check_launch("fwd_int8");
