@@ -96,11 +96,13 @@ def test_reorder_matches_index_select(pkg, dev):
     assert torch.equal(mort.reorder_tokens(s, idx, dim=0), s[idx])
 
 
-FWD_CASES = [  # (B, T, H, block, tau)
-    (1, 1000, 2, 64, 0.9),
-    (1, 2500, 2, 128, 0.9),
-    (2, 777, 3, 128, 0.3),
-    (1, 4096, 2, 64, 1.5),
+FWD_CASES = [  # (B, T, H, block, tau, sink_kv, sink_q)
+    (1, 1000, 2, 64, 0.9, (0, 0), (0, 0)),      # ragged last tile
+    (1, 2500, 2, 128, 0.9, (0, 0), (0, 0)),     # block 128: 64-row full tile + 4-row ragged tile
+    (2, 777, 3, 128, 0.3, (0, 0), (0, 0)),      # short rows, ragged 9-row tile
+    (1, 4096, 2, 64, 1.5, (0, 0), (0, 0)),      # no ragged tile
+    (2, 1000, 2, 64, 0.7, (0, 2), (0, 1)),      # sink blocks and sink query blocks
+    (1, 3000, 2, 128, 1e30, (0, 0), (0, 0)),    # band only: pooled-heavy, 1-6 exact tiles per block
 ]
 
 
@@ -115,12 +117,13 @@ def _rows(B, H, NT, limit=None, seed=0):
 @pytest.mark.parametrize("case", FWD_CASES)
 def test_fwd_bf16_vs_port(pkg, dev, case):
     tri = _mods(pkg)[1]
-    B, T, H, block, tau = case
+    B, T, H, block, tau, skv, sq = case
     print(f"[fwd_bf16] case={case}", flush=True)
     q, k, v = (randn_bf16((B, T, H, 128), s) for s in (20, 21, 22))
-    out = tri.sol_attn(q.to(dev), k.to(dev), v.to(dev), tau=tau, block=block)
+    out = tri.sol_attn(q.to(dev), k.to(dev), v.to(dev), tau=tau, block=block, sink_blocks=skv,
+                       sink_q=sq)
     torch.cuda.synchronize()
-    ref = oracle.prepare(bits(q), bits(k), bits(v), block=block, tau=tau)
+    ref = oracle.prepare(bits(q), bits(k), bits(v), block=block, tau=tau, sink_kv=skv, sink_q=sq)
     rows = _rows(B, H, ref["NT"], limit=24)
     port = oracle.forward_port(bits(q), bits(k), bits(v), ref, rows)
     err, cos = compare_rows(out.float().cpu().numpy(), port, block)
@@ -128,12 +131,14 @@ def test_fwd_bf16_vs_port(pkg, dev, case):
     assert err < BF16_MAXABS and cos >= BF16_COS
 
 
-def test_fwd_bf16_all_exact_is_dense(pkg, dev):
+@pytest.mark.parametrize("block", [64, 128])
+def test_fwd_bf16_all_exact_is_dense(pkg, dev, block):
     """tau = -inf routes every block: the output is dense SDPA."""
     tri = _mods(pkg)[1]
     B, T, H = 1, 1500, 2
+    print(f"[fwd_bf16 dense] block={block}", flush=True)
     q, k, v = (randn_bf16((B, T, H, 128), s) for s in (30, 31, 32))
-    out = tri.sol_attn(q.to(dev), k.to(dev), v.to(dev), tau=-1e30, block=128)
+    out = tri.sol_attn(q.to(dev), k.to(dev), v.to(dev), tau=-1e30, block=block)
     ref = torch.nn.functional.scaled_dot_product_attention(
         *(t.float().transpose(1, 2).to(dev) for t in (q, k, v))).transpose(1, 2)
     err = (out.float() - ref).abs().max().item()
@@ -142,15 +147,17 @@ def test_fwd_bf16_all_exact_is_dense(pkg, dev):
 
 
 @pytest.mark.parametrize("int8_pv", [True, False])
-@pytest.mark.parametrize("case", FWD_CASES[:3])
+@pytest.mark.parametrize("case", FWD_CASES)
 def test_fwd_int8_vs_port(pkg, dev, case, int8_pv):
     i8 = _mods(pkg)[2]
-    B, T, H, block, tau = case
+    B, T, H, block, tau, skv, sq = case
     print(f"[fwd_int8] case={case} int8_pv={int8_pv}", flush=True)
     q, k, v = (randn_bf16((B, T, H, 128), s) for s in (40, 41, 42))
-    out = i8.sol_attn_int8(q.to(dev), k.to(dev), v.to(dev), tau=tau, block=block, int8_pv=int8_pv)
+    out = i8.sol_attn_int8(q.to(dev), k.to(dev), v.to(dev), tau=tau, block=block, int8_pv=int8_pv,
+                           sink_blocks=skv, sink_q=sq)
     torch.cuda.synchronize()
-    ref = oracle.prepare(bits(q), bits(k), bits(v), block=block, tau=tau, int8=True, int8_pv=int8_pv)
+    ref = oracle.prepare(bits(q), bits(k), bits(v), block=block, tau=tau, int8=True, int8_pv=int8_pv,
+                         sink_kv=skv, sink_q=sq)
     rows = _rows(B, H, ref["NT"], limit=16)
     port = oracle.forward_int8_port(bits(q), bits(v), ref, rows, int8_pv=int8_pv)
     err, cos = compare_rows(out.float().cpu().numpy(), port, block)
