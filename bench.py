@@ -71,7 +71,7 @@ def make_inputs(cfg, device="cpu", dtype=None):
         if seed == 1 and cfg.get("k_offset"):
             g = torch.Generator().manual_seed(3)
             t = t + (cfg["k_offset"] * torch.randn(1, 1, H, D, generator=g)).to(device)
-        out.append(t.to(dtype))
+        out.append(t.to(dtype).contiguous())
         del t
     return tuple(out)
 
@@ -92,6 +92,32 @@ def routed_flops(counts, mask, T, block, D):
     exact_tok = (ex.double() * lens).sum(-1)
     n_approx = (~ex).sum(-1).double()
     return float(4 * D * (lens * (exact_tok + n_approx)).sum())
+
+
+def split_ops(counts, mask, T, block, D):
+    """(exact, pooled) algorithmic ops of the forward on valid tokens: half of
+    each is QK, half P.V (the terms of routed_flops)."""
+    NT = (T + block - 1) // block
+    lens = torch.full((NT,), float(block), dtype=torch.float64)
+    lens[-1] = T - (NT - 1) * block
+    j = torch.arange(NT)
+    words = mask.to(torch.int64)[..., j >> 5] & 0xFFFFFFFF
+    ex = ((words >> (j & 31)) & 1).bool()
+    exact = float(4 * D * (lens * (ex.double() * lens).sum(-1)).sum())
+    pooled = float(4 * D * (lens * (~ex).sum(-1).double()).sum())
+    return exact, pooled
+
+
+def int8_roofline(ms, exact, pooled, int8_pv):
+    """Fraction of the MFMA roofline for the INT8 forward: the time the op mix
+    takes at peak (QK on int8 MFMA, exact P.V on int8 or bf16 MFMA, pooled tiles
+    on bf16 MFMA) over the measured launch time."""
+    ideal_ms = 1e3 * (exact / 2 / (PEAK_INT8_TOPS * 1e12)
+                      + exact / 2 / ((PEAK_INT8_TOPS if int8_pv else PEAK_BF16_TFLOPS) * 1e12)
+                      + pooled / (PEAK_BF16_TFLOPS * 1e12))
+    return {"launch_ms": round(ms, 4), "exact_ops": exact, "pooled_flops": pooled,
+            "ideal_ms_at_peak": round(ideal_ms, 4), "frac": round(ideal_ms / ms, 4),
+            "tops": round((exact + pooled) / (ms * 1e-3) / 1e12, 2)}
 
 
 def time_cuda(fn, steps, warmup):
@@ -178,16 +204,17 @@ def run_kernel_only(args, mods, cfg, q, k, v):
     del src, dst
     if args.kernel_only == "fwd":
         r = mods["_preprocess"].route(q, k, v, scale=D ** -0.5, tau=tau, block=block)
-        out = torch.empty_like(q)
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
         for _ in range(args.steps):
             mods["_tri_fwd"].forward_bf16(q, k, v, r, out=out)
-    elif args.kernel_only == "fwd_int8":
+    elif args.kernel_only in ("fwd_int8", "fwd_int8_bf16pv"):
         fp = mods["_fused_prep"].fused_preprocess_routing(q, k, v, tau=tau, scale=D ** -0.5,
                                                           block=block)
         r, qi, qs, ki, ks, vi = fp
-        out = torch.empty_like(q)
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+        pv = args.kernel_only == "fwd_int8"
         for _ in range(args.steps):
-            mods["_int8_fwd"].forward_int8(q, v, r, qi, qs, ki, ks, vi, out=out)
+            mods["_int8_fwd"].forward_int8(q, v, r, qi, qs, ki, ks, vi, int8_pv=pv, out=out)
     elif args.kernel_only == "prep":
         for _ in range(args.steps):
             mods["_preprocess"].route(q, k, v, scale=D ** -0.5, tau=tau, block=block)
@@ -207,8 +234,10 @@ def main():
     ap.add_argument("--config", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
-    ap.add_argument("--extra", action="store_true", help="also time INT8 (cfg 3) and cfg 4")
-    ap.add_argument("--kernel-only", choices=["fwd", "fwd_int8", "prep", "reorder"],
+    ap.add_argument("--extra", action="store_true", help="also time the INT8 forward (cfg 3)")
+    ap.add_argument("--block", type=int, choices=[64, 128],
+                    help="routing block size instead of the config's (a diagnostic, not the metric)")
+    ap.add_argument("--kernel-only", choices=["fwd", "fwd_int8", "fwd_int8_bf16pv", "prep", "reorder"],
                     help="profiling driver: run only this kernel --steps times (after a "
                          "512 MiB device copy used to calibrate memory counters); no JSON")
     args = ap.parse_args()
@@ -222,7 +251,9 @@ def main():
 
     mods = _pkg()
     dev = torch.device("cuda:0")
-    cfg = CONFIGS[args.config]
+    cfg = dict(CONFIGS[args.config])
+    if args.block:
+        cfg["block"] = args.block
     print(f"[bench] config {args.config} {cfg['name']}: generating inputs", file=sys.stderr, flush=True)
     q, k, v = make_inputs(cfg, dev)
     B, T, H, D = q.shape
@@ -244,7 +275,7 @@ def main():
     ms = time_cuda(step, args.steps, args.warmup)
 
     r = mods["_preprocess"].route(q, k, v, scale=D ** -0.5, tau=tau, block=block)
-    out = torch.empty_like(q)
+    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     fwd = lambda: mods["_tri_fwd"].forward_bf16(q, k, v, r, out=out)
     fwd_ms = time_cuda(fwd, args.steps, args.warmup)
     prep_ms = time_cuda(lambda: mods["_preprocess"].route(q, k, v, scale=D ** -0.5, tau=tau,
@@ -267,13 +298,14 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (seeded smooth field + noise, Morton 3d reordered)",
+        "data": "synthetic (seeded smooth field + noise" + (", Morton 3d reordered)" if cfg["morton"] else ")"),
         "config": {"workload": f"cfg{args.config} {cfg['name']}: B{B} H{H} D{D} N{T} grid "
                                f"{'x'.join(map(str, cfg['grid']))} block {block} tau {tau}",
                    "global_batch": B, "seq_len": T, "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": _traffic(), "kernel": "fwd_bf16_kernel<128>",
+                     "traffic": _traffic() if (args.config, block) == (2, 128) else None,
+                     "kernel": f"bf16fwd::fwd_bf16_kernel<{block}>",
                      "algorithmic_flops_per_launch": rflops, "launch_ms": round(fwd_ms, 4)},
         "routed_density": round(density, 4),
         "prep_ms": round(prep_ms, 4),
@@ -289,6 +321,21 @@ def main():
         for key, pv in (("int8_ms", False), ("int8_pv_ms", True)):
             line[key] = {str(t): round(time_cuda(lambda: i8(q, k, v, tau=t, block=block, int8_pv=pv),
                                                  args.steps, args.warmup), 4) for t in (0.8, 0.9, 0.95)}
+        # the INT8 forward kernel alone at the config's tau, against the MFMA roofline
+        fp = mods["_fused_prep"].fused_preprocess_routing(q, k, v, tau=tau, scale=D ** -0.5,
+                                                          block=block)
+        ri, qi, qs, ki, ks, vi = fp
+        exact, pooled = split_ops(ri.counts.cpu(), ri.mask.cpu(), T, block, D)
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+        line["int8_fwd"] = {}
+        for key, pv in (("pv_bf16", False), ("pv_int8", True)):
+            ms_i8 = time_cuda(lambda: mods["_int8_fwd"].forward_int8(q, v, ri, qi, qs, ki, ks, vi,
+                                                                     int8_pv=pv, out=out),
+                              args.steps, args.warmup)
+            line["int8_fwd"][key] = int8_roofline(ms_i8, exact, pooled, pv)
+        line["int8_fwd"]["routed_density"] = round(float(ri.counts.double().sum()
+                                                         / (B * H * NT * NT)), 4)
+        del fp, ri, qi, qs, ki, ks, vi, out
     if not args.no_cpu:
         print("[bench] CPU baseline", file=sys.stderr, flush=True)
         line["cpu_baseline"] = cpu_baseline(cfg, q, k, v, args.cpu_budget)
