@@ -17,6 +17,7 @@ attention path, timed on a bounded sample on this host).
 from __future__ import annotations
 
 import argparse
+import importlib
 import json
 import math
 import os
@@ -215,6 +216,15 @@ def run_kernel_only(args, mods, cfg, q, k, v):
         pv = args.kernel_only == "fwd_int8"
         for _ in range(args.steps):
             mods["_int8_fwd"].forward_int8(q, v, r, qi, qs, ki, ks, vi, int8_pv=pv, out=out)
+    elif args.kernel_only == "quant":
+        fq = importlib.import_module(mods["_preprocess"].__name__.rsplit(".", 1)[0] + "._fused_quant")
+        fp = mods["_fused_prep"].fused_preprocess_routing(q, k, v, tau=tau, scale=D ** -0.5,
+                                                          block=block)
+        r = fp[0]
+        for _ in range(args.steps):
+            fq.quantize_bthd(q)
+            fq.quantize_bthd(k, mean=r.kc_mean.reshape(-1, D))
+            fq.quantize_v_per_channel(v)
     elif args.kernel_only == "prep":
         for _ in range(args.steps):
             mods["_preprocess"].route(q, k, v, scale=D ** -0.5, tau=tau, block=block)
@@ -237,7 +247,7 @@ def main():
     ap.add_argument("--extra", action="store_true", help="also time the INT8 forward (cfg 3)")
     ap.add_argument("--block", type=int, choices=[64, 128],
                     help="routing block size instead of the config's (a diagnostic, not the metric)")
-    ap.add_argument("--kernel-only", choices=["fwd", "fwd_int8", "fwd_int8_bf16pv", "prep", "reorder"],
+    ap.add_argument("--kernel-only", choices=["fwd", "fwd_int8", "fwd_int8_bf16pv", "prep", "quant", "reorder"],
                     help="profiling driver: run only this kernel --steps times (after a "
                          "512 MiB device copy used to calibrate memory counters); no JSON")
     args = ap.parse_args()

@@ -64,12 +64,19 @@ def test_route_bit_exact(pkg, dev, case, int8):
         assert np.array_equal(r.vscale.cpu().numpy().view(np.uint32), ref["vscale"].view(np.uint32))
 
 
+@pytest.mark.parametrize("shape", [(2, 333, 3), (1, 2048, 8)])
 @pytest.mark.parametrize("mean", [False, True])
-def test_quant_bit_exact(pkg, dev, mean):
+def test_quant_bit_exact(pkg, dev, mean, shape):
+    """Codes and scales bit-exact, including exact ties: rows with scale 1 and
+    values k + 0.5 must round away from zero."""
     fq = _mods(pkg)[4]
-    B, T, H = 2, 333, 3
+    B, T, H = shape
     x = randn_bf16((B, T, H, 128), 5, scale=3.0)
     x[0, 7, 1] = 0  # all-zero row: scale floors at 1e-8
+    ties = torch.arange(128, dtype=torch.float32) + 0.5
+    ties[-1] = 127.0  # row max 127: scale exactly 1
+    x[0, 5, 0] = ties.to(torch.bfloat16)
+    x[0, 6, H - 1] = (-ties).to(torch.bfloat16)
     m = torch.randn(B, H, 128, generator=torch.Generator().manual_seed(6)) if mean else None
     xi, xs = fq.quantize_bthd(x.to(dev), mean=None if m is None else m.reshape(B * H, 128).to(dev))
     rxi, rxs = oracle.quant_rows(bits(x), None if m is None else m.numpy())
