@@ -177,11 +177,24 @@ def cpu_baseline(cfg, q, k, v, budget_s=15.0):
         "unit": "ms/call",
         "cores": threads,
         "kind": "port",
-        "sample": (f"oracle C routing on the full input ({t_prep:.2f} s) + torch-fp32 masked "
-                   f"attention over [tokens; pooled keys] for {done} of {len(order)} "
-                   f"(head, query-block) pairs ({t_attn:.1f} s), scaled to the full call"),
+        "cpu": _cpu_model(),
+        "sample": (f"reference semantics, restated (the reference has no CPU path): oracle C "
+                   f"routing on the full input ({t_prep:.2f} s) + torch-fp32 masked attention "
+                   f"over [tokens; pooled keys] for {done} of {len(order)} (head, query-block) "
+                   f"pairs ({t_attn:.1f} s), scaled to the full call"),
         "dense_equiv_tflops": round(dense_flops(B, H, T, D) / per_call_s / 1e12, 4),
     }
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip() + f" ({os.cpu_count()} logical CPUs)"
+    except OSError:
+        pass
+    return None
 
 
 def _traffic():
@@ -247,6 +260,9 @@ def main():
     ap.add_argument("--extra", action="store_true", help="also time the INT8 forward (cfg 3)")
     ap.add_argument("--block", type=int, choices=[64, 128],
                     help="routing block size instead of the config's (a diagnostic, not the metric)")
+    ap.add_argument("--heads", type=int,
+                    help="number of heads instead of the config's, e.g. 3 = one GPU's share of an "
+                         "8-way head split at cfg 2 (not the metric)")
     ap.add_argument("--kernel-only", choices=["fwd", "fwd_int8", "fwd_int8_bf16pv", "prep", "quant", "reorder"],
                     help="profiling driver: run only this kernel --steps times (after a "
                          "512 MiB device copy used to calibrate memory counters); no JSON")
@@ -264,6 +280,8 @@ def main():
     cfg = dict(CONFIGS[args.config])
     if args.block:
         cfg["block"] = args.block
+    if args.heads:
+        cfg["H"] = args.heads
     print(f"[bench] config {args.config} {cfg['name']}: generating inputs", file=sys.stderr, flush=True)
     q, k, v = make_inputs(cfg, dev)
     B, T, H, D = q.shape
@@ -314,7 +332,7 @@ def main():
                    "global_batch": B, "seq_len": T, "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": _traffic() if (args.config, block) == (2, 128) else None,
+                     "traffic": _traffic() if (args.config, block, H) == (2, 128, 24) else None,
                      "kernel": f"bf16fwd::fwd_bf16_kernel<{block}>",
                      "algorithmic_flops_per_launch": rflops, "launch_ms": round(fwd_ms, 4)},
         "routed_density": round(density, 4),
@@ -346,6 +364,11 @@ def main():
         line["int8_fwd"]["routed_density"] = round(float(ri.counts.double().sum()
                                                          / (B * H * NT * NT)), 4)
         del fp, ri, qi, qs, ki, ks, vi, out
+        # dense comparator at the same shape: every block exact (tau = -inf)
+        dense_ms = time_cuda(lambda: sol_attn(q, k, v, tau=-1e30, block=block), max(3, args.steps // 4),
+                             1)
+        line["dense_all_exact_ms"] = round(dense_ms, 3)
+        line["dense_all_exact_tflops"] = round(dflops / (dense_ms * 1e-3) / 1e12, 1)
     if not args.no_cpu:
         print("[bench] CPU baseline", file=sys.stderr, flush=True)
         line["cpu_baseline"] = cpu_baseline(cfg, q, k, v, args.cpu_budget)
