@@ -30,10 +30,12 @@ namespace solattn {
 namespace bf16fwd {
 
 // Pipelined step over full exact tile n (scores in sc): S(n+1) from the K tile
-// kn goes to sn, interleaved with the softmax of tile n; then P(n) . V(n).
+// kn goes to sn, interleaved with the softmax of tile n; `mid` runs before
+// P(n) . V(n).
+template <typename Mid>
 __device__ __forceinline__ void fast_step(SoftmaxState& st, f32x16 (&sc)[2], f32x16 (&sn)[2],
                                           const uint16_t* kn, const uint16_t* vt,
-                                          const bf16x8 (&q)[8], float c, int lane) {
+                                          const bf16x8 (&q)[8], float c, int lane, Mid&& mid) {
   const int col = lane & 31, half = lane >> 5;
   const f32x16 zero = {};
   bf16x8 pb[4];
@@ -70,6 +72,7 @@ __device__ __forceinline__ void fast_step(SoftmaxState& st, f32x16 (&sc)[2], f32
   }
   st.l = fmaf(st.l, alpha, psum);
   rescale(st, alpha);
+  mid();
   pv_tile(vt, pb, lane, st.acc);
 }
 
@@ -82,8 +85,11 @@ __device__ __forceinline__ TileDesc desc(const TileList& tl, int n, int nrag, in
   return exact_desc<BLK>(tl, n - tl.npool - nrag, T, NT);
 }
 
-template <int BLK>
-__global__ void __launch_bounds__(BLK * 2, 2)
+// NBUF = 2: K and V tiles double buffered (64 KiB), two workgroups per CU.
+// NBUF = 1: single buffered (32 KiB), four workgroups per CU; the pipeline
+// step then waits twice (K refilled after the QK phase, V after P.V).
+template <int BLK, int NBUF>
+__global__ void __launch_bounds__(BLK * 2) __attribute__((amdgpu_waves_per_eu(2)))
 fwd_bf16_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
                 const uint16_t* __restrict__ k, int64_t sk_b, int64_t sk_t, int64_t sk_h,
                 const uint16_t* __restrict__ v, int64_t sv_b, int64_t sv_t, int64_t sv_h,
@@ -93,9 +99,10 @@ fwd_bf16_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
                 uint16_t* __restrict__ o, int64_t so_b, int64_t so_t, int64_t so_h) {
   constexpr int NTHREADS = BLK * 2;
   constexpr int kCopiesPerTile = 2 * CopyOffsets<NTHREADS>::U;
-  __shared__ __align__(16) uint16_t kbuf[2][kTileElems];
-  __shared__ __align__(16) uint16_t vbuf[2][kTileElems];
+  __shared__ __align__(16) uint16_t kbuf[NBUF][kTileElems];
+  __shared__ __align__(16) uint16_t vbuf[NBUF][kTileElems];
   __shared__ TileList tl;
+  const auto bi = [](int n) { return NBUF == 2 ? (n & 1) : 0; };  // buffer of tile n
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int col = lane & 31, half = lane >> 5;
@@ -152,42 +159,71 @@ fwd_bf16_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
   SoftmaxState st;
   st.init();
 
-  // ---- plain tiles (pooled, ragged): tile n+1 is copied while tile n computes
+  // ---- plain tiles (pooled, ragged)
   for (int n = 0; n < nplain; ++n) {
-    if (n + 1 < ntiles) {
-      issue_tile(n + 1, (n + 1) & 1);
-      wait_vmcnt<kCopiesPerTile>();  // tile n landed; tile n+1 stays in flight
+    if constexpr (NBUF == 2) {
+      // tile n+1 is copied while tile n computes
+      if (n + 1 < ntiles) {
+        issue_tile(n + 1, (n + 1) & 1);
+        wait_vmcnt<kCopiesPerTile>();  // tile n landed; tile n+1 stays in flight
+      } else {
+        wait_tile_copies();
+      }
     } else {
       wait_tile_copies();
     }
     __syncthreads();
     f32x16 s[2];
-    qk_tile(kbuf[n & 1], qreg, col, half, s);
-    finish_tile<BLK>(st, s, vbuf[n & 1], desc<BLK>(tl, n, nrag, T, NT), c, lane, NT, T);
+    qk_tile(kbuf[bi(n)], qreg, col, half, s);
+    finish_tile<BLK>(st, s, vbuf[bi(n)], desc<BLK>(tl, n, nrag, T, NT), c, lane, NT, T);
     __syncthreads();
+    if constexpr (NBUF == 1) {
+      if (n + 1 < ntiles) issue_tile(n + 1, 0);
+    }
   }
 
-  // ---- full exact tiles, pipelined; tile F is in buffer F & 1 (or in flight)
+  // ---- full exact tiles, pipelined; tile F was issued into buffers bi(F).
+  // K(n+2) past the last tile is clamped to it: a redundant copy into a
+  // buffer that nothing reads afterwards, which keeps the loop free of branches.
   const int F = nplain;
   if (F < ntiles) {
-    wait_tile_copies();
-    __syncthreads();
-    if (F + 1 < ntiles) issue_k(F + 1, (F + 1) & 1);
     f32x16 sa[2], sb[2];
-    qk_tile(kbuf[F & 1], qreg, col, half, sa);
-    wait_tile_copies();
-    __syncthreads();  // kbuf[F & 1] is refilled (K of tile F+2) by the first step
-
     int n = F;
-    // Step n computes S(n+1) and needs n + 1 < ntiles. K(n+2) of the last
-    // step is clamped to the last tile: a redundant copy into a buffer that
-    // nothing reads afterwards, which keeps the loop free of branches.
-    const auto step = [&](f32x16 (&sc)[2], f32x16 (&sn)[2]) {
-      issue_k(min(n + 2, ntiles - 1), n & 1);
-      issue_v(n + 1, (n + 1) & 1);
-      fast_step(st, sc, sn, kbuf[(n + 1) & 1], vbuf[n & 1], qreg, c, lane);
+    if constexpr (NBUF == 2) {
       wait_tile_copies();
       __syncthreads();
+      if (F + 1 < ntiles) issue_k(F + 1, (F + 1) & 1);
+      qk_tile(kbuf[F & 1], qreg, col, half, sa);
+      wait_tile_copies();
+      __syncthreads();  // kbuf[F & 1] is refilled (K of tile F+2) by the first step
+    } else {
+      wait_tile_copies();
+      __syncthreads();
+      qk_tile(kbuf[0], qreg, col, half, sa);
+      __syncthreads();  // kbuf is free
+      if (F + 1 < ntiles) issue_k(F + 1, 0);
+      wait_tile_copies();
+      __syncthreads();  // K(F+1) and V(F) in LDS
+    }
+    // Step n computes S(n+1) and needs n + 1 < ntiles.
+    const auto step = [&](f32x16 (&sc)[2], f32x16 (&sn)[2]) {
+      if constexpr (NBUF == 2) {
+        issue_k(min(n + 2, ntiles - 1), n & 1);
+        issue_v(n + 1, (n + 1) & 1);
+        fast_step(st, sc, sn, kbuf[(n + 1) & 1], vbuf[n & 1], qreg, c, lane, [] {});
+        wait_tile_copies();
+        __syncthreads();
+      } else {
+        // On entry kbuf holds K(n+1), vbuf V(n) (copy possibly in flight).
+        fast_step(st, sc, sn, kbuf[0], vbuf[0], qreg, c, lane, [&] {
+          wait_tile_copies();  // V(n)
+          __syncthreads();     // every wave is done with K(n+1)
+          issue_k(min(n + 2, ntiles - 1), 0);
+        });
+        wait_tile_copies();  // K(n+2)
+        __syncthreads();     // every wave is done with V(n)
+        issue_v(n + 1, 0);
+      }
       ++n;
     };
     // Pairs of steps, so the S buffers swap roles without register copies.
@@ -198,11 +234,20 @@ fwd_bf16_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
     const TileDesc full{0, 0, kKeys, ~0ull};
     if (n + 1 < ntiles) {
       step(sa, sb);
-      finish_tile<BLK>(st, sb, vbuf[n & 1], full, c, lane, NT, T);
+      if constexpr (NBUF == 1) {
+        wait_tile_copies();
+        __syncthreads();
+      }
+      finish_tile<BLK>(st, sb, vbuf[bi(n)], full, c, lane, NT, T);
     } else {
-      finish_tile<BLK>(st, sa, vbuf[n & 1], full, c, lane, NT, T);
+      if constexpr (NBUF == 1) {
+        wait_tile_copies();
+        __syncthreads();
+      }
+      finish_tile<BLK>(st, sa, vbuf[bi(n)], full, c, lane, NT, T);
     }
   }
+  wait_tile_copies();
 
   store_rows(st, o + b * so_b + h * so_h, so_t, qrow, T, half);
 }
@@ -231,12 +276,12 @@ extern "C" int solattn_fwd_bf16(const uint16_t* q, int64_t sq_b, int64_t sq_t, i
   const uint32_t grid = static_cast<uint32_t>(B * H * NT);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (block == 128) {
-    hipLaunchKernelGGL(bf16fwd::fwd_bf16_kernel<128>, dim3(grid), dim3(256), 0, s,
+    hipLaunchKernelGGL((bf16fwd::fwd_bf16_kernel<128, 2>), dim3(grid), dim3(256), 0, s,
                        q, sq_b, sq_t, sq_h, k, sk_b, sk_t, sk_h, v, sv_b, sv_t, sv_h, kc, vc, npad,
                        counts, lists, mask, static_cast<int>(T), static_cast<int>(H),
                        static_cast<int>(NT), W, c, o, so_b, so_t, so_h);
   } else {
-    hipLaunchKernelGGL(bf16fwd::fwd_bf16_kernel<64>, dim3(grid), dim3(128), 0, s, q,
+    hipLaunchKernelGGL((bf16fwd::fwd_bf16_kernel<64, 1>), dim3(grid), dim3(128), 0, s, q,
                        sq_b, sq_t, sq_h, k, sk_b, sk_t, sk_h, v, sv_b, sv_t, sv_h, kc, vc, npad,
                        counts, lists, mask, static_cast<int>(T), static_cast<int>(H),
                        static_cast<int>(NT), W, c, o, so_b, so_t, so_h);
