@@ -178,10 +178,12 @@ __device__ __forceinline__ void exact_softmax_pv(SoftmaxState& st, f32x16 (&s)[2
 // Pipelined step over full exact tile n (scaled scores in sc): the i8 MFMAs
 // of S(n+1) from the K tile kn are interleaved with the softmax of tile n;
 // then P(n).V(n) and the conversion of S(n+1) into sn (ks of tile n+1 from kn).
-template <bool INT8_PV>
+// With EARLY the conversion of S(n+1) runs before `mid` (a single K buffer is
+// refilled there); otherwise `mid` is empty and the conversion comes last.
+template <bool INT8_PV, bool EARLY, typename Mid>
 __device__ __forceinline__ void fast_step(SoftmaxState& st, f32x16 (&sc)[2], f32x16 (&sn)[2],
                                           const char* kn, const void* vt, const i32x4 (&qi)[4],
-                                          float qsl, int lane) {
+                                          float qsl, int lane, Mid&& mid) {
   const int col = lane & 31, half = lane >> 5;
   const i32x16 zero = {};
   i32x16 si[2];
@@ -231,7 +233,12 @@ __device__ __forceinline__ void fast_step(SoftmaxState& st, f32x16 (&sc)[2], f32
     st.l = fmaf(st.l, alpha, psum);
   }
   rescale(st, alpha);
-  if constexpr (INT8_PV) {
+  if constexpr (EARLY) {
+    scale_scores(kn, si, half, sn);
+    mid();
+    if constexpr (INT8_PV) pv_i8(static_cast<const char*>(vt), pi, beta * (1.f / 127.f), lane, st.acc);
+    else pv_tile(static_cast<const uint16_t*>(vt), pb, lane, st.acc);
+  } else if constexpr (INT8_PV) {
     scale_scores(kn, si, half, sn);  // frees the int32 scores before the P.V accumulators
     pv_i8(static_cast<const char*>(vt), pi, beta * (1.f / 127.f), lane, st.acc);
   } else {
@@ -304,8 +311,15 @@ __device__ __forceinline__ void issue_i8(char* dst, const int8_t* rows, const I8
   }
 }
 
-template <int BLK, bool INT8_PV>
-__global__ void __launch_bounds__(BLK * 2, 2)
+// NBUF = 2: double-buffered tiles (68 KB of LDS), two workgroups per CU: two
+// waves per SIMD at block 128, one (512 registers) at block 64. NBUF = 1
+// (block 64 with INT8 P.V): single-buffered, four workgroups and two waves per
+// SIMD, two waits per pipeline step. Block 64 with BF16 P.V stays
+// double-buffered: its single-buffered form spills in the step loop and ran
+// 1.5x slower.
+template <int BLK, bool INT8_PV, int NBUF>
+__global__ void __launch_bounds__(BLK * 2)
+__attribute__((amdgpu_waves_per_eu(BLK == 64 && NBUF == 2 ? 1 : 2)))
 fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
                 const int8_t* __restrict__ qi, const float* __restrict__ qs,
                 const int8_t* __restrict__ ki, const float* __restrict__ ks,
@@ -316,9 +330,10 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
                 const uint32_t* __restrict__ mask, int T, int H, int NT, int W, float c,
                 uint16_t* __restrict__ o, int64_t so_b, int64_t so_t, int64_t so_h) {
   constexpr int NTHREADS = BLK * 2;
-  __shared__ __align__(16) uint16_t kbuf[2][kTileElems];
-  __shared__ __align__(16) uint16_t vbuf[2][kTileElems];
+  __shared__ __align__(16) uint16_t kbuf[NBUF][kTileElems];
+  __shared__ __align__(16) uint16_t vbuf[NBUF][kTileElems];
   __shared__ TileList tl;
+  const auto bi = [](int n) { return NBUF == 2 ? (n & 1) : 0; };  // buffer of tile n
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int col = lane & 31, half = lane >> 5;
@@ -405,7 +420,9 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
     if (nrag) {
       wait_tile_copies();
       __syncthreads();
-      if (1 < ntiles) issue_tile(1, 1);
+      if constexpr (NBUF == 2) {
+        if (1 < ntiles) issue_tile(1, 1);
+      }
       const TileDesc td = exact_tile(0);
       i32x16 si[2];
       f32x16 s[2];
@@ -421,34 +438,62 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
       }
       exact_softmax_pv<INT8_PV>(st, s, vbuf[0], qsl, lane);
       __syncthreads();
+      if constexpr (NBUF == 1) {
+        if (1 < ntiles) issue_tile(1, 0);
+      }
     }
-    // full exact tiles, pipelined (tile F = nrag was issued into buffers F & 1)
+    // full exact tiles, pipelined (tile F = nrag was issued into buffers bi(F))
     const int F = nrag;
     if (nfast > 0) {
       const int E = nexact;  // one past the last full exact tile
-      wait_tile_copies();
-      __syncthreads();
-      if (F + 1 < E)
-        issue_exact_full(F + 1, reinterpret_cast<char*>(kbuf[(F + 1) & 1]), nullptr, true, false);
       f32x16 sa[2], sb[2];
-      {
+      const auto qk_scaled = [&](const uint16_t* kb, f32x16 (&s)[2]) {
         i32x16 si[2];
-        const char* kt = reinterpret_cast<const char*>(kbuf[F & 1]);
+        const char* kt = reinterpret_cast<const char*>(kb);
         qk_i8_tile(kt, qireg, col, half, si);
-        scale_scores(kt, si, half, sa);
+        scale_scores(kt, si, half, s);
+      };
+      if constexpr (NBUF == 2) {
+        wait_tile_copies();
+        __syncthreads();
+        if (F + 1 < E)
+          issue_exact_full(F + 1, reinterpret_cast<char*>(kbuf[(F + 1) & 1]), nullptr, true, false);
+        qk_scaled(kbuf[F & 1], sa);
+        wait_tile_copies();
+        __syncthreads();  // kbuf[F & 1] is refilled (K of tile F+2) by the first step
+      } else {
+        wait_tile_copies();
+        __syncthreads();
+        qk_scaled(kbuf[0], sa);
+        __syncthreads();  // kbuf is free
+        if (F + 1 < E) issue_exact_full(F + 1, reinterpret_cast<char*>(kbuf[0]), nullptr, true, false);
+        wait_tile_copies();
+        __syncthreads();  // K(F+1) and V(F) in LDS
       }
-      wait_tile_copies();
-      __syncthreads();  // kbuf[F & 1] is refilled (K of tile F+2) by the first step
       int n = F;
       // Step n needs n + 1 < E. K(n+2) of the last step is clamped to the
       // last full tile: a redundant copy into a buffer nothing reads afterwards.
       const auto step = [&](f32x16 (&sc)[2], f32x16 (&sn)[2]) {
-        issue_exact_full(min(n + 2, E - 1), reinterpret_cast<char*>(kbuf[n & 1]), nullptr, true, false);
-        issue_exact_full(n + 1, nullptr, vbuf[(n + 1) & 1], false, true);
-        fast_step<INT8_PV>(st, sc, sn, reinterpret_cast<const char*>(kbuf[(n + 1) & 1]), vbuf[n & 1],
-                           qireg, qsl, lane);
-        wait_tile_copies();
-        __syncthreads();
+        if constexpr (NBUF == 2) {
+          issue_exact_full(min(n + 2, E - 1), reinterpret_cast<char*>(kbuf[n & 1]), nullptr, true, false);
+          issue_exact_full(n + 1, nullptr, vbuf[(n + 1) & 1], false, true);
+          fast_step<INT8_PV, false>(st, sc, sn, reinterpret_cast<const char*>(kbuf[(n + 1) & 1]),
+                                    vbuf[n & 1], qireg, qsl, lane, [] {});
+          wait_tile_copies();
+          __syncthreads();
+        } else {
+          // On entry kbuf holds K(n+1), vbuf V(n) (copy possibly in flight).
+          fast_step<INT8_PV, true>(st, sc, sn, reinterpret_cast<const char*>(kbuf[0]), vbuf[0], qireg,
+                                   qsl, lane, [&] {
+                                     wait_tile_copies();  // V(n)
+                                     __syncthreads();     // every wave is done with K(n+1), ks(n+1)
+                                     issue_exact_full(min(n + 2, E - 1), reinterpret_cast<char*>(kbuf[0]),
+                                                      nullptr, true, false);
+                                   });
+          wait_tile_copies();  // K(n+2)
+          __syncthreads();     // every wave is done with V(n)
+          issue_exact_full(n + 1, nullptr, vbuf[0], false, true);
+        }
         ++n;
       };
       while (n + 2 < E) {
@@ -457,9 +502,17 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
       }
       if (n + 1 < E) {
         step(sa, sb);
-        exact_softmax_pv<INT8_PV>(st, sb, vbuf[n & 1], qsl, lane);
+        if constexpr (NBUF == 1) {
+          wait_tile_copies();
+          __syncthreads();
+        }
+        exact_softmax_pv<INT8_PV>(st, sb, vbuf[bi(n)], qsl, lane);
       } else {
-        exact_softmax_pv<INT8_PV>(st, sa, vbuf[n & 1], qsl, lane);
+        if constexpr (NBUF == 1) {
+          wait_tile_copies();
+          __syncthreads();
+        }
+        exact_softmax_pv<INT8_PV>(st, sa, vbuf[bi(n)], qsl, lane);
       }
       __syncthreads();
     }
@@ -486,15 +539,20 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
       if (qvalid) r = *reinterpret_cast<const uint4*>(qp + cc * 16);
       qreg[cc] = __builtin_bit_cast(bf16x8, r);
     }
-    if (nexact > 0) issue_tile(nexact, nexact & 1);  // every earlier copy has landed
+    if (nexact > 0) issue_tile(nexact, bi(nexact));  // every earlier copy has landed
     for (int n = nexact; n < ntiles; ++n) {
       wait_tile_copies();  // tile n: the only copies in flight
       __syncthreads();
-      if (n + 1 < ntiles) issue_tile(n + 1, (n + 1) & 1);
+      if constexpr (NBUF == 2) {
+        if (n + 1 < ntiles) issue_tile(n + 1, (n + 1) & 1);
+      }
       f32x16 s[2];
-      qk_tile(kbuf[n & 1], qreg, col, half, s);
-      finish_tile<BLK>(st, s, vbuf[n & 1], pooled_desc(tl, n - nexact, NT), c, lane, NT, T);
+      qk_tile(kbuf[bi(n)], qreg, col, half, s);
+      finish_tile<BLK>(st, s, vbuf[bi(n)], pooled_desc(tl, n - nexact, NT), c, lane, NT, T);
       __syncthreads();
+      if constexpr (NBUF == 1) {
+        if (n + 1 < ntiles) issue_tile(n + 1, 0);
+      }
     }
   }
   wait_tile_copies();
@@ -509,7 +567,7 @@ void launch_i8(uint32_t grid, hipStream_t s, const uint16_t* q, int64_t sq_b, in
                int64_t npad, const int32_t* counts, const int16_t* lists, const uint32_t* mask,
                int T, int H, int NT, int W, float c, uint16_t* o, int64_t so_b, int64_t so_t,
                int64_t so_h) {
-  hipLaunchKernelGGL((fwd_int8_kernel<BLK, PV>), dim3(grid), dim3(BLK * 2), 0, s, q, sq_b, sq_t,
+  hipLaunchKernelGGL((fwd_int8_kernel<BLK, PV, (BLK == 64 && PV) ? 1 : 2>), dim3(grid), dim3(BLK * 2), 0, s, q, sq_b, sq_t,
                      sq_h, qi, qs, ki, ks, vi, vscale, v, sv_b, sv_t, sv_h, TP, kc, vc, npad,
                      counts, lists, mask, T, H, NT, W, c, o, so_b, so_t, so_h);
 }
