@@ -333,7 +333,8 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                      "traffic": _traffic() if (args.config, block, H) == (2, 128, 24) else None,
-                     "kernel": f"bf16fwd::fwd_bf16_kernel<{block}>",
+                     "kernel": ("bf16fwd::fwd_bf16_kernel<128>" if block == 128
+                                else "bf16fwd::fwd_bf16_sbuf_kernel<64>"),
                      "algorithmic_flops_per_launch": rflops, "launch_ms": round(fwd_ms, 4)},
         "routed_density": round(density, 4),
         "prep_ms": round(prep_ms, 4),

@@ -76,6 +76,61 @@ __device__ __forceinline__ void fast_step(SoftmaxState& st, f32x16 (&sc)[2], f32
   pv_tile(vt, pb, lane, st.acc);
 }
 
+// Three-stage step: S(n+1) = K(n+1) Q^T, O += P(n-1) V(n-1) and the softmax of
+// S(n) -> P(n) share one instruction stream, so the softmax's VALU work
+// overlaps 32 MFMAs instead of 16. O is rescaled to the new running max after
+// the P(n-1) V(n-1) products; P(n) V(n) is left to the next step. QK = false
+// drops the score product (last tile), PV = false the value product (first).
+// Register budget: the softmax turns S(n) into P(n) during the first half,
+// while only the keys 0-31 half of S(n+1) accumulates; keys 32-63 start after
+// S(n) is dead. kl, vl: this lane's operand addresses (k_lane, v_lane) in
+// K(n+1) and V(n-1).
+template <bool QK, bool PV>
+__device__ __forceinline__ void step3(SoftmaxState& st, const f32x16 (&sc)[2], f32x16 (&sn)[2],
+                                      const bf16x8 (&pp)[4], bf16x8 (&pn)[4], uint32_t kl,
+                                      uint32_t vl, const bf16x8 (&q)[8], float c) {
+  const f32x16 zero = {};
+  constexpr int LK = 2, LV = 2;
+  bf16x8 ka[16], va[16];
+  if constexpr (QK) {
+#pragma unroll
+    for (int i = 0; i < LK; ++i) ka[i] = k_op_x(kl, i >> 3, i & 7);
+  }
+  if constexpr (PV) {
+#pragma unroll
+    for (int i = 0; i < LV; ++i) va[i] = v_op_x(vl, i >> 2, i & 3);
+  }
+  float mx = -INFINITY, alpha = 1.f, neg = 0.f, psum = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    if constexpr (QK) {
+      if (i + LK < 16) ka[i + LK] = k_op_x(kl, (i + LK) >> 3, (i + LK) & 7);
+      sn[i >> 3] = mfma_bf16(ka[i], q[i & 7], (i & 7) == 0 ? zero : sn[i >> 3]);
+    }
+    if constexpr (PV) {
+      if (i + LV < 16) va[i + LV] = v_op_x(vl, (i + LV) >> 2, (i + LV) & 3);
+      st.acc[i & 3] = mfma_bf16(va[i], pp[i >> 2], st.acc[i & 3]);
+    }
+    if (i < 4) {
+#pragma unroll
+      for (int r = 0; r < 8; ++r) mx = fmaxf(mx, sc[i >> 1][8 * (i & 1) + r]);
+      if (i == 3) {
+        st.m = new_max(st.m, xhalf_max(mx) * c, alpha);
+        neg = -st.m;
+      }
+    } else if (i < 8) {
+      // P(n) chunk i - 4; the empty asm keeps the exps in this slot (left
+      // alone, the compiler sinks them to P(n)'s first use in the next step
+      // and S(n) stays live through this one).
+      const int k = i - 4;
+      psum = k & 1 ? exp8<8>(sc[k >> 1], c, neg, pn[k], psum) : exp8<0>(sc[k >> 1], c, neg, pn[k], psum);
+      asm volatile("" : "+v"(pn[k]), "+v"(psum));
+    }
+  }
+  st.l = fmaf(st.l, alpha, psum);
+  rescale(st, alpha);
+}
+
 // Tile n of this kernel's order: pooled tiles, the ragged exact tile (if
 // any), then the full exact tiles in ascending key order.
 template <int BLK>
@@ -85,12 +140,13 @@ __device__ __forceinline__ TileDesc desc(const TileList& tl, int n, int nrag, in
   return exact_desc<BLK>(tl, n - tl.npool - nrag, T, NT);
 }
 
-// NBUF = 2: K and V tiles double buffered (64 KiB), two workgroups per CU.
-// NBUF = 1: single buffered (32 KiB), four workgroups per CU; the pipeline
-// step then waits twice (K refilled after the QK phase, V after P.V).
-template <int BLK, int NBUF>
+// Block 64 forward (workgroups of 2 waves). K and V are single buffered
+// (32 KiB), so four workgroups and two waves per SIMD fit a CU; the pipeline
+// step waits twice (K refilled after the QK phase, V after P.V). Tile order:
+// pooled tiles, the ragged exact tile (if any), then the full exact tiles.
+template <int BLK>
 __global__ void __launch_bounds__(BLK * 2) __attribute__((amdgpu_waves_per_eu(2)))
-fwd_bf16_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
+fwd_bf16_sbuf_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
                 const uint16_t* __restrict__ k, int64_t sk_b, int64_t sk_t, int64_t sk_h,
                 const uint16_t* __restrict__ v, int64_t sv_b, int64_t sv_t, int64_t sv_h,
                 const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc, int64_t npad,
@@ -98,11 +154,9 @@ fwd_bf16_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
                 const uint32_t* __restrict__ mask, int T, int H, int NT, int W, float c,
                 uint16_t* __restrict__ o, int64_t so_b, int64_t so_t, int64_t so_h) {
   constexpr int NTHREADS = BLK * 2;
-  constexpr int kCopiesPerTile = 2 * CopyOffsets<NTHREADS>::U;
-  __shared__ __align__(16) uint16_t kbuf[NBUF][kTileElems];
-  __shared__ __align__(16) uint16_t vbuf[NBUF][kTileElems];
+  __shared__ __align__(16) uint16_t kbuf[kTileElems];
+  __shared__ __align__(16) uint16_t vbuf[kTileElems];
   __shared__ TileList tl;
-  const auto bi = [](int n) { return NBUF == 2 ? (n & 1) : 0; };  // buffer of tile n
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int col = lane & 31, half = lane >> 5;
@@ -123,25 +177,26 @@ fwd_bf16_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
                      static_cast<int64_t>(H) * kD, vc + (static_cast<int64_t>(b) * npad * H + h) * kD};
   CopyOffsets<NTHREADS> off;
   off.init(sk_t, sv_t);
-  const auto issue_k = [&](int n, int buf) {
+  const uint32_t kb = lds_addr(kbuf), vb = lds_addr(vbuf);  // LDS byte addresses
+  const auto issue_k = [&](int n) {
     const int first = exact_first<BLK>(tl, n - nplain);
-    issue_full<NTHREADS>(kbuf[buf], src.k + static_cast<int64_t>(first) * src.sk, src.sk, off.k);
+    issue_full<NTHREADS>(kb, src.k + static_cast<int64_t>(first) * src.sk, src.sk, off.k);
   };
-  const auto issue_v = [&](int n, int buf) {
+  const auto issue_v = [&](int n) {
     const int first = exact_first<BLK>(tl, n - nplain);
-    issue_full<NTHREADS>(vbuf[buf], src.v + static_cast<int64_t>(first) * src.sv, src.sv, off.v);
+    issue_full<NTHREADS>(vb, src.v + static_cast<int64_t>(first) * src.sv, src.sv, off.v);
   };
-  const auto issue_tile = [&](int n, int buf) {
+  const auto issue_tile = [&](int n) {
     if (n >= nplain) {
-      issue_k(n, buf);
-      issue_v(n, buf);
+      issue_k(n);
+      issue_v(n);
     } else {
       const TileDesc td = desc<BLK>(tl, n, nrag, T, NT);
-      issue_generic<NTHREADS>(kbuf[buf], 0, td, src);
-      issue_generic<NTHREADS>(vbuf[buf], 1, td, src);
+      issue_generic<NTHREADS>(kb, 0, td, src);
+      issue_generic<NTHREADS>(vb, 1, td, src);
     }
   };
-  issue_tile(0, 0);
+  issue_tile(0);
 
   // This wave's 32 query rows as the B operand of S^T = K Q^T.
   const int qrow = qb * BLK + wave * 32 + col;
@@ -161,69 +216,40 @@ fwd_bf16_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
 
   // ---- plain tiles (pooled, ragged)
   for (int n = 0; n < nplain; ++n) {
-    if constexpr (NBUF == 2) {
-      // tile n+1 is copied while tile n computes
-      if (n + 1 < ntiles) {
-        issue_tile(n + 1, (n + 1) & 1);
-        wait_vmcnt<kCopiesPerTile>();  // tile n landed; tile n+1 stays in flight
-      } else {
-        wait_tile_copies();
-      }
-    } else {
-      wait_tile_copies();
-    }
+    wait_tile_copies();
     __syncthreads();
     f32x16 s[2];
-    qk_tile(kbuf[bi(n)], qreg, col, half, s);
-    finish_tile<BLK>(st, s, vbuf[bi(n)], desc<BLK>(tl, n, nrag, T, NT), c, lane, NT, T);
+    qk_tile(kbuf, qreg, col, half, s);
+    finish_tile<BLK>(st, s, vbuf, desc<BLK>(tl, n, nrag, T, NT), c, lane, NT, T);
     __syncthreads();
-    if constexpr (NBUF == 1) {
-      if (n + 1 < ntiles) issue_tile(n + 1, 0);
-    }
+    if (n + 1 < ntiles) issue_tile(n + 1);
   }
 
-  // ---- full exact tiles, pipelined; tile F was issued into buffers bi(F).
-  // K(n+2) past the last tile is clamped to it: a redundant copy into a
-  // buffer that nothing reads afterwards, which keeps the loop free of branches.
+  // ---- full exact tiles, pipelined; tile F was issued. K(n+2) past the last
+  // tile is clamped to it: a redundant copy that nothing reads afterwards,
+  // which keeps the loop free of branches.
   const int F = nplain;
   if (F < ntiles) {
     f32x16 sa[2], sb[2];
     int n = F;
-    if constexpr (NBUF == 2) {
-      wait_tile_copies();
-      __syncthreads();
-      if (F + 1 < ntiles) issue_k(F + 1, (F + 1) & 1);
-      qk_tile(kbuf[F & 1], qreg, col, half, sa);
-      wait_tile_copies();
-      __syncthreads();  // kbuf[F & 1] is refilled (K of tile F+2) by the first step
-    } else {
-      wait_tile_copies();
-      __syncthreads();
-      qk_tile(kbuf[0], qreg, col, half, sa);
-      __syncthreads();  // kbuf is free
-      if (F + 1 < ntiles) issue_k(F + 1, 0);
-      wait_tile_copies();
-      __syncthreads();  // K(F+1) and V(F) in LDS
-    }
-    // Step n computes S(n+1) and needs n + 1 < ntiles.
+    wait_tile_copies();
+    __syncthreads();
+    qk_tile(kbuf, qreg, col, half, sa);
+    __syncthreads();  // kbuf is free
+    if (F + 1 < ntiles) issue_k(F + 1);
+    wait_tile_copies();
+    __syncthreads();  // K(F+1) and V(F) in LDS
+    // Step n computes S(n+1) and needs n + 1 < ntiles. On entry kbuf holds
+    // K(n+1), vbuf V(n) (copy possibly in flight).
     const auto step = [&](f32x16 (&sc)[2], f32x16 (&sn)[2]) {
-      if constexpr (NBUF == 2) {
-        issue_k(min(n + 2, ntiles - 1), n & 1);
-        issue_v(n + 1, (n + 1) & 1);
-        fast_step(st, sc, sn, kbuf[(n + 1) & 1], vbuf[n & 1], qreg, c, lane, [] {});
-        wait_tile_copies();
-        __syncthreads();
-      } else {
-        // On entry kbuf holds K(n+1), vbuf V(n) (copy possibly in flight).
-        fast_step(st, sc, sn, kbuf[0], vbuf[0], qreg, c, lane, [&] {
-          wait_tile_copies();  // V(n)
-          __syncthreads();     // every wave is done with K(n+1)
-          issue_k(min(n + 2, ntiles - 1), 0);
-        });
-        wait_tile_copies();  // K(n+2)
-        __syncthreads();     // every wave is done with V(n)
-        issue_v(n + 1, 0);
-      }
+      fast_step(st, sc, sn, kbuf, vbuf, qreg, c, lane, [&] {
+        wait_tile_copies();  // V(n)
+        __syncthreads();     // every wave is done with K(n+1)
+        issue_k(min(n + 2, ntiles - 1));
+      });
+      wait_tile_copies();  // K(n+2)
+      __syncthreads();     // every wave is done with V(n)
+      issue_v(n + 1);
       ++n;
     };
     // Pairs of steps, so the S buffers swap roles without register copies.
@@ -234,18 +260,187 @@ fwd_bf16_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
     const TileDesc full{0, 0, kKeys, ~0ull};
     if (n + 1 < ntiles) {
       step(sa, sb);
-      if constexpr (NBUF == 1) {
-        wait_tile_copies();
-        __syncthreads();
-      }
-      finish_tile<BLK>(st, sb, vbuf[bi(n)], full, c, lane, NT, T);
+      wait_tile_copies();
+      __syncthreads();
+      finish_tile<BLK>(st, sb, vbuf, full, c, lane, NT, T);
     } else {
-      if constexpr (NBUF == 1) {
+      wait_tile_copies();
+      __syncthreads();
+      finish_tile<BLK>(st, sa, vbuf, full, c, lane, NT, T);
+    }
+  }
+  wait_tile_copies();
+
+  store_rows(st, o + b * so_b + h * so_h, so_t, qrow, T, half);
+}
+
+// Block 128 forward with the three-stage pipeline. Tile order: the full
+// exact tiles first (list tiles 0 .. nfast-1, ascending keys), then the
+// ragged exact tile (if any) and the pooled tiles. K and V are double
+// buffered (64 KiB, two workgroups per CU). The full exact phase runs first
+// so that the plain phase's registers are not live across its loop.
+template <int BLK>
+__global__ void __launch_bounds__(BLK * 2) __attribute__((amdgpu_waves_per_eu(2)))
+fwd_bf16_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
+                     const uint16_t* __restrict__ k, int64_t sk_b, int64_t sk_t, int64_t sk_h,
+                     const uint16_t* __restrict__ v, int64_t sv_b, int64_t sv_t, int64_t sv_h,
+                     const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc, int64_t npad,
+                     const int32_t* __restrict__ counts, const int16_t* __restrict__ lists,
+                     const uint32_t* __restrict__ mask, int T, int H, int NT, int W, float c,
+                     uint16_t* __restrict__ o, int64_t so_b, int64_t so_t, int64_t so_h) {
+  constexpr int NTHREADS = BLK * 2;
+  constexpr int kCopiesPerTile = 2 * CopyOffsets<NTHREADS>::U;
+  __shared__ __align__(256) uint16_t kbuf[2][kTileElems];
+  __shared__ __align__(256) uint16_t vbuf[2][kTileElems];
+  __shared__ TileList tl;
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int col = lane & 31, half = lane >> 5;
+  int bh, qb;
+  tile_coords(blockIdx.x, gridDim.x, NT, bh, qb);
+  const int b = bh / H, h = bh % H;
+  const int64_t row = static_cast<int64_t>(bh) * NT + qb;
+
+  const int ntiles = build_tile_list<BLK>(tl, counts, lists, mask, row, NT, W, T);
+  if (ntiles == 0) return;  // cannot happen for routed lists: the diagonal is exact
+  const int nrag = ragged_tiles(tl, counts, row, NT, T);
+  const int nplain = tl.npool + nrag;
+  const int nfast = ntiles - nplain;  // full exact tiles: list tiles 0 .. nfast-1
+
+  const KVSource src{k + b * sk_b + h * sk_h, sk_t, v + b * sv_b + h * sv_h, sv_t,
+                     kc + (static_cast<int64_t>(b) * npad * H + h) * kD,
+                     static_cast<int64_t>(H) * kD, vc + (static_cast<int64_t>(b) * npad * H + h) * kD};
+  CopyOffsets<NTHREADS> off;
+  off.init(sk_t, sv_t);
+  const uint32_t kb = lds_addr(kbuf[0]), vb = lds_addr(vbuf[0]);  // LDS byte addresses
+  const auto issue_k = [&](int e, int buf) {
+    const int first = exact_first<BLK>(tl, e);
+    issue_full<NTHREADS>(kb + buf * kTileBytes, src.k + static_cast<int64_t>(first) * src.sk, src.sk, off.k);
+  };
+  const auto issue_v = [&](int e, int buf) {
+    const int first = exact_first<BLK>(tl, e);
+    issue_full<NTHREADS>(vb + buf * kTileBytes, src.v + static_cast<int64_t>(first) * src.sv, src.sv, off.v);
+  };
+  // Plain tile p: the ragged exact tile (p < nrag), then the pooled tiles.
+  const auto plain_desc = [&](int p) {
+    return p < nrag ? exact_desc<BLK>(tl, tl.nexact - 1, T, NT) : pooled_desc(tl, p - nrag, NT);
+  };
+  const auto issue_plain_k = [&](int p, int buf) {
+    issue_generic<NTHREADS>(kb + buf * kTileBytes, 0, plain_desc(p), src);
+  };
+  const auto issue_plain_v = [&](int p, int buf) {
+    issue_generic<NTHREADS>(vb + buf * kTileBytes, 1, plain_desc(p), src);
+  };
+  if (nfast > 0) {
+    issue_k(0, 0);
+    issue_v(0, 0);
+    if (nfast > 1) issue_k(1, 1);
+  } else {
+    issue_plain_k(0, 0);
+    issue_plain_v(0, 0);
+  }
+
+  // This wave's 32 query rows as the B operand of S^T = K Q^T.
+  const int qrow = qb * BLK + wave * 32 + col;
+  bf16x8 qreg[8];
+  {
+    const uint16_t* qp = q + b * sq_b + static_cast<int64_t>(qrow) * sq_t + h * sq_h + half * 8;
+#pragma unroll
+    for (int cc = 0; cc < 8; ++cc) {
+      uint4 r = make_uint4(0u, 0u, 0u, 0u);
+      if (qrow < T) r = *reinterpret_cast<const uint4*>(qp + cc * 16);
+      qreg[cc] = __builtin_bit_cast(bf16x8, r);
+    }
+  }
+
+  SoftmaxState st;
+  st.init();
+  const TileDesc full{0, 0, kKeys, ~0ull};
+  int pbuf = 0;  // buffer of plain tile 0
+
+  // ---- full exact tiles. On entry to step n (0 < n < nfast): S(n) and
+  // P(n-1) in registers, K(n+1) and V(n-1) in LDS; the step copies K(n+2)
+  // over K(n) and V(n) over V(n-2). K(n+2) past the last tile is clamped to
+  // it: a redundant copy into a buffer nothing reads afterwards.
+  if (nfast > 0) {
+    f32x16 sa[2], sb[2];
+    wait_tile_copies();
+    __syncthreads();
+    qk_tile(kbuf[0], qreg, col, half, sa);
+    __syncthreads();  // every wave is done with K(0)
+    if (nfast == 1) {
+      finish_tile<BLK>(st, sa, vbuf[0], full, c, lane, NT, T);
+      __syncthreads();
+      if (nplain > 0) {
+        issue_plain_k(0, 0);
+        issue_plain_v(0, 0);
+      }
+    } else {
+      const int E = nfast;
+      const uint32_t kl0 = k_lane(kb, col, half);
+      const uint32_t vl0 = v_lane(vb, lane);
+      bf16x8 pa[4], pb[4];
+      issue_k(min(2, E - 1), 0);
+      step3<true, false>(st, sa, sb, pb, pa, kl0 + kTileBytes, 0u, qreg, c);
+      wait_tile_copies();
+      __syncthreads();
+      int n = 1;  // S(n) in sb, P(n-1) in pa
+      const auto gstep = [&](const f32x16 (&sc)[2], f32x16 (&sn)[2], const bf16x8 (&pp)[4],
+                             bf16x8 (&pn)[4]) {
+        issue_k(min(n + 2, E - 1), n & 1);
+        issue_v(n, n & 1);
+        step3<true, true>(st, sc, sn, pp, pn, kl0 + ((n + 1) & 1) * kTileBytes,
+                          vl0 + ((n - 1) & 1) * kTileBytes, qreg, c);
         wait_tile_copies();
         __syncthreads();
+        ++n;
+      };
+      // Last tile n = E-1: no K left. Plain tile 0 is copied into the buffers
+      // of tile n-1 while P(n-1) V(n-1), the softmax of S(n) and P(n) V(n) run.
+      const auto last = [&](const f32x16 (&sc)[2], f32x16 (&dummy)[2], const bf16x8 (&pp)[4],
+                            bf16x8 (&pn)[4]) {
+        pbuf = (n - 1) & 1;
+        issue_v(n, n & 1);
+        if (nplain > 0) issue_plain_k(0, pbuf);
+        step3<false, true>(st, sc, dummy, pp, pn, 0u, vl0 + pbuf * kTileBytes, qreg, c);
+        if (nplain > 0)
+          wait_vmcnt<kCopiesPerTile / 2>();  // V(n) landed; plain K(0) may be in flight
+        else
+          wait_tile_copies();
+        __syncthreads();  // every wave is done with V(n-1)
+        if (nplain > 0) issue_plain_v(0, pbuf);
+        pv_tile(vbuf[n & 1], pn, lane, st.acc);
+      };
+      // Pairs of steps, so the S and P buffers swap roles without copies.
+      while (n + 2 < E) {
+        gstep(sb, sa, pa, pb);
+        gstep(sa, sb, pb, pa);
       }
-      finish_tile<BLK>(st, sa, vbuf[bi(n)], full, c, lane, NT, T);
+      if (n + 1 < E) {
+        gstep(sb, sa, pa, pb);
+        last(sa, sb, pb, pa);
+      } else {
+        last(sb, sa, pa, pb);
+      }
+      __syncthreads();  // every wave is done with V(E-1) before plain tile 1 lands there
     }
+  }
+
+  // ---- ragged and pooled tiles; plain tile p sits in buffers (pbuf + p) & 1
+  for (int p = 0; p < nplain; ++p) {
+    const int cur = (pbuf + p) & 1;
+    if (p + 1 < nplain) {
+      issue_plain_k(p + 1, cur ^ 1);
+      issue_plain_v(p + 1, cur ^ 1);
+      wait_vmcnt<kCopiesPerTile>();  // tile p landed; tile p+1 stays in flight
+    } else {
+      wait_tile_copies();
+    }
+    __syncthreads();
+    f32x16 s[2];
+    qk_tile(kbuf[cur], qreg, col, half, s);
+    finish_tile<BLK>(st, s, vbuf[cur], plain_desc(p), c, lane, NT, T);
+    __syncthreads();
   }
   wait_tile_copies();
 
@@ -276,12 +471,12 @@ extern "C" int solattn_fwd_bf16(const uint16_t* q, int64_t sq_b, int64_t sq_t, i
   const uint32_t grid = static_cast<uint32_t>(B * H * NT);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (block == 128) {
-    hipLaunchKernelGGL((bf16fwd::fwd_bf16_kernel<128, 2>), dim3(grid), dim3(256), 0, s,
+    hipLaunchKernelGGL((bf16fwd::fwd_bf16_kernel<128>), dim3(grid), dim3(256), 0, s,
                        q, sq_b, sq_t, sq_h, k, sk_b, sk_t, sk_h, v, sv_b, sv_t, sv_h, kc, vc, npad,
                        counts, lists, mask, static_cast<int>(T), static_cast<int>(H),
                        static_cast<int>(NT), W, c, o, so_b, so_t, so_h);
   } else {
-    hipLaunchKernelGGL((bf16fwd::fwd_bf16_kernel<64, 1>), dim3(grid), dim3(128), 0, s, q,
+    hipLaunchKernelGGL((bf16fwd::fwd_bf16_sbuf_kernel<64>), dim3(grid), dim3(128), 0, s, q,
                        sq_b, sq_t, sq_h, k, sk_b, sk_t, sk_h, v, sv_b, sv_t, sv_h, kc, vc, npad,
                        counts, lists, mask, static_cast<int>(T), static_cast<int>(H),
                        static_cast<int>(NT), W, c, o, so_b, so_t, so_h);

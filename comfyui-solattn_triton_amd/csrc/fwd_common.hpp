@@ -139,33 +139,40 @@ __device__ __forceinline__ int exact_first(const TileList& tl, int e) {
 //   V: physical chunk = chunk ^ 4*(row & 3): a ds_read_b64_tr_b16 serves 32
 //      lanes = 4 rows x 4 consecutive chunks per cycle, all distinct.
 constexpr int kTileElems = kKeys * kD;  // one K or V tile in LDS (16 KiB)
+constexpr uint32_t kTileBytes = kTileElems * 2;
 
 __device__ __forceinline__ int swz_k(int row, int chunk) { return chunk ^ (row & 15); }
 __device__ __forceinline__ int swz_v(int row, int chunk) { return chunk ^ ((row & 3) << 2); }
 
 // Global -> LDS copies (global_load_lds_*): lane i's bytes land at
-// lds + size * i, lds wave-uniform (M0). They are issued through inline asm so
-// that the compiler does not make later, unrelated LDS reads wait for them;
-// every consumer orders them itself: s_waitcnt vmcnt, then a barrier.
+// lds + size * i, with lds a wave-uniform LDS byte address (M0). They are
+// issued through inline asm so that the compiler does not make later,
+// unrelated LDS reads wait for them; every consumer orders them itself:
+// s_waitcnt vmcnt, then a barrier. Callers convert the LDS pointer once
+// (lds_addr) and add scalar offsets, so the addresses stay in SGPRs.
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return __builtin_amdgcn_readfirstlane(
       static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)p)));
 }
+// This wave's index in the workgroup, as a scalar.
+__device__ __forceinline__ int wave_id() {
+  return __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+}
 // 16 bytes per lane from a per-lane address.
-__device__ __forceinline__ void g2l16(const void* g, void* lds) {
-  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(lds_addr(lds)) : "memory");
+__device__ __forceinline__ void g2l16(const void* g, uint32_t lds) {
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(lds) : "memory");
 }
 // 16 bytes per lane from a wave-uniform base plus a 32-bit lane offset.
-__device__ __forceinline__ void g2l16_s(const void* base, uint32_t off, void* lds) {
-  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds_addr(lds)) : "memory");
+__device__ __forceinline__ void g2l16_s(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
 }
 // 4 bytes per lane from a per-lane address.
-__device__ __forceinline__ void g2l4(const void* g, void* lds) {
-  asm volatile("global_load_lds_dword %0, off" ::"v"(g), "{m0}"(lds_addr(lds)) : "memory");
+__device__ __forceinline__ void g2l4(const void* g, uint32_t lds) {
+  asm volatile("global_load_lds_dword %0, off" ::"v"(g), "{m0}"(lds) : "memory");
 }
 // 4 bytes per lane from a wave-uniform base plus a 32-bit lane offset.
-__device__ __forceinline__ void g2l4_s(const void* base, uint32_t off, void* lds) {
-  asm volatile("global_load_lds_dword %0, %1" ::"v"(off), "s"(base), "{m0}"(lds_addr(lds)) : "memory");
+__device__ __forceinline__ void g2l4_s(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("global_load_lds_dword %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
 }
 
 __device__ __forceinline__ void wait_tile_copies() { __builtin_amdgcn_s_waitcnt(0); }
@@ -181,11 +188,12 @@ __device__ __forceinline__ void wait_vmcnt() {
 // Copy the K (kv == 0) or V (kv == 1) rows of the bf16 tile `td` into an LDS
 // tile, each lane computing its own source rows: rows past nvalid re-read row
 // 0 of the tile (finite data that the softmax masks out). U copies per lane.
+// dst is the tile's LDS byte address.
 template <int NTHREADS>
-__device__ __forceinline__ void issue_generic(uint16_t* dst, int kv, const TileDesc& td,
+__device__ __forceinline__ void issue_generic(uint32_t dst, int kv, const TileDesc& td,
                                               const KVSource& src) {
   constexpr int U = kKeys * 16 / NTHREADS;
-  const int wave_base = threadIdx.x & ~63;
+  const uint32_t l0 = dst + wave_id() * 64 * 16;
   const uint16_t* b = kv == 0 ? (td.pooled ? src.kc : src.k) : (td.pooled ? src.vc : src.v);
   const int64_t stride = td.pooled ? src.skc : (kv == 0 ? src.sk : src.sv);
 #pragma unroll
@@ -194,7 +202,7 @@ __device__ __forceinline__ void issue_generic(uint16_t* dst, int kv, const TileD
     const int row = e >> 4, pc = e & 15;
     const int srow = td.first + (row < td.nvalid ? row : 0);
     const int chunk = kv == 0 ? swz_k(row, pc) : swz_v(row, pc);
-    g2l16(b + static_cast<int64_t>(srow) * stride + chunk * 8, dst + (wave_base + NTHREADS * u) * 8);
+    g2l16(b + static_cast<int64_t>(srow) * stride + chunk * 8, l0 + NTHREADS * u * 16);
   }
 }
 
@@ -219,17 +227,17 @@ struct CopyOffsets {
 };
 
 // Copies of a full bf16 tile whose first row is at `base` (row stride
-// `stride` elements) into LDS tile dst.
+// `stride` elements) into the LDS tile at byte address dst.
 template <int NTHREADS>
-__device__ __forceinline__ void issue_full(uint16_t* dst, const uint16_t* base, int64_t stride,
+__device__ __forceinline__ void issue_full(uint32_t dst, const uint16_t* base, int64_t stride,
                                            const uint32_t (&off)[CopyOffsets<NTHREADS>::P]) {
   using CO = CopyOffsets<NTHREADS>;
-  const int wave_base = static_cast<int>(threadIdx.x) & ~63;
+  const uint32_t l0 = dst + wave_id() * 64 * 16;
   const char* b = reinterpret_cast<const char*>(base);
 #pragma unroll
   for (int u = 0; u < CO::U; ++u) {
     const char* row_base = b + static_cast<int64_t>(u / CO::P) * 16 * stride * 2;
-    g2l16_s(row_base, off[u % CO::P], dst + (wave_base + NTHREADS * u) * 8);
+    g2l16_s(row_base, off[u % CO::P], l0 + NTHREADS * u * 16);
   }
 }
 
@@ -266,6 +274,36 @@ __device__ __forceinline__ bf16x8 v_op(const uint16_t* vt, int ks, int dt, int l
   const bf16x4 lo = tr16(&vt[row0 * kD + swz_v(row0, chunk) * 8 + sub * 4]);
   const bf16x4 hi = tr16(&vt[row1 * kD + swz_v(row1, chunk) * 8 + sub * 4]);
   return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// Operand addressing by XOR. In a 256-byte-aligned K tile the operand (m, cc)
+// of a lane sits at (k_lane ^ (cc << 5)) + m * 8192, because the swizzle
+// c ^ (row & 15) only flips chunk bits that cc's chunk index 2cc + half
+// shares with bits 5-7 of the address. In a V tile the transposed operand
+// (ks, dt) rows row0 / row0 + 8 sit at (v_lane ^ (dt << 6)) + ks * 4096 and
+// 2048 further (swizzle c ^ ((row & 3) << 2) flips address bits 6-7). One
+// lane address per tile replaces one per (cc) or (dt).
+__device__ __forceinline__ uint32_t k_lane(uint32_t tile, int col, int half) {
+  return tile + col * 256 + 16 * (half ^ (col & 15));
+}
+__device__ __forceinline__ uint32_t v_lane(uint32_t tile, int lane) {
+  const int g = lane >> 4, sl = lane & 15;
+  const int row0 = 4 * (g >> 1) + (sl >> 2);
+  const int cp = 2 * (g & 1) + ((sl & 3) >> 1);
+  return tile + row0 * 256 + 64 * (row0 & 3) + 16 * cp + 8 * (sl & 1);
+}
+__device__ __forceinline__ bf16x8 k_op_x(uint32_t kl, int m, int cc) {
+  const uint32_t a = (kl ^ static_cast<uint32_t>(cc << 5)) + m * 8192;
+  return *reinterpret_cast<const __attribute__((address_space(3))) bf16x8*>(static_cast<uintptr_t>(a));
+}
+__device__ __forceinline__ bf16x8 v_op_x(uint32_t vl, int ks, int dt) {
+  typedef short v4i16 __attribute__((ext_vector_type(4)));
+  const uint32_t a = (vl ^ static_cast<uint32_t>(dt << 6)) + ks * 4096;
+  const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      reinterpret_cast<__attribute__((address_space(3))) v4i16*>(static_cast<uintptr_t>(a)));
+  const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      reinterpret_cast<__attribute__((address_space(3))) v4i16*>(static_cast<uintptr_t>(a + 2048)));
+  return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
 __device__ __forceinline__ void qk_tile(const uint16_t* kt, const bf16x8 (&q)[8], int col, int half,

@@ -276,13 +276,14 @@ struct I8Offsets {
 // of ki (or vi) into an LDS tile; with KS also the 64 ks, each wave copying
 // 64 / nwaves of them.
 template <int NTHREADS, bool FULL, bool KS>
-__device__ __forceinline__ void issue_i8(char* dst, const int8_t* rows, const I8Source& is, int first,
+__device__ __forceinline__ void issue_i8(uint32_t dst, const int8_t* rows, const I8Source& is, int first,
                                          int nvalid, uint32_t off, uint32_t ks_off, bool is_v) {
   constexpr int U = I8Offsets<NTHREADS>::U;
-  const int wave_base = static_cast<int>(threadIdx.x) & ~63;
+  const uint32_t l0 = dst;
+  const int wave = wave_id();
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    char* d = dst + (wave_base + NTHREADS * u) * 16;
+    const uint32_t d = l0 + (wave * 64 + NTHREADS * u) * 16;
     if constexpr (FULL) {
       const char* base = reinterpret_cast<const char*>(rows) +
                          static_cast<int64_t>(first + u * (NTHREADS / 8)) * is.srow;
@@ -297,9 +298,9 @@ __device__ __forceinline__ void issue_i8(char* dst, const int8_t* rows, const I8
   }
   if constexpr (KS) {
     constexpr int kpw = I8Offsets<NTHREADS>::kKsPerWave;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int lane = threadIdx.x & 63;
     if (lane < kpw) {
-      char* d = dst + kKsOffset + 4 * kpw * wave;
+      const uint32_t d = l0 + kKsOffset + 4 * kpw * wave;
       if constexpr (FULL) {
         g2l4_s(is.ks + static_cast<int64_t>(first) * is.H, ks_off, d);
       } else {
@@ -330,8 +331,8 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
                 const uint32_t* __restrict__ mask, int T, int H, int NT, int W, float c,
                 uint16_t* __restrict__ o, int64_t so_b, int64_t so_t, int64_t so_h) {
   constexpr int NTHREADS = BLK * 2;
-  __shared__ __align__(16) uint16_t kbuf[NBUF][kTileElems];
-  __shared__ __align__(16) uint16_t vbuf[NBUF][kTileElems];
+  __shared__ __align__(256) uint16_t kbuf[NBUF][kTileElems];
+  __shared__ __align__(256) uint16_t vbuf[NBUF][kTileElems];
   __shared__ TileList tl;
   const auto bi = [](int n) { return NBUF == 2 ? (n & 1) : 0; };  // buffer of tile n
 
@@ -365,33 +366,34 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
   const auto exact_tile = [&](int n) {
     return exact_desc<BLK>(tl, n < nrag ? nexact - 1 : n - nrag, T, NT);
   };
-  const auto issue_exact_full = [&](int n, char* kd, void* vd, bool with_k, bool with_v) {
+  const uint32_t kb = lds_addr(kbuf[0]), vb = lds_addr(vbuf[0]);  // LDS byte addresses
+  const auto kbuf_at = [&](int buf) { return kb + buf * kTileBytes; };
+  const auto vbuf_at = [&](int buf) { return vb + buf * kTileBytes; };
+  const auto issue_exact_full = [&](int n, uint32_t kd, uint32_t vd, bool with_k, bool with_v) {
     const int first = exact_first<BLK>(tl, n - nrag);
     if (with_k) issue_i8<NTHREADS, true, true>(kd, is.ki, is, first, kKeys, ioff.k, ioff.ks, false);
     if (with_v) {
       if constexpr (INT8_PV)
-        issue_i8<NTHREADS, true, false>(static_cast<char*>(vd), is.vi, is, first, kKeys, ioff.v, 0, true);
+        issue_i8<NTHREADS, true, false>(vd, is.vi, is, first, kKeys, ioff.v, 0, true);
       else
-        issue_full<NTHREADS>(static_cast<uint16_t*>(vd), src.v + static_cast<int64_t>(first) * src.sv,
-                             src.sv, boff.v);
+        issue_full<NTHREADS>(vd, src.v + static_cast<int64_t>(first) * src.sv, src.sv, boff.v);
     }
   };
   const auto issue_tile = [&](int n, int buf) {
-    char* kd = reinterpret_cast<char*>(kbuf[buf]);
+    const uint32_t kd = kbuf_at(buf), vd = vbuf_at(buf);
     if (n >= nexact) {
       const TileDesc td = pooled_desc(tl, n - nexact, NT);
-      issue_generic<NTHREADS>(kbuf[buf], 0, td, src);
-      issue_generic<NTHREADS>(vbuf[buf], 1, td, src);
+      issue_generic<NTHREADS>(kd, 0, td, src);
+      issue_generic<NTHREADS>(vd, 1, td, src);
     } else if (n >= nrag) {
-      issue_exact_full(n, kd, vbuf[buf], true, true);
+      issue_exact_full(n, kd, vd, true, true);
     } else {
       const TileDesc td = exact_tile(n);
       issue_i8<NTHREADS, false, true>(kd, is.ki, is, td.first, td.nvalid, 0, 0, false);
       if constexpr (INT8_PV)
-        issue_i8<NTHREADS, false, false>(reinterpret_cast<char*>(vbuf[buf]), is.vi, is, td.first,
-                                          td.nvalid, 0, 0, true);
+        issue_i8<NTHREADS, false, false>(vd, is.vi, is, td.first, td.nvalid, 0, 0, true);
       else
-        issue_generic<NTHREADS>(vbuf[buf], 1, td, src);
+        issue_generic<NTHREADS>(vd, 1, td, src);
     }
   };
   issue_tile(0, 0);
@@ -457,7 +459,7 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
         wait_tile_copies();
         __syncthreads();
         if (F + 1 < E)
-          issue_exact_full(F + 1, reinterpret_cast<char*>(kbuf[(F + 1) & 1]), nullptr, true, false);
+          issue_exact_full(F + 1, kbuf_at((F + 1) & 1), 0u, true, false);
         qk_scaled(kbuf[F & 1], sa);
         wait_tile_copies();
         __syncthreads();  // kbuf[F & 1] is refilled (K of tile F+2) by the first step
@@ -466,7 +468,7 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
         __syncthreads();
         qk_scaled(kbuf[0], sa);
         __syncthreads();  // kbuf is free
-        if (F + 1 < E) issue_exact_full(F + 1, reinterpret_cast<char*>(kbuf[0]), nullptr, true, false);
+        if (F + 1 < E) issue_exact_full(F + 1, kbuf_at(0), 0u, true, false);
         wait_tile_copies();
         __syncthreads();  // K(F+1) and V(F) in LDS
       }
@@ -475,8 +477,8 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
       // last full tile: a redundant copy into a buffer nothing reads afterwards.
       const auto step = [&](f32x16 (&sc)[2], f32x16 (&sn)[2]) {
         if constexpr (NBUF == 2) {
-          issue_exact_full(min(n + 2, E - 1), reinterpret_cast<char*>(kbuf[n & 1]), nullptr, true, false);
-          issue_exact_full(n + 1, nullptr, vbuf[(n + 1) & 1], false, true);
+          issue_exact_full(min(n + 2, E - 1), kbuf_at(n & 1), 0u, true, false);
+          issue_exact_full(n + 1, 0u, vbuf_at((n + 1) & 1), false, true);
           fast_step<INT8_PV, false>(st, sc, sn, reinterpret_cast<const char*>(kbuf[(n + 1) & 1]),
                                     vbuf[n & 1], qireg, qsl, lane, [] {});
           wait_tile_copies();
@@ -487,12 +489,11 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
                                    qsl, lane, [&] {
                                      wait_tile_copies();  // V(n)
                                      __syncthreads();     // every wave is done with K(n+1), ks(n+1)
-                                     issue_exact_full(min(n + 2, E - 1), reinterpret_cast<char*>(kbuf[0]),
-                                                      nullptr, true, false);
+                                     issue_exact_full(min(n + 2, E - 1), kbuf_at(0), 0u, true, false);
                                    });
           wait_tile_copies();  // K(n+2)
           __syncthreads();     // every wave is done with V(n)
-          issue_exact_full(n + 1, nullptr, vbuf[0], false, true);
+          issue_exact_full(n + 1, 0u, vbuf_at(0), false, true);
         }
         ++n;
       };
