@@ -103,35 +103,80 @@ pool_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int64_t 
 
 // --------------------------------------------------------------- moments --
 // /root/reference/_preprocess.py:241-243 and /root/reference/_fused_prep.py:77-81.
-// 8 lane groups sum blocks j = g (mod 8) in ascending order; the partials are
-// combined ((p0+p1)+(p2+p3)) + ((p4+p5)+(p6+p7)).
+// 8 partial groups sum blocks j = g (mod 8) in ascending order; the partials
+// are combined ((p0+p1)+(p2+p3)) + ((p4+p5)+(p6+p7)).
 __device__ __forceinline__ float tree8(const float (*part)[kHeadDim], int d) {
   return ((part[0][d] + part[1][d]) + (part[2][d] + part[3][d])) +
          ((part[4][d] + part[5][d]) + (part[6][d] + part[7][d]));
 }
 
-__global__ void __launch_bounds__(1024)
+// One workgroup of 128 threads per (head, batch): thread t owns partial group
+// g = t / 16 and channels c8 .. c8+7 (16-byte loads of 8 bf16). Loads are
+// issued in chunks of kMomU before they are summed, in the same ascending
+// order as a plain loop.
+constexpr int kMomThreads = 128;
+constexpr int kMomU = 16;
+__device__ __forceinline__ void unpack8(const uint4& w, float (&x)[8]) {
+  x[0] = lo_bf16(w.x); x[1] = hi_bf16(w.x); x[2] = lo_bf16(w.y); x[3] = hi_bf16(w.y);
+  x[4] = lo_bf16(w.z); x[5] = hi_bf16(w.z); x[6] = lo_bf16(w.w); x[7] = hi_bf16(w.w);
+}
+
+__global__ void __launch_bounds__(kMomThreads)
 moments_kernel(uint16_t* __restrict__ kc, int64_t npad, int NT, int H, int centre,
                float* __restrict__ kc_mean, float* __restrict__ kc_var,
                const float* __restrict__ vamax_part, float* __restrict__ vscale) {
   const int h = blockIdx.x, b = blockIdx.y;
-  const int d = threadIdx.x & (kHeadDim - 1), g = threadIdx.x >> 7;
+  const int g = threadIdx.x >> 4, c8 = (threadIdx.x & 15) * 8;
   __shared__ float part[8][kHeadDim];
   __shared__ float amx[8][kHeadDim];
   __shared__ float smean[kHeadDim];
   const float fnt = static_cast<float>(NT);
-  uint16_t* col = kc + (static_cast<int64_t>(b) * npad * H + h) * kHeadDim + d;
+  uint16_t* col = kc + (static_cast<int64_t>(b) * npad * H + h) * kHeadDim + c8;
   const int64_t sj = static_cast<int64_t>(H) * kHeadDim;
-  float s = 0.f, am = 0.f;
-  for (int j = g; j < NT; j += 8) s = s + bf2f(col[j * sj]);
-  if (vamax_part) {
-    const float* a = vamax_part + (static_cast<int64_t>(b) * NT * H + h) * kHeadDim + d;
-    for (int j = g; j < NT; j += 8) am = fmaxf(am, a[j * sj]);
+  float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float am[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int j0 = g; j0 < NT; j0 += 8 * kMomU) {
+    uint4 w[kMomU];
+#pragma unroll
+    for (int u = 0; u < kMomU; ++u)  // clamped row: no branch around the load
+      w[u] = *reinterpret_cast<const uint4*>(col + min(j0 + 8 * u, NT - 1) * sj);
+#pragma unroll
+    for (int u = 0; u < kMomU; ++u) {
+      if (j0 + 8 * u < NT) {
+        float x[8];
+        unpack8(w[u], x);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s[e] = s[e] + x[e];
+      }
+    }
   }
-  part[g][d] = s;
-  amx[g][d] = am;
+  if (vamax_part) {
+    const float* a = vamax_part + (static_cast<int64_t>(b) * NT * H + h) * kHeadDim + c8;
+    for (int j0 = g; j0 < NT; j0 += 8 * kMomU) {
+      float4 w[kMomU][2];
+#pragma unroll
+      for (int u = 0; u < kMomU; ++u) {
+        const float4* p = reinterpret_cast<const float4*>(a + min(j0 + 8 * u, NT - 1) * sj);
+        w[u][0] = p[0];
+        w[u][1] = p[1];
+      }
+#pragma unroll
+      for (int u = 0; u < kMomU; ++u) {  // duplicated rows leave the max unchanged
+        am[0] = fmaxf(am[0], w[u][0].x); am[1] = fmaxf(am[1], w[u][0].y);
+        am[2] = fmaxf(am[2], w[u][0].z); am[3] = fmaxf(am[3], w[u][0].w);
+        am[4] = fmaxf(am[4], w[u][1].x); am[5] = fmaxf(am[5], w[u][1].y);
+        am[6] = fmaxf(am[6], w[u][1].z); am[7] = fmaxf(am[7], w[u][1].w);
+      }
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    part[g][c8 + e] = s[e];
+    amx[g][c8 + e] = am[e];
+  }
   __syncthreads();
-  if (g == 0) {
+  {
+    const int d = threadIdx.x;  // one channel per thread
     const float mean = tree8(part, d) / fnt;
     smean[d] = mean;
     kc_mean[(static_cast<int64_t>(b) * H + h) * kHeadDim + d] = mean;
@@ -145,21 +190,50 @@ moments_kernel(uint16_t* __restrict__ kc, int64_t npad, int NT, int H, int centr
     }
   }
   __syncthreads();
-  const float mean = smean[d];
-  float acc = 0.f;
-  for (int j = g; j < NT; j += 8) {
-    float x = bf2f(col[j * sj]) - mean;
-    if (centre) {
-      const uint16_t nb = f2bf(x);
-      col[j * sj] = nb;
-      x = bf2f(nb);
+  float mean[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) mean[e] = smean[c8 + e];
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int j0 = g; j0 < NT; j0 += 8 * kMomU) {
+    uint4 w[kMomU];
+#pragma unroll
+    for (int u = 0; u < kMomU; ++u)
+      w[u] = *reinterpret_cast<const uint4*>(col + min(j0 + 8 * u, NT - 1) * sj);
+#pragma unroll
+    for (int u = 0; u < kMomU; ++u) {
+      const int j = j0 + 8 * u;
+      if (j < NT) {
+        float x[8];
+        unpack8(w[u], x);
+        uint16_t nb[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float y = x[e] - mean[e];
+          if (centre) {
+            nb[e] = f2bf(y);
+            y = bf2f(nb[e]);
+          }
+          acc[e] = acc[e] + y * y;
+        }
+        if (centre) {
+          uint4 o;
+          o.x = nb[0] | (static_cast<uint32_t>(nb[1]) << 16);
+          o.y = nb[2] | (static_cast<uint32_t>(nb[3]) << 16);
+          o.z = nb[4] | (static_cast<uint32_t>(nb[5]) << 16);
+          o.w = nb[6] | (static_cast<uint32_t>(nb[7]) << 16);
+          *reinterpret_cast<uint4*>(col + j * sj) = o;
+        }
+      }
     }
-    acc = acc + x * x;
   }
   __syncthreads();  // every thread has read part[] above
-  part[g][d] = acc;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) part[g][c8 + e] = acc[e];
   __syncthreads();
-  if (g == 0) kc_var[(static_cast<int64_t>(b) * H + h) * kHeadDim + d] = tree8(part, d) / fnt;
+  {
+    const int d = threadIdx.x;
+    kc_var[(static_cast<int64_t>(b) * H + h) * kHeadDim + d] = tree8(part, d) / fnt;
+  }
 }
 
 // ----------------------------------------------------------------- route --
@@ -170,6 +244,7 @@ constexpr int kQB = 8;
 constexpr int kRouteThreads = 256;
 constexpr int kMaxWords = 128;  // NT <= 4096
 constexpr int kKcStride = kHeadDim + 4;  // bf16 per staged kc row (264 B): conflict-free 8-byte reads
+constexpr int kKcLoads = kHeadDim / 8;   // 16-byte loads per thread to stage 256 kc rows
 
 __global__ void __launch_bounds__(kRouteThreads)
 route_kernel(const float* __restrict__ qbar, const uint16_t* __restrict__ kc, int64_t npad,
@@ -180,25 +255,38 @@ route_kernel(const float* __restrict__ qbar, const uint16_t* __restrict__ kc, in
              uint32_t* __restrict__ mask) {
   const int i0 = blockIdx.x * kQB, h = blockIdx.y, b = blockIdx.z;
   const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
-  __shared__ __align__(16) float sq[kQB][kHeadDim + 4];
+  __shared__ __align__(16) float sq[kQB][kHeadDim];
+  __shared__ float smk[kHeadDim], svk[kHeadDim];
   __shared__ float sthr[kQB];
   __shared__ uint32_t smask[kQB][kMaxWords];
   __shared__ __align__(16) uint16_t skc[kRouteThreads * kKcStride];
   const int64_t bh = static_cast<int64_t>(b) * H + h;
-  for (int e = t; e < kQB * kHeadDim; e += kRouteThreads) {
-    const int i = e / kHeadDim, d = e % kHeadDim;
-    sq[i][d] = (i0 + i < NT) ? qbar[(bh * NT + i0 + i) * kHeadDim + d] : 0.f;
+  // The prologue's global loads are all issued before any of them is used:
+  // the query centroids (one float4 per thread) and the moments.
+  {
+    static_assert(kQB * kHeadDim == 4 * kRouteThreads, "one float4 of qbar per thread");
+    const int i = t / (kHeadDim / 4), d4 = t % (kHeadDim / 4);
+    float4 qv = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (i0 + i < NT) qv = *reinterpret_cast<const float4*>(qbar + (bh * NT + i0 + i) * kHeadDim + 4 * d4);
+    float mk = 0.f, vk = 0.f;
+    if (t < kHeadDim) {
+      mk = kc_mean[bh * kHeadDim + t];
+      vk = kc_var[bh * kHeadDim + t];
+    }
+    *reinterpret_cast<float4*>(&sq[i][4 * d4]) = qv;
+    if (t < kHeadDim) {
+      smk[t] = mk;
+      svk[t] = vk;
+    }
   }
   for (int e = t; e < kQB * kMaxWords; e += kRouteThreads) smask[e / kMaxWords][e % kMaxWords] = 0u;
   __syncthreads();
   if (t < kQB) {
-    const float* mk = kc_mean + bh * kHeadDim;
-    const float* vk = kc_var + bh * kHeadDim;
     float mu = 0.f, var = 0.f;
     for (int d = 0; d < kHeadDim; ++d) {
       const float qd = sq[t][d];
-      if (mode == 0) mu = fmaf(qd, mk[d], mu);
-      var = fmaf(qd * qd, vk[d], var);
+      if (mode == 0) mu = fmaf(qd, smk[d], mu);
+      var = fmaf(qd * qd, svk[d], var);
     }
     float th;
     if (mode == 0) {
@@ -216,18 +304,29 @@ route_kernel(const float* __restrict__ qbar, const uint16_t* __restrict__ kc, in
   __syncthreads();
 
   for (int j0 = 0; j0 < NT; j0 += kRouteThreads) {
-    // Stage kc rows j0 .. j0+255 (coalesced 16-byte loads; rows past NT are 0).
-    __syncthreads();
-    for (int e = t; e < kRouteThreads * (kHeadDim / 8); e += kRouteThreads) {
-      const int r = e >> 4, cc = e & 15;
-      const int j = j0 + r;
-      uint4 v = make_uint4(0u, 0u, 0u, 0u);
-      if (j < NT)
-        v = *reinterpret_cast<const uint4*>(
-            kc + ((static_cast<int64_t>(b) * npad + j) * H + h) * kHeadDim + cc * 8);
-      uint2* dst = reinterpret_cast<uint2*>(&skc[r * kKcStride + cc * 8]);
-      dst[0] = make_uint2(v.x, v.y);
-      dst[1] = make_uint2(v.z, v.w);
+    // Stage kc rows j0 .. j0+255 (coalesced 16-byte loads, all issued before
+    // the LDS stores; rows past NT are 0), then thread t scores row t.
+    {
+      uint4 v[kKcLoads];
+#pragma unroll
+      for (int u = 0; u < kKcLoads; ++u) {
+        const int e = t + kRouteThreads * u;
+        const int r = e >> 4, cc = e & 15;
+        const int j = j0 + r;
+        v[u] = make_uint4(0u, 0u, 0u, 0u);
+        if (j < NT)
+          v[u] = *reinterpret_cast<const uint4*>(
+              kc + ((static_cast<int64_t>(b) * npad + j) * H + h) * kHeadDim + cc * 8);
+      }
+      __syncthreads();  // the previous chunk's rows have been read
+#pragma unroll
+      for (int u = 0; u < kKcLoads; ++u) {
+        const int e = t + kRouteThreads * u;
+        const int r = e >> 4, cc = e & 15;
+        uint2* dst = reinterpret_cast<uint2*>(&skc[r * kKcStride + cc * 8]);
+        dst[0] = make_uint2(v[u].x, v[u].y);
+        dst[1] = make_uint2(v[u].z, v[u].w);
+      }
     }
     __syncthreads();
     const int j = j0 + t;
@@ -359,8 +458,11 @@ extern "C" int solattn_moments(uint16_t* kc, int64_t npad, int64_t B, int64_t NT
                   SOLATTN_EINVAL, "moments: bad sizes");
   SOLATTN_REQUIRE(kc && kc_mean && kc_var, SOLATTN_EINVAL, "moments: null pointer");
   SOLATTN_REQUIRE(!vamax_part || vscale, SOLATTN_EINVAL, "moments: vamax_part needs vscale");
+  SOLATTN_REQUIRE(reinterpret_cast<uintptr_t>(kc) % 16 == 0 &&
+                      reinterpret_cast<uintptr_t>(vamax_part) % 16 == 0,
+                  SOLATTN_EINVAL, "moments: kc and vamax_part must be 16-byte aligned");
   hipLaunchKernelGGL(moments_kernel, dim3(static_cast<uint32_t>(H), static_cast<uint32_t>(B)),
-                     dim3(1024), 0, reinterpret_cast<hipStream_t>(stream), kc, npad,
+                     dim3(kMomThreads), 0, reinterpret_cast<hipStream_t>(stream), kc, npad,
                      static_cast<int>(NT), static_cast<int>(H), centre ? 1 : 0, kc_mean, kc_var,
                      vamax_part, vscale);
   return check_launch("moments");

@@ -28,61 +28,74 @@ __device__ __forceinline__ uint32_t pack_i8x4(int8_t a, int8_t b, int8_t c, int8
 // /root/reference/_fused_quant.py:403-426 (per token, optional smoothing mean)
 // and /root/reference/_fused_prep.py:325-331 (Q; clamp-then-round gives the
 // same codes). vscale != nullptr switches to the per-channel V rule,
-// /root/reference/_fused_quant.py:455-472.
+// /root/reference/_fused_quant.py:455-472. Each 16-lane group handles kRowsPerGroup
+// rows, kQuantThreads / 16 groups apart, with every row's load issued before
+// any arithmetic (more bytes in flight per lane).
+constexpr int kRowsPerGroup = 4;
 __global__ void __launch_bounds__(kQuantThreads)
 quant_kernel(const uint16_t* __restrict__ x, int64_t sx_b, int64_t sx_t, int64_t sx_h,
              uint32_t T, uint32_t H, uint32_t rows, const float* __restrict__ mean,
              const float* __restrict__ vscale, int8_t* __restrict__ xi, float* __restrict__ xs,
              int64_t TP) {
-  const uint32_t row = blockIdx.x * kRowsPerWG + (threadIdx.x >> 4);
-  if (row >= rows) return;
   const int c8 = (threadIdx.x & 15) * 8;
-  const uint32_t h = row % H;
-  const uint32_t bt = row / H;
-  const uint32_t t = bt % T;
-  const uint32_t b = bt / T;
-  const uint4 raw =
-      *reinterpret_cast<const uint4*>(x + b * sx_b + static_cast<int64_t>(t) * sx_t + h * sx_h + c8);
-  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
-  float y[8];
+  uint32_t rw[kRowsPerGroup], hh[kRowsPerGroup], tt[kRowsPerGroup], bb[kRowsPerGroup];
+  uint4 raw[kRowsPerGroup];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    y[2 * e] = lo_bf16(w[e]);
-    y[2 * e + 1] = hi_bf16(w[e]);
+  for (int k = 0; k < kRowsPerGroup; ++k) {
+    rw[k] = (blockIdx.x * kRowsPerGroup + k) * kRowsPerWG + (threadIdx.x >> 4);
+    const uint32_t row = rw[k] < rows ? rw[k] : rows - 1;  // clamped: loads stay in bounds
+    hh[k] = row % H;
+    const uint32_t bt = row / H;
+    tt[k] = bt % T;
+    bb[k] = bt / T;
+    raw[k] = *reinterpret_cast<const uint4*>(x + bb[k] * sx_b + static_cast<int64_t>(tt[k]) * sx_t +
+                                             hh[k] * sx_h + c8);
   }
-  const int64_t bh = static_cast<int64_t>(b) * H + h;
-  int8_t code[8];
-  if (vscale) {
-    const float4* sp = reinterpret_cast<const float4*>(vscale + bh * kQD + c8);
-    const float4 s0 = sp[0], s1 = sp[1];
-    const float s[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
 #pragma unroll
-    for (int e = 0; e < 8; ++e) code[e] = round_half_away_clamp(y[e] / s[e]);
-  } else {
-    if (mean) {
-      const float4* mp = reinterpret_cast<const float4*>(mean + bh * kQD + c8);
-      const float4 m0 = mp[0], m1 = mp[1];
-      const float m[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
+  for (int k = 0; k < kRowsPerGroup; ++k) {
+    const uint32_t b = bb[k], t = tt[k], h = hh[k];
+    const uint32_t w[4] = {raw[k].x, raw[k].y, raw[k].z, raw[k].w};
+    float y[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) y[e] = y[e] - m[e];
+    for (int e = 0; e < 4; ++e) {
+      y[2 * e] = lo_bf16(w[e]);
+      y[2 * e + 1] = hi_bf16(w[e]);
     }
-    float amax = 0.f;
+    const int64_t bh = static_cast<int64_t>(b) * H + h;
+    int8_t code[8];
+    if (vscale) {
+      const float4* sp = reinterpret_cast<const float4*>(vscale + bh * kQD + c8);
+      const float4 s0 = sp[0], s1 = sp[1];
+      const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
 #pragma unroll
-    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(y[e]));
+      for (int e = 0; e < 8; ++e) code[e] = round_half_away_clamp(y[e] / sv[e]);
+    } else {
+      if (mean) {
+        const float4* mp = reinterpret_cast<const float4*>(mean + bh * kQD + c8);
+        const float4 m0 = mp[0], m1 = mp[1];
+        const float m[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
 #pragma unroll
-    for (int s = 1; s < 16; s <<= 1) amax = fmaxf(amax, __shfl_xor(amax, s));
-    const float sc = amax / 127.0f;
-    const float ss = sc > 1e-8f ? sc : 1e-8f;
+        for (int e = 0; e < 8; ++e) y[e] = y[e] - m[e];
+      }
+      float amax = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) code[e] = round_half_away_clamp(y[e] / ss);
-    if ((threadIdx.x & 15) == 0) xs[(static_cast<int64_t>(b) * TP + t) * H + h] = ss;
+      for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(y[e]));
+#pragma unroll
+      for (int sh = 1; sh < 16; sh <<= 1) amax = fmaxf(amax, __shfl_xor(amax, sh));
+      const float sc = amax / 127.0f;
+      const float ss = sc > 1e-8f ? sc : 1e-8f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) code[e] = round_half_away_clamp(y[e] / ss);
+      if ((threadIdx.x & 15) == 0 && rw[k] < rows) xs[(static_cast<int64_t>(b) * TP + t) * H + h] = ss;
+    }
+    if (rw[k] < rows) {
+      uint2 o;
+      o.x = pack_i8x4(code[0], code[1], code[2], code[3]);
+      o.y = pack_i8x4(code[4], code[5], code[6], code[7]);
+      *reinterpret_cast<uint2*>(xi + ((static_cast<int64_t>(b) * TP + t) * H + h) * kQD + c8) = o;
+    }
   }
-  uint2 o;
-  o.x = pack_i8x4(code[0], code[1], code[2], code[3]);
-  o.y = pack_i8x4(code[4], code[5], code[6], code[7]);
-  *reinterpret_cast<uint2*>(xi + ((static_cast<int64_t>(b) * TP + t) * H + h) * kQD + c8) = o;
 }
-
 int launch_quant(const uint16_t* x, int64_t sx_b, int64_t sx_t, int64_t sx_h, int64_t B,
                  int64_t T, int64_t H, int64_t D, const float* mean, const float* vscale,
                  int8_t* xi, float* xs, int64_t TP, hipStream_t stream, const char* what) {
@@ -94,7 +107,7 @@ int launch_quant(const uint16_t* x, int64_t sx_b, int64_t sx_t, int64_t sx_h, in
                       sx_h % 8 == 0 && reinterpret_cast<uintptr_t>(xi) % 8 == 0,
                   SOLATTN_EINVAL, "%s: unaligned input or strides", what);
   const uint32_t rows = static_cast<uint32_t>(B * T * H);
-  hipLaunchKernelGGL(quant_kernel, dim3(static_cast<uint32_t>(cdiv(rows, kRowsPerWG))),
+  hipLaunchKernelGGL(quant_kernel, dim3(static_cast<uint32_t>(cdiv(rows, kRowsPerWG * kRowsPerGroup))),
                      dim3(kQuantThreads), 0, stream, x, sx_b, sx_t, sx_h,
                      static_cast<uint32_t>(T), static_cast<uint32_t>(H), rows, mean, vscale, xi,
                      xs, TP);

@@ -104,7 +104,7 @@ int solattn_pool(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
  * kc_mean, kc_var: fp32 [B, H, D].
  * If vamax_part != NULL also vscale[b, h, d] = max(max_j vamax_part * (1/127)f, 1e-8)
  * (/root/reference/_fused_quant.py:102-105: torch divides by a scalar as a
- * multiply by its fp32 reciprocal). */
+ * multiply by its fp32 reciprocal). kc and vamax_part must be 16-byte aligned. */
 int solattn_moments(uint16_t* kc, int64_t npad, int64_t B, int64_t NT, int64_t H,
                     int64_t D, int centre, float* kc_mean, float* kc_var,
                     const float* vamax_part, float* vscale, solattn_stream_t stream);
