@@ -144,6 +144,27 @@ def _pkg():
             for m in ("_tri_fwd", "_int8_fwd", "_preprocess", "_fused_prep", "_morton")}
 
 
+def torch_sdpa(q, k, v, dflops, steps):
+    """PyTorch's dense SDPA at the same shape (the path ComfyUI takes when the
+    node declines): BHND contiguous bf16, fused backends only (flash, then
+    memory-efficient); a backend that has no kernel for this GPU raises and is
+    recorded instead of falling back to the unfused math path."""
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    qh, kh, vh = (t.transpose(1, 2).contiguous() for t in (q, k, v))
+    tried = {}
+    for name, backend in (("flash", SDPBackend.FLASH_ATTENTION),
+                          ("efficient", SDPBackend.EFFICIENT_ATTENTION)):
+        try:
+            with sdpa_kernel([backend]):
+                ms = time_cuda(lambda: F.scaled_dot_product_attention(qh, kh, vh), steps, 1)
+            return {"backend": name, "ms": round(ms, 3),
+                    "dense_tflops": round(dflops / (ms * 1e-3) / 1e12, 1), "unavailable": tried}
+        except RuntimeError as e:
+            tried[name] = str(e).splitlines()[0][:160]
+    return {"backend": None, "unavailable": tried}
+
+
 def cpu_baseline(cfg, q, k, v, budget_s=15.0):
     """The oracle's masked-attention CPU path (torch fp32, augmented keys, one
     query block at a time) on a bounded sample of query blocks; the oracle's C
@@ -370,6 +391,11 @@ def main():
                              1)
         line["dense_all_exact_ms"] = round(dense_ms, 3)
         line["dense_all_exact_tflops"] = round(dflops / (dense_ms * 1e-3) / 1e12, 1)
+        # the sparse BF16 call per tau, beside the dense path the node falls back to
+        line["bf16_ms"] = {str(t): round(time_cuda(lambda: sol_attn(q, k, v, tau=t, block=block),
+                                                   args.steps, args.warmup), 4)
+                           for t in (0.8, 0.9, 0.95)}
+        line["torch_sdpa"] = torch_sdpa(q, k, v, dflops, max(3, args.steps // 4))
     if not args.no_cpu:
         print("[bench] CPU baseline", file=sys.stderr, flush=True)
         line["cpu_baseline"] = cpu_baseline(cfg, q, k, v, args.cpu_budget)
