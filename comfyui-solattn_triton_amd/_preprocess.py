@@ -97,7 +97,7 @@ def route(q, k, v, *, scale: float, tau: float, block: int = BLOCK_SIZE, int8: b
     """pool -> moments -> thresholds + routing lists, all on the device.
 
     ``int8`` selects the INT8 path's centred pooled keys and tau*sigma
-    threshold (/root/reference/_fused_prep.py:77-81, 334-342); ``v_absmax``
+    threshold (/root/reference/_fused_prep.py:77-81, 50-59); ``v_absmax``
     also produces the per-channel V scale from the same pass.
     """
     check_inputs(q, k, v, block)

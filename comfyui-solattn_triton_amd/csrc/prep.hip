@@ -237,7 +237,7 @@ moments_kernel(uint16_t* __restrict__ kc, int64_t npad, int NT, int H, int centr
 }
 
 // ----------------------------------------------------------------- route --
-// Thresholds (/root/reference/_preprocess.py:149-163, /root/reference/_fused_prep.py:334-342)
+// Thresholds (/root/reference/_preprocess.py:149-163, /root/reference/_fused_prep.py:50-59)
 // and the routing rule of the forward (/root/reference/_tri_fwd.py:279-286),
 // for kQB query blocks per workgroup; thread t scores key block j0 + t.
 constexpr int kQB = 8;

@@ -25,10 +25,10 @@ __device__ __forceinline__ uint32_t pack_i8x4(int8_t a, int8_t b, int8_t c, int8
          (static_cast<uint32_t>(static_cast<uint8_t>(d)) << 24);
 }
 
-// /root/reference/_fused_quant.py:403-426 (per token, optional smoothing mean)
-// and /root/reference/_fused_prep.py:325-331 (Q; clamp-then-round gives the
+// /root/reference/_fused_quant.py:8-42 (per token, optional smoothing mean)
+// and /root/reference/_fused_prep.py:42-48 (Q; clamp-then-round gives the
 // same codes). vscale != nullptr switches to the per-channel V rule,
-// /root/reference/_fused_quant.py:455-472. Each 16-lane group handles kRowsPerGroup
+// /root/reference/_fused_quant.py:61-88. Each 16-lane group handles kRowsPerGroup
 // rows, kQuantThreads / 16 groups apart, with every row's load issued before
 // any arithmetic (more bytes in flight per lane).
 constexpr int kRowsPerGroup = 4;

@@ -3,7 +3,7 @@
 // HBM-bound copy: every workgroup moves a run of whole rows in 16-byte lanes,
 // so each wave issues fully coalesced 1 KiB loads and stores. Replaces the
 // torch index_select calls of /root/reference/_morton.py:113,128,148 and
-// /root/reference/_morton_h3.py:349,373.
+// /root/reference/_morton_h3.py:193,217.
 #include <algorithm>
 
 #include "common.hpp"

@@ -71,7 +71,7 @@ int solattn_morton_perm(int64_t frames, int64_t height, int64_t width, int curve
  * A row is row_bytes contiguous bytes (row_bytes % 16 == 0, 16-byte aligned
  * rows). index: device int64 [rows], each entry in [0, src_rows).
  * Replaces: the torch index_select / fancy-index gathers of the Morton hooks,
- * /root/reference/_morton.py:113,128,148 and /root/reference/_morton_h3.py:349,373. */
+ * /root/reference/_morton.py:113,128,148 and /root/reference/_morton_h3.py:193,217. */
 int solattn_reorder_rows(const void* src, int64_t src_rows, int64_t src_stride_b_bytes,
                          int64_t src_stride_row_bytes, void* dst, int64_t dst_stride_b_bytes,
                          int64_t dst_stride_row_bytes, int64_t batch, int64_t rows,
@@ -86,7 +86,7 @@ int solattn_reorder_rows(const void* src, int64_t src_rows, int64_t src_stride_b
  * Replaces: _reduce_kc_kernel / _reduce_vc_kernel / _reduce_kv,
  * /root/reference/_preprocess.py:23-113,172-224, and the Q centroid of
  * _diag_threshold_kernel (:144-149) / _q_quant_threshold_kernel
- * (/root/reference/_fused_prep.py:320-334). */
+ * (/root/reference/_fused_prep.py:16-59). */
 int solattn_pool(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
                  const uint16_t* k, int64_t sk_b, int64_t sk_t, int64_t sk_h,
                  const uint16_t* v, int64_t sv_b, int64_t sv_t, int64_t sv_h,
@@ -115,7 +115,7 @@ int solattn_moments(uint16_t* kc, int64_t npad, int64_t B, int64_t NT, int64_t H
  *     mu  = (fmaf chain qbar*kc_mean) * c
  *     var = (fmaf chain (qbar*qbar)*kc_var) * (c*c)
  *     thr = mu + tau * sqrtf(fmaxf(var, 0) + 1e-6f)
- *   mode 1 (INT8, /root/reference/_fused_prep.py:334-342, kc already centred):
+ *   mode 1 (INT8, /root/reference/_fused_prep.py:50-59, kc already centred):
  *     thr = tau * sqrtf(var + 1e-6f)
  *   R[i][j] = (fmaf chain qbar_i*kc_j) * c
  *   exact(i, j) = i in [sink_q_lo, sink_q_hi) ? 1
@@ -136,7 +136,7 @@ int solattn_route(const float* qbar, const uint16_t* kc, int64_t npad, const flo
  *   code = clamp(y/s >= 0 ? trunc(y/s + 0.5) : trunc(y/s - 0.5), -127, 127)
  * xi: int8 [B, TP, H, D]; xs: fp32 [B, TP, H]; rows t >= T are not written.
  * Replaces: _quant_kernel / quantize_bthd, /root/reference/_fused_quant.py:8-58
- * (and the Q half of _q_quant_threshold_kernel, _fused_prep.py:325-331). */
+ * (and the Q half of _q_quant_threshold_kernel, _fused_prep.py:42-48). */
 int solattn_quant_rows(const uint16_t* x, int64_t sx_b, int64_t sx_t, int64_t sx_h,
                        int64_t B, int64_t T, int64_t H, int64_t D, const float* mean,
                        int8_t* xi, float* xs, int64_t TP, solattn_stream_t stream);

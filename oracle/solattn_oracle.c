@@ -216,7 +216,7 @@ void or_moments(uint16_t* kc, int64_t npad, int64_t B, int64_t NT, int64_t H, in
 
 /* ----------------------------------------------------------------- route --
  * Threshold: BF16 /root/reference/_preprocess.py:149-163; INT8
- * /root/reference/_fused_prep.py:334-342. Routing rule: the forward's
+ * /root/reference/_fused_prep.py:50-59. Routing rule: the forward's
  * /root/reference/_tri_fwd.py:279-286 (R = sum_r (q_r . kc_j) * c / len_i,
  * restated as c * (qbar_i . kc_j)); exact = q_in_sink ? valid : routed. */
 void or_threshold(const float* qbar, const float* kc_mean, const float* kc_var, int64_t B,
@@ -291,8 +291,8 @@ void or_route(const float* qbar, const uint16_t* kc, int64_t npad, const float* 
 }
 
 /* ----------------------------------------------------------------- quant --
- * Per token: /root/reference/_fused_quant.py:409-426 (K, optional smoothing
- * mean, round-then-clamp) and /root/reference/_fused_prep.py:326-331 (Q,
+ * Per token: /root/reference/_fused_quant.py:25-42 (K, optional smoothing
+ * mean, round-then-clamp) and /root/reference/_fused_prep.py:43-48 (Q,
  * clamp-then-round; identical codes). */
 static inline int8_t round_half_away_clamp(float val) {
   float r = val >= 0.f ? truncf(val + 0.5f) : truncf(val - 0.5f);
@@ -326,7 +326,7 @@ void or_quant_rows(const uint16_t* x, int64_t sx_b, int64_t sx_t, int64_t sx_h, 
       }
 }
 
-/* Per channel V: /root/reference/_fused_quant.py:461-472. */
+/* Per channel V: /root/reference/_fused_quant.py:77-88. */
 void or_quant_v(const uint16_t* v, int64_t sv_b, int64_t sv_t, int64_t sv_h, int64_t B,
                 int64_t T, int64_t H, int64_t D, const float* vscale, int8_t* vi, int64_t TP) {
 #pragma omp parallel for collapse(2) schedule(static)
