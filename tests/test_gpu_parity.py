@@ -181,3 +181,73 @@ def test_strided_qkv_view(pkg, dev):
     a = tri.sol_attn(q, k, v, tau=0.7, block=64)
     b = tri.sol_attn(q.contiguous(), k.contiguous(), v.contiguous(), tau=0.7, block=64)
     assert torch.equal(a, b)
+
+
+TINY_CASES = [  # (T, block): one partial block, exactly one block, one block + 1 row
+    (1, 64), (63, 64), (64, 64), (65, 64), (100, 128), (128, 128), (129, 128),
+]
+
+
+@pytest.mark.parametrize("case", TINY_CASES)
+def test_fwd_tiny_sequences(pkg, dev, case):
+    """Sequences of one or two blocks, both forwards, against the oracle."""
+    tri, i8 = _mods(pkg)[1], _mods(pkg)[2]
+    T, block = case
+    B, H = 2, 3
+    print(f"[fwd tiny] T={T} block={block}", flush=True)
+    q, k, v = (randn_bf16((B, T, H, 128), s) for s in (60, 61, 62))
+    out = tri.sol_attn(q.to(dev), k.to(dev), v.to(dev), tau=0.9, block=block)
+    ref = oracle.prepare(bits(q), bits(k), bits(v), block=block, tau=0.9)
+    rows = _rows(B, H, ref["NT"])
+    err, cos = compare_rows(out.float().cpu().numpy(), oracle.forward_port(bits(q), bits(k), bits(v), ref, rows), block)
+    assert err < BF16_MAXABS and cos >= BF16_COS
+    for pv in (True, False):
+        out8 = i8.sol_attn_int8(q.to(dev), k.to(dev), v.to(dev), tau=0.9, block=block, int8_pv=pv)
+        ref8 = oracle.prepare(bits(q), bits(k), bits(v), block=block, tau=0.9, int8=True, int8_pv=pv)
+        port8 = oracle.forward_int8_port(bits(q), bits(v), ref8, rows, int8_pv=pv)
+        _, cos8 = compare_rows(out8.float().cpu().numpy(), port8, block)
+        assert cos8 >= INT8_COS
+
+
+def _block_constant_closed_form(q, kb, vb, T, block, dev, chunk=16384):
+    """Exact attention when K and V are constant inside every key block: the
+    pooled approximation is then exact for any routing, and the output is a
+    softmax over the NT blocks with log(len_j) added to each logit."""
+    NT = kb.shape[0]
+    lens = torch.tensor([min(block, T - block * j) for j in range(NT)], dtype=torch.float32, device=dev)
+    kf, vf = kb.float().to(dev), vb.float().to(dev)
+    out = torch.empty((T, 128), dtype=torch.float32, device=dev)
+    for t0 in range(0, T, chunk):
+        z = (q[t0:t0 + chunk].float().to(dev) @ kf.t()) * 128 ** -0.5 + lens.log()
+        out[t0:t0 + chunk] = torch.softmax(z, dim=-1) @ vf
+    return out
+
+
+@pytest.mark.parametrize("block", [64, 128])
+def test_fwd_max_blocks_closed_form(pkg, dev, block):
+    """The largest supported sequence (2048 query/key blocks, ragged last block)
+    with K and V constant inside each block, against the closed form; size-
+    independent, so it runs at the full block count."""
+    tri, i8 = _mods(pkg)[1], _mods(pkg)[2]
+    NT = 2048
+    T = NT * block - 17
+    print(f"[fwd max NT] block={block} T={T}", flush=True)
+    g = torch.Generator().manual_seed(70)
+    kb = torch.randn(NT, 128, generator=g).to(torch.bfloat16)
+    vb = torch.randn(NT, 128, generator=g).to(torch.bfloat16)
+    q = (torch.randn(T, 128, generator=g) * 2.0).to(torch.bfloat16)
+    k = kb.repeat_interleave(block, dim=0)[:T]
+    v = vb.repeat_interleave(block, dim=0)[:T]
+    ref = _block_constant_closed_form(q, kb, vb, T, block, dev)
+    qd, kd, vd = (t.reshape(1, T, 1, 128).to(dev) for t in (q, k, v))
+    out = tri.sol_attn(qd, kd, vd, tau=0.9, block=block)[0, :, 0].float()
+    err = (out - ref).abs().max().item()
+    cos = cosine(out.cpu().numpy(), ref.cpu().numpy())
+    print(f"[fwd max NT] bf16 max|err|={err:.3e} cos={cos:.6f}", flush=True)
+    assert err < BF16_MAXABS and cos >= BF16_COS
+    for pv in (True, False):
+        out8 = i8.sol_attn_int8(qd, kd, vd, tau=0.9, block=block, int8_pv=pv)[0, :, 0].float()
+        cos8 = cosine(out8.cpu().numpy(), ref.cpu().numpy())
+        print(f"[fwd max NT] int8_pv={pv} cos={cos8:.6f}", flush=True)
+        assert cos8 >= INT8_COS
+
