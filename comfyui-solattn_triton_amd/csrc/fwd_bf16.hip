@@ -1,21 +1,22 @@
 // BF16 Sol-Attn forward on gfx950 MFMA.
 //
 // One workgroup per (batch, head, query block of BLK rows); each wave owns 32
-// query rows, two workgroups share a CU (two waves per SIMD). Work is a list
-// of 64-key tiles staged in LDS (double buffered):
+// query rows, two waves share a SIMD. Work is a list of 64-key tiles staged in
+// LDS by global -> LDS copies (no VGPR staging):
 //   pooled tiles  64 pooled keys kc_j / values vc_j, masked to the approximate
 //                 blocks of this query block, softmax weight x len_j
 //                 (/root/reference/_tri_fwd.py:288-308);
 //   exact tiles   64 tokens of an exact block (/root/reference/_tri_fwd.py:310-340).
 // All tiles feed one online softmax per query row, which is exact under any
-// tile order (up to fp32 rounding): pooled tiles and the ragged exact tile run
-// first through a plain path; the full exact tiles then run through a
-// software pipeline whose step n
-//   * issues the copies of K(n+2) and V(n+1) (global -> LDS, no VGPR staging),
-//   * computes S(n+1) = K(n+1) Q^T (16 MFMAs) with the softmax VALU of tile n
-//     interleaved between them (row max, running max, exps packed to bf16,
-//     row sums by v_dot2),
-//   * accumulates O += P(n) V(n) (16 MFMAs), V operands read one step ahead.
+// tile order (up to fp32 rounding). The full exact tiles run through a
+// software pipeline, the pooled tiles and the ragged last exact tile through a
+// plain path:
+//   block 128 (fwd_bf16_kernel): K and V double buffered, two workgroups per
+//     CU; exact tiles first, three-stage step n = S(n+1) = K(n+1) Q^T, O +=
+//     P(n-1) V(n-1) and the softmax of S(n) in one instruction stream;
+//   block 64 (fwd_bf16_sbuf_kernel): K and V single buffered, four workgroups
+//     per CU; plain tiles first, two-stage step n = S(n+1) with the softmax of
+//     tile n interleaved, then O += P(n) V(n).
 //
 // MFMA dataflow (v_mfma_f32_32x32x16_bf16): S^T = K . Q^T puts one query row
 // per lane column, so row max / sum need one cross-lane step (lanes 32 apart,
