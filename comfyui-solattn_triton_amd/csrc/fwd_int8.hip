@@ -85,21 +85,24 @@ __device__ __forceinline__ void qk_i8_tile(const char* kt, const i32x4 (&qi)[4],
 // p_e = exp2(s*qsl - bmax) in [0, 1] for the 16 scores of key tile m, codes
 // round(p_e * 127) (v_cvt_pk_u8_f32: nearest, ties to even) packed 4 per
 // dword in element order; returns the fp32 sum of p_e.
-__device__ __forceinline__ float probs_i8(const f32x16& s, float qsl, float negb, i32x4& pi) {
+// negb127 = log2(127) - (tile max): the exponent yields 127 * pe directly, so
+// the codes need no multiply; the returned row sum is 127 * sum(pe).
+__device__ __forceinline__ float probs_i8(const f32x16& s, float qsl, float negb127, i32x4& pi) {
   float sum = 0.f;
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
     uint32_t d = 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const float pe = __builtin_amdgcn_exp2f(fmaf(s[4 * w + j], qsl, negb));
-      sum += pe;
-      d = __builtin_amdgcn_cvt_pk_u8_f32(pe * 127.f, j, d);
+      const float pe127 = __builtin_amdgcn_exp2f(fmaf(s[4 * w + j], qsl, negb127));
+      sum += pe127;
+      d = __builtin_amdgcn_cvt_pk_u8_f32(pe127, j, d);
     }
     pi[w] = static_cast<int>(d);
   }
   return sum;
 }
+constexpr float kLog2_127 = 6.98868468677216585f;  // log2(127)
 
 // O^T += (Vi^T . Pi^T) * f: lane (channel 32dt + col, half) takes keys
 // 32ks + 8i + 4half + j (i, j < 4) of the int8 V tile from two ds_read_tr8:
@@ -155,9 +158,9 @@ __device__ __forceinline__ void exact_softmax_pv(SoftmaxState& st, f32x16 (&s)[2
   if constexpr (INT8_PV) {
     const float beta = __builtin_amdgcn_exp2f(bmax - st.m);
     i32x4 pi[2];
-    float psum = probs_i8(s[0], qsl, -bmax, pi[0]);
-    psum += probs_i8(s[1], qsl, -bmax, pi[1]);
-    st.l = fmaf(st.l, alpha, beta * psum);
+    float psum = probs_i8(s[0], qsl, kLog2_127 - bmax, pi[0]);
+    psum += probs_i8(s[1], qsl, kLog2_127 - bmax, pi[1]);
+    st.l = fmaf(st.l, alpha, beta * (1.f / 127.f) * psum);
     rescale(st, alpha);
     pv_i8(static_cast<const char*>(vt), pi, beta * (1.f / 127.f), lane, st.acc);
   } else {
@@ -211,14 +214,14 @@ __device__ __forceinline__ void fast_step(SoftmaxState& st, f32x16 (&sc)[2], f32
       neg = -st.m;
     } else if (cc == 1) {
       if constexpr (INT8_PV) {
-        psum = probs_i8(sc[0], qsl, -bmax, pi[0]);
+        psum = probs_i8(sc[0], qsl, kLog2_127 - bmax, pi[0]);
       } else {
         psum = exp8<0>(sc[0], qsl, neg, pb[0], psum);
         psum = exp8<8>(sc[0], qsl, neg, pb[1], psum);
       }
     } else if (cc == 2) {
       if constexpr (INT8_PV) {
-        psum += probs_i8(sc[1], qsl, -bmax, pi[1]);
+        psum += probs_i8(sc[1], qsl, kLog2_127 - bmax, pi[1]);
       } else {
         psum = exp8<0>(sc[1], qsl, neg, pb[2], psum);
         psum = exp8<8>(sc[1], qsl, neg, pb[3], psum);
@@ -228,7 +231,7 @@ __device__ __forceinline__ void fast_step(SoftmaxState& st, f32x16 (&sc)[2], f32
   float beta = 1.f;
   if constexpr (INT8_PV) {
     beta = __builtin_amdgcn_exp2f(bmax - st.m);
-    st.l = fmaf(st.l, alpha, beta * psum);
+    st.l = fmaf(st.l, alpha, beta * (1.f / 127.f) * psum);
   } else {
     st.l = fmaf(st.l, alpha, psum);
   }
