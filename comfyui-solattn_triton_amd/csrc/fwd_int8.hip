@@ -181,12 +181,10 @@ __device__ __forceinline__ void exact_softmax_pv(SoftmaxState& st, f32x16 (&s)[2
 // Pipelined step over full exact tile n (scaled scores in sc): the i8 MFMAs
 // of S(n+1) from the K tile kn are interleaved with the softmax of tile n;
 // then P(n).V(n) and the conversion of S(n+1) into sn (ks of tile n+1 from kn).
-// With EARLY the conversion of S(n+1) runs before `mid` (a single K buffer is
-// refilled there); otherwise `mid` is empty and the conversion comes last.
-template <bool INT8_PV, bool EARLY, typename Mid>
+template <bool INT8_PV>
 __device__ __forceinline__ void fast_step(SoftmaxState& st, f32x16 (&sc)[2], f32x16 (&sn)[2],
                                           const char* kn, const void* vt, const i32x4 (&qi)[4],
-                                          float qsl, int lane, Mid&& mid) {
+                                          float qsl, int lane) {
   const int col = lane & 31, half = lane >> 5;
   const i32x16 zero = {};
   i32x16 si[2];
@@ -236,12 +234,7 @@ __device__ __forceinline__ void fast_step(SoftmaxState& st, f32x16 (&sc)[2], f32
     st.l = fmaf(st.l, alpha, psum);
   }
   rescale(st, alpha);
-  if constexpr (EARLY) {
-    scale_scores(kn, si, half, sn);
-    mid();
-    if constexpr (INT8_PV) pv_i8(static_cast<const char*>(vt), pi, beta * (1.f / 127.f), lane, st.acc);
-    else pv_tile(static_cast<const uint16_t*>(vt), pb, lane, st.acc);
-  } else if constexpr (INT8_PV) {
+  if constexpr (INT8_PV) {
     scale_scores(kn, si, half, sn);  // frees the int32 scores before the P.V accumulators
     pv_i8(static_cast<const char*>(vt), pi, beta * (1.f / 127.f), lane, st.acc);
   } else {
@@ -315,15 +308,14 @@ __device__ __forceinline__ void issue_i8(uint32_t dst, const int8_t* rows, const
   }
 }
 
-// NBUF = 2: double-buffered tiles (68 KB of LDS), two workgroups per CU: two
-// waves per SIMD at block 128, one (512 registers) at block 64. NBUF = 1
-// (block 64 with INT8 P.V): single-buffered, four workgroups and two waves per
-// SIMD, two waits per pipeline step. Block 64 with BF16 P.V stays
-// double-buffered: its single-buffered form spills in the step loop and ran
-// 1.5x slower.
-template <int BLK, bool INT8_PV, int NBUF>
+// K and V tiles double buffered. Block 128: 68 KB of LDS, two workgroups per
+// CU, two waves per SIMD. Block 64 with int8 P.V: packed int8 tiles (37 KB),
+// four workgroups per CU, two waves per SIMD. Block 64 with bf16 P.V: 68 KB,
+// two workgroups per CU, one wave per SIMD with 512 registers (its
+// single-buffered form spilled in the step loop and ran 1.5x slower).
+template <int BLK, bool INT8_PV>
 __global__ void __launch_bounds__(BLK * 2)
-__attribute__((amdgpu_waves_per_eu(BLK == 64 && NBUF == 2 ? 1 : 2)))
+__attribute__((amdgpu_waves_per_eu(BLK == 64 && !INT8_PV ? 1 : 2)))
 fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
                 const int8_t* __restrict__ qi, const float* __restrict__ qs,
                 const int8_t* __restrict__ ki, const float* __restrict__ ks,
@@ -334,10 +326,24 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
                 const uint32_t* __restrict__ mask, int T, int H, int NT, int W, float c,
                 uint16_t* __restrict__ o, int64_t so_b, int64_t so_t, int64_t so_h) {
   constexpr int NTHREADS = BLK * 2;
-  __shared__ __align__(256) uint16_t kbuf[NBUF][kTileElems];
-  __shared__ __align__(256) uint16_t vbuf[NBUF][kTileElems];
+  // LDS: exact-tile buffers K(i), V(i), i < 2. COMPACT (block 64, int8 P.V):
+  // the int8 tiles are packed (K + its ks: 8448 B, V: 8192 B), so two of each
+  // take 33 KB and four workgroups fit a CU; a bf16 pooled tile then spans
+  // K(0)-K(1) (or V(0)-V(1)) and the pooled tiles are single buffered.
+  constexpr int NBUF = 2;
+  constexpr bool COMPACT = BLK == 64 && INT8_PV;
+  constexpr int KSTRIDE = COMPACT ? kKsOffset + 256 : static_cast<int>(kTileBytes);
+  constexpr int VSTRIDE = COMPACT ? kKeys * kD : static_cast<int>(kTileBytes);
+  constexpr int VBASE = NBUF * KSTRIDE;
+  constexpr int PNBUF = COMPACT ? 1 : NBUF;  // buffers for pooled tiles
+  static_assert(!COMPACT || (2 * KSTRIDE >= static_cast<int>(kTileBytes) &&
+                             2 * VSTRIDE >= static_cast<int>(kTileBytes)), "pooled tile must fit");
+  __shared__ __align__(256) char arena[VBASE + NBUF * VSTRIDE];
   __shared__ TileList tl;
-  const auto bi = [](int n) { return NBUF == 2 ? (n & 1) : 0; };  // buffer of tile n
+  const auto Kp = [&](int i) { return reinterpret_cast<uint16_t*>(arena + i * KSTRIDE); };
+  const auto Vp = [&](int i) { return reinterpret_cast<uint16_t*>(arena + VBASE + i * VSTRIDE); };
+  const auto bi = [](int n) { return n & 1; };                      // buffer of exact tile n
+  const auto bp = [](int n) { return PNBUF == 2 ? (n & 1) : 0; };   // buffer of pooled tile n
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int col = lane & 31, half = lane >> 5;
@@ -369,9 +375,9 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
   const auto exact_tile = [&](int n) {
     return exact_desc<BLK>(tl, n < nrag ? nexact - 1 : n - nrag, T, NT);
   };
-  const uint32_t kb = lds_addr(kbuf[0]), vb = lds_addr(vbuf[0]);  // LDS byte addresses
-  const auto kbuf_at = [&](int buf) { return kb + buf * kTileBytes; };
-  const auto vbuf_at = [&](int buf) { return vb + buf * kTileBytes; };
+  const uint32_t kb = lds_addr(arena), vb = kb + VBASE;  // LDS byte addresses
+  const auto kbuf_at = [&](int buf) { return kb + buf * KSTRIDE; };
+  const auto vbuf_at = [&](int buf) { return vb + buf * VSTRIDE; };
   const auto issue_exact_full = [&](int n, uint32_t kd, uint32_t vd, bool with_k, bool with_v) {
     const int first = exact_first<BLK>(tl, n - nrag);
     if (with_k) issue_i8<NTHREADS, true, true>(kd, is.ki, is, first, kKeys, ioff.k, ioff.ks, false);
@@ -425,13 +431,12 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
     if (nrag) {
       wait_tile_copies();
       __syncthreads();
-      if constexpr (NBUF == 2) {
-        if (1 < ntiles) issue_tile(1, 1);
-      }
+      // a pooled tile 1 does not fit buffer 1 when COMPACT: the pooled phase issues it
+      if (1 < ntiles && (!COMPACT || 1 < nexact)) issue_tile(1, 1);
       const TileDesc td = exact_tile(0);
       i32x16 si[2];
       f32x16 s[2];
-      const char* kt = reinterpret_cast<const char*>(kbuf[0]);
+      const char* kt = reinterpret_cast<const char*>(Kp(0));
       qk_i8_tile(kt, qireg, col, half, si);
       scale_scores(kt, si, half, s);
 #pragma unroll
@@ -441,11 +446,8 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
         for (int r = 0; r < 16; ++r)
           s[m][r] = ((bits >> (8 * (r >> 2) + (r & 3))) & 1u) ? s[m][r] : -INFINITY;
       }
-      exact_softmax_pv<INT8_PV>(st, s, vbuf[0], qsl, lane);
+      exact_softmax_pv<INT8_PV>(st, s, Vp(0), qsl, lane);
       __syncthreads();
-      if constexpr (NBUF == 1) {
-        if (1 < ntiles) issue_tile(1, 0);
-      }
     }
     // full exact tiles, pipelined (tile F = nrag was issued into buffers bi(F))
     const int F = nrag;
@@ -458,46 +460,22 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
         qk_i8_tile(kt, qireg, col, half, si);
         scale_scores(kt, si, half, s);
       };
-      if constexpr (NBUF == 2) {
-        wait_tile_copies();
-        __syncthreads();
-        if (F + 1 < E)
-          issue_exact_full(F + 1, kbuf_at((F + 1) & 1), 0u, true, false);
-        qk_scaled(kbuf[F & 1], sa);
-        wait_tile_copies();
-        __syncthreads();  // kbuf[F & 1] is refilled (K of tile F+2) by the first step
-      } else {
-        wait_tile_copies();
-        __syncthreads();
-        qk_scaled(kbuf[0], sa);
-        __syncthreads();  // kbuf is free
-        if (F + 1 < E) issue_exact_full(F + 1, kbuf_at(0), 0u, true, false);
-        wait_tile_copies();
-        __syncthreads();  // K(F+1) and V(F) in LDS
-      }
+      wait_tile_copies();
+      __syncthreads();
+      if (F + 1 < E) issue_exact_full(F + 1, kbuf_at((F + 1) & 1), 0u, true, false);
+      qk_scaled(Kp(F & 1), sa);
+      wait_tile_copies();
+      __syncthreads();  // K(F & 1) is refilled (K of tile F+2) by the first step
       int n = F;
       // Step n needs n + 1 < E. K(n+2) of the last step is clamped to the
       // last full tile: a redundant copy into a buffer nothing reads afterwards.
       const auto step = [&](f32x16 (&sc)[2], f32x16 (&sn)[2]) {
-        if constexpr (NBUF == 2) {
-          issue_exact_full(min(n + 2, E - 1), kbuf_at(n & 1), 0u, true, false);
-          issue_exact_full(n + 1, 0u, vbuf_at((n + 1) & 1), false, true);
-          fast_step<INT8_PV, false>(st, sc, sn, reinterpret_cast<const char*>(kbuf[(n + 1) & 1]),
-                                    vbuf[n & 1], qireg, qsl, lane, [] {});
-          wait_tile_copies();
-          __syncthreads();
-        } else {
-          // On entry kbuf holds K(n+1), vbuf V(n) (copy possibly in flight).
-          fast_step<INT8_PV, true>(st, sc, sn, reinterpret_cast<const char*>(kbuf[0]), vbuf[0], qireg,
-                                   qsl, lane, [&] {
-                                     wait_tile_copies();  // V(n)
-                                     __syncthreads();     // every wave is done with K(n+1), ks(n+1)
-                                     issue_exact_full(min(n + 2, E - 1), kbuf_at(0), 0u, true, false);
-                                   });
-          wait_tile_copies();  // K(n+2)
-          __syncthreads();     // every wave is done with V(n)
-          issue_exact_full(n + 1, 0u, vbuf_at(0), false, true);
-        }
+        issue_exact_full(min(n + 2, E - 1), kbuf_at(n & 1), 0u, true, false);
+        issue_exact_full(n + 1, 0u, vbuf_at((n + 1) & 1), false, true);
+        fast_step<INT8_PV>(st, sc, sn, reinterpret_cast<const char*>(Kp((n + 1) & 1)), Vp(n & 1),
+                           qireg, qsl, lane);
+        wait_tile_copies();
+        __syncthreads();
         ++n;
       };
       while (n + 2 < E) {
@@ -506,17 +484,9 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
       }
       if (n + 1 < E) {
         step(sa, sb);
-        if constexpr (NBUF == 1) {
-          wait_tile_copies();
-          __syncthreads();
-        }
-        exact_softmax_pv<INT8_PV>(st, sb, vbuf[bi(n)], qsl, lane);
+        exact_softmax_pv<INT8_PV>(st, sb, Vp(bi(n)), qsl, lane);
       } else {
-        if constexpr (NBUF == 1) {
-          wait_tile_copies();
-          __syncthreads();
-        }
-        exact_softmax_pv<INT8_PV>(st, sa, vbuf[bi(n)], qsl, lane);
+        exact_softmax_pv<INT8_PV>(st, sa, Vp(bi(n)), qsl, lane);
       }
       __syncthreads();
     }
@@ -543,18 +513,18 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
       if (qvalid) r = *reinterpret_cast<const uint4*>(qp + cc * 16);
       qreg[cc] = __builtin_bit_cast(bf16x8, r);
     }
-    if (nexact > 0) issue_tile(nexact, bi(nexact));  // every earlier copy has landed
+    if (nexact > 0) issue_tile(nexact, bp(nexact));  // every earlier copy has landed
     for (int n = nexact; n < ntiles; ++n) {
       wait_tile_copies();  // tile n: the only copies in flight
       __syncthreads();
-      if constexpr (NBUF == 2) {
+      if constexpr (PNBUF == 2) {
         if (n + 1 < ntiles) issue_tile(n + 1, (n + 1) & 1);
       }
       f32x16 s[2];
-      qk_tile(kbuf[bi(n)], qreg, col, half, s);
-      finish_tile<BLK>(st, s, vbuf[bi(n)], pooled_desc(tl, n - nexact, NT), c, lane, NT, T);
+      qk_tile(Kp(bp(n)), qreg, col, half, s);
+      finish_tile<BLK>(st, s, Vp(bp(n)), pooled_desc(tl, n - nexact, NT), c, lane, NT, T);
       __syncthreads();
-      if constexpr (NBUF == 1) {
+      if constexpr (PNBUF == 1) {
         if (n + 1 < ntiles) issue_tile(n + 1, 0);
       }
     }
@@ -571,7 +541,7 @@ void launch_i8(uint32_t grid, hipStream_t s, const uint16_t* q, int64_t sq_b, in
                int64_t npad, const int32_t* counts, const int16_t* lists, const uint32_t* mask,
                int T, int H, int NT, int W, float c, uint16_t* o, int64_t so_b, int64_t so_t,
                int64_t so_h) {
-  hipLaunchKernelGGL((fwd_int8_kernel<BLK, PV, (BLK == 64 && PV) ? 1 : 2>), dim3(grid), dim3(BLK * 2), 0, s, q, sq_b, sq_t,
+  hipLaunchKernelGGL((fwd_int8_kernel<BLK, PV>), dim3(grid), dim3(BLK * 2), 0, s, q, sq_b, sq_t,
                      sq_h, qi, qs, ki, ks, vi, vscale, v, sv_b, sv_t, sv_h, TP, kc, vc, npad,
                      counts, lists, mask, T, H, NT, W, c, o, so_b, so_t, so_h);
 }
