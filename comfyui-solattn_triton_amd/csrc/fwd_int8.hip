@@ -84,23 +84,25 @@ __device__ __forceinline__ void qk_i8_tile(const char* kt, const i32x4 (&qi)[4],
 // ---------------------------------------------------------- INT8 P . V path
 // p_e = exp2(s*qsl - bmax) in [0, 1] for the 16 scores of key tile m, codes
 // round(p_e * 127) (v_cvt_pk_u8_f32: nearest, ties to even) packed 4 per
-// dword in element order; returns the fp32 sum of p_e.
+// dword in element order; adds the 16 codes to csum (v_dot4_u32_u8 with
+// ones, exact), so the row sum is that of the quantised P the P.V MFMAs
+// multiply.
 // negb127 = log2(127) - (tile max): the exponent yields 127 * pe directly, so
-// the codes need no multiply; the returned row sum is 127 * sum(pe).
-__device__ __forceinline__ float probs_i8(const f32x16& s, float qsl, float negb127, i32x4& pi) {
-  float sum = 0.f;
+// the codes need no multiply.
+__device__ __forceinline__ uint32_t probs_i8(const f32x16& s, float qsl, float negb127, i32x4& pi,
+                                             uint32_t csum) {
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
     uint32_t d = 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const float pe127 = __builtin_amdgcn_exp2f(fmaf(s[4 * w + j], qsl, negb127));
-      sum += pe127;
       d = __builtin_amdgcn_cvt_pk_u8_f32(pe127, j, d);
     }
     pi[w] = static_cast<int>(d);
+    csum = __builtin_amdgcn_udot4(d, 0x01010101u, csum, false);
   }
-  return sum;
+  return csum;
 }
 constexpr float kLog2_127 = 6.98868468677216585f;  // log2(127)
 
@@ -158,9 +160,9 @@ __device__ __forceinline__ void exact_softmax_pv(SoftmaxState& st, f32x16 (&s)[2
   if constexpr (INT8_PV) {
     const float beta = __builtin_amdgcn_exp2f(bmax - st.m);
     i32x4 pi[2];
-    float psum = probs_i8(s[0], qsl, kLog2_127 - bmax, pi[0]);
-    psum += probs_i8(s[1], qsl, kLog2_127 - bmax, pi[1]);
-    st.l = fmaf(st.l, alpha, beta * (1.f / 127.f) * psum);
+    uint32_t csum = probs_i8(s[0], qsl, kLog2_127 - bmax, pi[0], 0u);
+    csum = probs_i8(s[1], qsl, kLog2_127 - bmax, pi[1], csum);
+    st.l = fmaf(st.l, alpha, beta * (1.f / 127.f) * static_cast<float>(csum));
     rescale(st, alpha);
     pv_i8(static_cast<const char*>(vt), pi, beta * (1.f / 127.f), lane, st.acc);
   } else {
@@ -190,6 +192,7 @@ __device__ __forceinline__ void fast_step(SoftmaxState& st, f32x16 (&sc)[2], f32
   i32x16 si[2];
   i32x4 ka[4][2];
   float mx = -INFINITY, alpha = 1.f, bmax = 0.f, neg = 0.f, psum = 0.f;
+  uint32_t csum = 0u;
   bf16x8 pb[4];
   i32x4 pi[2];
   ka[0][0] = ki_op(kn, 0, 0, col, half);
@@ -212,14 +215,14 @@ __device__ __forceinline__ void fast_step(SoftmaxState& st, f32x16 (&sc)[2], f32
       neg = -st.m;
     } else if (cc == 1) {
       if constexpr (INT8_PV) {
-        psum = probs_i8(sc[0], qsl, kLog2_127 - bmax, pi[0]);
+        csum = probs_i8(sc[0], qsl, kLog2_127 - bmax, pi[0], 0u);
       } else {
         psum = exp8<0>(sc[0], qsl, neg, pb[0], psum);
         psum = exp8<8>(sc[0], qsl, neg, pb[1], psum);
       }
     } else if (cc == 2) {
       if constexpr (INT8_PV) {
-        psum += probs_i8(sc[1], qsl, kLog2_127 - bmax, pi[1]);
+        csum = probs_i8(sc[1], qsl, kLog2_127 - bmax, pi[1], csum);
       } else {
         psum = exp8<0>(sc[1], qsl, neg, pb[2], psum);
         psum = exp8<8>(sc[1], qsl, neg, pb[3], psum);
@@ -229,7 +232,7 @@ __device__ __forceinline__ void fast_step(SoftmaxState& st, f32x16 (&sc)[2], f32
   float beta = 1.f;
   if constexpr (INT8_PV) {
     beta = __builtin_amdgcn_exp2f(bmax - st.m);
-    st.l = fmaf(st.l, alpha, beta * (1.f / 127.f) * psum);
+    st.l = fmaf(st.l, alpha, beta * (1.f / 127.f) * static_cast<float>(csum));
   } else {
     st.l = fmaf(st.l, alpha, psum);
   }
