@@ -396,6 +396,21 @@ def main():
                                                    args.steps, args.warmup), 4)
                            for t in (0.8, 0.9, 0.95)}
         line["torch_sdpa"] = torch_sdpa(q, k, v, dflops, max(3, args.steps // 4))
+        if cfg["morton"]:
+            # the whole node path on raster-order tokens: reorder q, k, v -> prep (+ quant)
+            # -> sparse forward -> inverse reorder of o (BASELINE config 4's pipeline)
+            mo = mods["_morton"]
+
+            def pipeline(fn):
+                qq, kk, vv = (mo.reorder_tokens(t, perm, dim=1) for t in (q, k, v))
+                return mo.reorder_tokens(fn(qq, kk, vv), inv, dim=1)
+
+            line["pipeline_ms"] = {
+                "bf16": round(time_cuda(lambda: pipeline(lambda a, b, c: sol_attn(a, b, c, tau=tau, block=block)),
+                                        args.steps, args.warmup), 4),
+                "int8_pv": round(time_cuda(lambda: pipeline(lambda a, b, c: i8(a, b, c, tau=tau, block=block)),
+                                           args.steps, args.warmup), 4),
+            }
     if not args.no_cpu:
         print("[bench] CPU baseline", file=sys.stderr, flush=True)
         line["cpu_baseline"] = cpu_baseline(cfg, q, k, v, args.cpu_budget)
