@@ -1,11 +1,14 @@
 // INT8 Sol-Attn forward on gfx950 MFMA (/root/reference/_int8_fwd.py:208-372).
 //
 // Exact tiles: S = int32(qi . ki) * (qs*c * ks) on v_mfma_i32_32x32x32_i8.
-//   INT8_PV: P is quantised per row against the tile's own max,
+//   INT8_PV: P is quantised per row against the max of its routed block,
 //     pe = exp2(s - bmax), code = round(pe * 127), and multiplied with
 //     per-channel int8 V on the i8 MFMA; the row factor beta/127 (beta =
-//     exp2(bmax - m)) is applied per tile, the channel scale vscale[d] once
-//     after the exact tiles (it is the same for every tile).
+//     exp2(bmax - m)) is applied per block, the channel scale vscale[d] once
+//     after the exact blocks (it is the same for every block). Block 64: the
+//     block is one 64-key tile (fwd_int8_kernel). Block 128:
+//     fwd_int8_b128_kernel works on whole 128-key blocks; the tiles of a
+//     ragged last block are quantised per 64-key tile.
 //   otherwise: P.V in bf16 against the bf16 V, as in the BF16 forward.
 // Pooled tiles run last in bf16 on the centred kc and vc. The online softmax
 // is exact under any tile order, up to fp32 rounding.
@@ -536,6 +539,342 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
   store_rows(st, o + b * so_b + h * so_h, so_t, qrow, T, half);
 }
 
+// ------------------------------------------- block 128 with int8 P.V
+// The unit of work is the routed block of 128 keys, as in the reference at
+// block 128 (/root/reference/_int8_fwd.py:333-353): P is quantised against the
+// row max over the whole block, and its 128 products per channel accumulate in
+// int32 before one conversion (half the conversions of two 64-key tiles).
+// K block in LDS: 128 int8 rows (XOR-swizzled as the tiles) with the 128 ks
+// behind them; V block: 128 int8 rows.
+constexpr int kBlkKsOffset = 2 * kKsOffset;            // 16384
+constexpr int kBlkKStride = kBlkKsOffset + 2 * 256;    // + 128 ks = 16896
+constexpr int kBlkVStride = 2 * kKsOffset;             // 16384
+
+// int8 rows [first, first + 128) of ki (KS: with their ks) or vi into an LDS
+// block; 256 threads, four 16-byte copies per lane, each wave copying 32 ks.
+template <bool KS>
+__device__ __forceinline__ void issue_blk(uint32_t dst, const int8_t* rows, const I8Source& is,
+                                          int first, uint32_t off, uint32_t ks_off) {
+  const int wave = wave_id();
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const char* base = reinterpret_cast<const char*>(rows) + static_cast<int64_t>(first + 32 * u) * is.srow;
+    g2l16_s(base, off, dst + (wave * 64 + 256 * u) * 16);
+  }
+  if constexpr (KS) {
+    if ((threadIdx.x & 63) < 32)
+      g2l4_s(is.ks + static_cast<int64_t>(first) * is.H, ks_off, dst + kBlkKsOffset + 128 * wave);
+  }
+}
+
+// s[m][r] = int32 score * ks[key] for the four 32-key chunks of a block.
+__device__ __forceinline__ void scale_block(const char* kt, const i32x16 (&si)[4], int half,
+                                            f32x16 (&s)[4]) {
+  const float* ksl = reinterpret_cast<const float*>(kt + kBlkKsOffset);
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    if (m > 0) asm volatile("" ::: "memory");  // one chunk's ks loads at a time
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float4 k4 = *reinterpret_cast<const float4*>(ksl + 32 * m + 8 * i + 4 * half);
+      s[m][4 * i + 0] = static_cast<float>(si[m][4 * i + 0]) * k4.x;
+      s[m][4 * i + 1] = static_cast<float>(si[m][4 * i + 1]) * k4.y;
+      s[m][4 * i + 2] = static_cast<float>(si[m][4 * i + 2]) * k4.z;
+      s[m][4 * i + 3] = static_cast<float>(si[m][4 * i + 3]) * k4.w;
+    }
+  }
+}
+
+// s = int32 scores of 32-key chunk m * ks[key].
+__device__ __forceinline__ void scale_chunk(const char* kt, const i32x16& si, int m, int half, f32x16& s) {
+  const float* ksl = reinterpret_cast<const float*>(kt + kBlkKsOffset) + 32 * m + 4 * half;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float4 k4 = *reinterpret_cast<const float4*>(ksl + 8 * i);
+    s[4 * i + 0] = static_cast<float>(si[4 * i + 0]) * k4.x;
+    s[4 * i + 1] = static_cast<float>(si[4 * i + 1]) * k4.y;
+    s[4 * i + 2] = static_cast<float>(si[4 * i + 2]) * k4.z;
+    s[4 * i + 3] = static_cast<float>(si[4 * i + 3]) * k4.w;
+  }
+}
+
+// int32 scores of 32-key chunk m of a K block.
+__device__ __forceinline__ i32x16 qk_chunk(const char* kt, const i32x4 (&qi)[4], int m, int col,
+                                           int half) {
+  const i32x16 zero = {};
+  i32x16 si;
+#pragma unroll
+  for (int cc = 0; cc < 4; ++cc) si = mfma_i8(ki_op(kt, m, cc, col, half), qi[cc], cc == 0 ? zero : si);
+  return si;
+}
+
+// O^T += (Vi^T . Pi^T) * f over the 128 keys of a block (4 MFMAs per channel
+// tile into one int32 accumulator); lane layout as pv_i8.
+template <typename Mid>
+__device__ __forceinline__ void pv_blk(const char* vt, const i32x4 (&pi)[4], float f, int lane,
+                                       f32x16 (&acc)[4], Mid&& mid) {
+  const i32x16 zero = {};
+  const int g = lane >> 4, sl = lane & 15, half = lane >> 5;
+  const int kk = sl >> 1;
+  const int key_in = 8 * (kk >> 2) + 4 * half + (kk & 3);
+  const auto tile = [&](int dt) {
+    const int chunk = 2 * dt + (g & 1);
+    i32x16 pv;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int r0 = 32 * ks + key_in, r1 = r0 + 16;
+      const i32x2 lo = tr8(vt + r0 * kI8Row + swz_vi(r0, chunk) * 16 + 8 * (sl & 1));
+      const i32x2 hi = tr8(vt + r1 * kI8Row + swz_vi(r1, chunk) * 16 + 8 * (sl & 1));
+      const i32x4 a = {lo[0], lo[1], hi[0], hi[1]};
+      pv = mfma_i8(a, pi[ks], ks == 0 ? zero : pv);
+    }
+    return pv;
+  };
+#ifdef BLK_PV_PIPE
+  i32x16 pv[2];
+  pv[0] = tile(0);
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) {
+    if (dt + 1 < 4) pv[(dt + 1) & 1] = tile(dt + 1);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[dt][r] = fmaf(static_cast<float>(pv[dt & 1][r]), f, acc[dt][r]);
+    asm volatile("" : "+v"(acc[dt]));
+  }
+#else
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) {
+    const i32x16 pv = tile(dt);
+    mid(dt);  // independent VALU work beside this tile's MFMAs
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[dt][r] = fmaf(static_cast<float>(pv[r]), f, acc[dt][r]);
+    asm volatile("" : "+v"(acc[dt]));
+  }
+#endif
+}
+
+// Block step: the i8 MFMAs of S(b+1) (chunk 0 beside the row max of block b,
+// chunks 1-2 beside its P codes), then P(b).V(b) and the conversion of
+// S(b+1) into scaled scores while block b+1's ks are in LDS. QK = false: the
+// last block (softmax and P.V only).
+template <bool QK>
+__device__ __forceinline__ void block_step(SoftmaxState& st, const f32x16 (&sc)[4], f32x16 (&sn)[4],
+                                           const char* kn, const char* vt, const i32x4 (&qi)[4],
+                                           float qsl, int lane) {
+  const int col = lane & 31, half = lane >> 5;
+  i32x16 si[4];
+  i32x4 pi[4];
+  float mx = -INFINITY, alpha = 1.f, bmax = 0.f;
+  uint32_t csum = 0u;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    // the K operand reads of chunk m stay behind the work of slot m - 1, so
+    // at most two chunks of S(b+1) are live beside S(b)
+    if (m > 0) asm volatile("" ::: "memory");
+    if constexpr (QK) si[m] = qk_chunk(kn, qi, m, col, half);
+    if (m == 0) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[j][r]);
+      bmax = xhalf_max(mx) * qsl;
+      st.m = new_max(st.m, bmax, alpha);
+    } else if (m < 3) {
+      // codes of chunks 2(m-1), 2(m-1)+1; the empty asm keeps them in this
+      // slot, so S(b) dies while S(b+1) accumulates
+      const int j0 = 2 * (m - 1);
+      csum = probs_i8(sc[j0], qsl, kLog2_127 - bmax, pi[j0], csum);
+      csum = probs_i8(sc[j0 + 1], qsl, kLog2_127 - bmax, pi[j0 + 1], csum);
+      asm volatile("" : "+v"(pi[j0]), "+v"(pi[j0 + 1]), "+v"(csum));
+    }
+  }
+  const float beta = __builtin_amdgcn_exp2f(bmax - st.m);
+  st.l = fmaf(st.l, alpha, beta * (1.f / 127.f) * static_cast<float>(csum));
+  rescale(st, alpha);
+  // P(b).V(b); chunk dt of S(b+1) is scaled beside channel tile dt's MFMAs
+  pv_blk(vt, pi, beta * (1.f / 127.f), lane, st.acc, [&](int dt) {
+    if constexpr (QK) {
+      scale_chunk(kn, si[dt], dt, half, sn[dt]);
+      asm volatile("" : "+v"(sn[dt]));
+    }
+  });
+}
+
+// Block 128, int8 P.V: full exact blocks pipelined (step b: copies of K(b+2)
+// and V(b+1); S(b+1) beside the softmax of block b; P(b).V(b)), then the
+// tiles of a ragged last block (plain, per 64-key tile), the V channel scale,
+// then the pooled tiles in bf16. K and V blocks double buffered: 65 KB of
+// LDS, two workgroups per CU, two waves per SIMD.
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+fwd_int8_b128_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
+                     const int8_t* __restrict__ qi, const float* __restrict__ qs,
+                     const int8_t* __restrict__ ki, const float* __restrict__ ks,
+                     const int8_t* __restrict__ vi, const float* __restrict__ vscale,
+                     int64_t TP, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
+                     int64_t npad, const int32_t* __restrict__ counts,
+                     const int16_t* __restrict__ lists, const uint32_t* __restrict__ mask, int T,
+                     int H, int NT, int W, float c, uint16_t* __restrict__ o, int64_t so_b,
+                     int64_t so_t, int64_t so_h) {
+  constexpr int BLK = 128, NTHREADS = 256;
+  __shared__ __align__(256) char arena[2 * kBlkKStride + 2 * kBlkVStride];
+  __shared__ TileList tl;
+  const auto Kp = [&](int i) { return arena + i * kBlkKStride; };
+  const auto Vp = [&](int i) { return arena + 2 * kBlkKStride + i * kBlkVStride; };
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int col = lane & 31, half = lane >> 5;
+  int bh, qb;
+  tile_coords(blockIdx.x, gridDim.x, NT, bh, qb);
+  const int b = bh / H, h = bh % H;
+  const int64_t row = static_cast<int64_t>(bh) * NT + qb;
+
+  const int ntiles = build_tile_list<BLK>(tl, counts, lists, mask, row, NT, W, T);
+  if (ntiles == 0) return;  // cannot happen for routed lists: the diagonal is exact
+  const int nexact = tl.nexact;  // exact 64-key tiles, list order
+  const int cnt = min(max(counts[row], 0), NT);
+  // full exact blocks: list entries [0, nfb); a ragged last block (T not a
+  // multiple of 128) keeps its tiles [2 nfb, nexact) for the plain path
+  const int nfb = cnt - ((cnt > 0 && tl.blist[cnt - 1] == NT - 1 && (T % BLK) != 0) ? 1 : 0);
+
+  const int64_t bhD = (static_cast<int64_t>(b) * npad * H + h) * kD;
+  const KVSource src{nullptr, 0, nullptr, 0, kc + bhD, static_cast<int64_t>(H) * kD, vc + bhD};
+  const I8Source is{ki + (static_cast<int64_t>(b) * TP * H + h) * kD,
+                    ks + static_cast<int64_t>(b) * TP * H + h,
+                    vi + (static_cast<int64_t>(b) * TP * H + h) * kD,
+                    static_cast<int64_t>(H) * kD, H};
+  I8Offsets<NTHREADS> ioff;
+  ioff.init(is.srow, H);
+  const uint32_t ks_blk = static_cast<uint32_t>((32 * wave + lane) * H * 4);
+  const uint32_t kb = lds_addr(arena);
+  const auto kbuf_at = [&](int i) { return kb + i * kBlkKStride; };
+  const auto vbuf_at = [&](int i) { return kb + 2 * kBlkKStride + i * kBlkVStride; };
+  const auto blk_first = [&](int e) { return __builtin_amdgcn_readfirstlane(tl.blist[e] * BLK); };
+  const auto issue_k = [&](int e, int i) { issue_blk<true>(kbuf_at(i), is.ki, is, blk_first(e), ioff.k, ks_blk); };
+  const auto issue_v = [&](int e, int i) { issue_blk<false>(vbuf_at(i), is.vi, is, blk_first(e), ioff.v, 0u); };
+
+  if (nfb > 0) {
+    issue_k(0, 0);
+    issue_v(0, 0);
+    if (nfb > 1) issue_k(1, 1);
+  }
+  const int qrow = qb * BLK + wave * 32 + col;
+  const bool qvalid = qrow < T;
+  SoftmaxState st;
+  st.init();
+
+  // ---- exact blocks and tiles (int8 Q: 16 VGPRs)
+  if (nexact > 0) {
+    i32x4 qireg[4];
+    float qsl = 0.f;
+    {
+      const int64_t qoff = (static_cast<int64_t>(b) * TP + qrow) * H + h;
+      const int8_t* qip = qi + qoff * kD + half * 16;
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc) {
+        uint4 r = make_uint4(0u, 0u, 0u, 0u);
+        if (qvalid) r = *reinterpret_cast<const uint4*>(qip + cc * 32);
+        qireg[cc] = __builtin_bit_cast(i32x4, r);
+      }
+      if (qvalid) qsl = qs[qoff] * c;
+    }
+    if (nfb > 0) {
+      f32x16 sa[4], sb[4];
+      wait_tile_copies();
+      __syncthreads();
+      {
+        i32x16 si[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) si[m] = qk_chunk(Kp(0), qireg, m, col, half);
+        scale_block(Kp(0), si, half, sa);
+      }
+      __syncthreads();  // K(0) is refilled (K of block 2) by the first step
+      int e = 0;
+      // Step e needs e + 1 < nfb; K(e+2) past the last block is clamped to it
+      // (a redundant copy into a buffer nothing reads afterwards).
+      const auto step = [&](const f32x16 (&sc)[4], f32x16 (&sn)[4]) {
+        issue_k(min(e + 2, nfb - 1), e & 1);
+        issue_v(e + 1, (e + 1) & 1);
+        block_step<true>(st, sc, sn, Kp((e + 1) & 1), Vp(e & 1), qireg, qsl, lane);
+        wait_tile_copies();
+        __syncthreads();
+        ++e;
+      };
+      while (e + 2 < nfb) {
+        step(sa, sb);
+        step(sb, sa);
+      }
+      f32x16 dummy[4];
+      if (e + 1 < nfb) {
+        step(sa, sb);
+        block_step<false>(st, sb, dummy, nullptr, Vp(e & 1), qireg, qsl, lane);
+      } else {
+        block_step<false>(st, sa, dummy, nullptr, Vp(e & 1), qireg, qsl, lane);
+      }
+      __syncthreads();
+    }
+    // tiles of a ragged last block: plain, masked, one at a time
+    for (int t = 2 * nfb; t < nexact; ++t) {
+      const TileDesc td = exact_desc<BLK>(tl, t, T, NT);
+      issue_i8<NTHREADS, false, true>(kbuf_at(0), is.ki, is, td.first, td.nvalid, 0, 0, false);
+      issue_i8<NTHREADS, false, false>(vbuf_at(0), is.vi, is, td.first, td.nvalid, 0, 0, true);
+      wait_tile_copies();
+      __syncthreads();
+      i32x16 si[2];
+      f32x16 s[2];
+      const char* kt = Kp(0);
+      qk_i8_tile(kt, qireg, col, half, si);
+      scale_scores(kt, si, half, s);
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        const uint32_t bits = static_cast<uint32_t>(td.amask >> (32 * m + 4 * half));
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          s[m][r] = ((bits >> (8 * (r >> 2) + (r & 3))) & 1u) ? s[m][r] : -INFINITY;
+      }
+      exact_softmax_pv<true>(st, s, Vp(0), qsl, lane);
+      __syncthreads();
+    }
+    // The per-channel V scale, common to every exact block; the empty asm
+    // keeps its 64 loads here.
+    const float* vsc = vscale + static_cast<int64_t>(bh) * kD;
+    asm volatile("" : "+s"(vsc));
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) st.acc[dt][r] *= vsc[32 * dt + 8 * (r >> 2) + 4 * half + (r & 3)];
+  }
+
+  // ---- pooled tiles (bf16 Q: 32 VGPRs), double buffered
+  if (nexact < ntiles) {
+    bf16x8 qreg[8];
+    const uint16_t* qp = q + b * sq_b + static_cast<int64_t>(qrow) * sq_t + h * sq_h + half * 8;
+#pragma unroll
+    for (int cc = 0; cc < 8; ++cc) {
+      uint4 r = make_uint4(0u, 0u, 0u, 0u);
+      if (qvalid) r = *reinterpret_cast<const uint4*>(qp + cc * 16);
+      qreg[cc] = __builtin_bit_cast(bf16x8, r);
+    }
+    const auto issue_pooled = [&](int p, int i) {
+      const TileDesc td = pooled_desc(tl, p, NT);
+      issue_generic<NTHREADS>(kbuf_at(i), 0, td, src);
+      issue_generic<NTHREADS>(vbuf_at(i), 1, td, src);
+    };
+    const int npool = ntiles - nexact;
+    issue_pooled(0, 0);  // every earlier copy has landed
+    for (int p = 0; p < npool; ++p) {
+      wait_tile_copies();  // pooled tile p: the only copies in flight
+      __syncthreads();
+      if (p + 1 < npool) issue_pooled(p + 1, (p + 1) & 1);
+      f32x16 s[2];
+      qk_tile(reinterpret_cast<const uint16_t*>(Kp(p & 1)), qreg, col, half, s);
+      finish_tile<BLK>(st, s, reinterpret_cast<const uint16_t*>(Vp(p & 1)), pooled_desc(tl, p, NT), c,
+                       lane, NT, T);
+      __syncthreads();
+    }
+  }
+  wait_tile_copies();
+  store_rows(st, o + b * so_b + h * so_h, so_t, qrow, T, half);
+}
+
 template <int BLK, bool PV>
 void launch_i8(uint32_t grid, hipStream_t s, const uint16_t* q, int64_t sq_b, int64_t sq_t,
                int64_t sq_h, const int8_t* qi, const float* qs, const int8_t* ki, const float* ks,
@@ -592,7 +931,11 @@ extern "C" int solattn_fwd_int8(const uint16_t* q, int64_t sq_b, int64_t sq_t, i
       counts, lists, mask, static_cast<int>(T), static_cast<int>(H), static_cast<int>(NT), W, c, o, \
       so_b, so_t, so_h
   if (block == 128) {
-    if (int8_pv) int8fwd::launch_i8<128, true>(SOLATTN_I8_ARGS);
+    if (int8_pv)
+      hipLaunchKernelGGL(int8fwd::fwd_int8_b128_kernel, dim3(grid), dim3(256), 0, s, q, sq_b, sq_t,
+                         sq_h, qi, qs, ki, ks, vi, vscale, TP, kc, vc, npad, counts, lists, mask,
+                         static_cast<int>(T), static_cast<int>(H), static_cast<int>(NT), W, c, o,
+                         so_b, so_t, so_h);
     else int8fwd::launch_i8<128, false>(SOLATTN_I8_ARGS);
   } else {
     if (int8_pv) int8fwd::launch_i8<64, true>(SOLATTN_I8_ARGS);
