@@ -630,17 +630,6 @@ __device__ __forceinline__ void pv_blk(const char* vt, const i32x4 (&pi)[4], flo
     }
     return pv;
   };
-#ifdef BLK_PV_PIPE
-  i32x16 pv[2];
-  pv[0] = tile(0);
-#pragma unroll
-  for (int dt = 0; dt < 4; ++dt) {
-    if (dt + 1 < 4) pv[(dt + 1) & 1] = tile(dt + 1);
-#pragma unroll
-    for (int r = 0; r < 16; ++r) acc[dt][r] = fmaf(static_cast<float>(pv[dt & 1][r]), f, acc[dt][r]);
-    asm volatile("" : "+v"(acc[dt]));
-  }
-#else
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) {
     const i32x16 pv = tile(dt);
@@ -649,7 +638,6 @@ __device__ __forceinline__ void pv_blk(const char* vt, const i32x4 (&pi)[4], flo
     for (int r = 0; r < 16; ++r) acc[dt][r] = fmaf(static_cast<float>(pv[r]), f, acc[dt][r]);
     asm volatile("" : "+v"(acc[dt]));
   }
-#endif
 }
 
 // Block step: the i8 MFMAs of S(b+1) (chunk 0 beside the row max of block b,
