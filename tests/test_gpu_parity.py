@@ -110,6 +110,8 @@ FWD_CASES = [  # (B, T, H, block, tau, sink_kv, sink_q)
     (1, 4096, 2, 64, 1.5, (0, 0), (0, 0)),      # no ragged tile
     (2, 1000, 2, 64, 0.7, (0, 2), (0, 1)),      # sink blocks and sink query blocks
     (1, 3000, 2, 128, 1e30, (0, 0), (0, 0)),    # band only: pooled-heavy, 1-6 exact tiles per block
+    (1, 2048, 2, 128, 0.8, (0, 0), (0, 0)),     # block 128, T a multiple of 128: no ragged block
+    (1, 2112, 2, 128, 0.8, (0, 1), (0, 0)),     # block 128, last block of exactly 64 keys
 ]
 
 
