@@ -174,6 +174,32 @@ def test_fwd_int8_vs_port(pkg, dev, case, int8_pv):
     assert cos >= INT8_COS
 
 
+@pytest.mark.parametrize("block", [64, 128])
+def test_fwd_vs_dense_block_mask_diagnostic(pkg, dev, block):
+    """Dense SDPA restricted to the same block mask (the pooled term dropped),
+    the second comparison the task names. It is a diagnostic, not the
+    reference's output: the skipped blocks carry real mass, so the check is
+    only that both forwards sit much closer to their own closed form than to
+    the masked dense one; the gaps are printed."""
+    tri, i8 = _mods(pkg)[1], _mods(pkg)[2]
+    B, T, H, tau = 1, 2500, 2, 0.9
+    q, k, v = (randn_bf16((B, T, H, 128), s) for s in (60, 61, 62))
+    out = tri.sol_attn(q.to(dev), k.to(dev), v.to(dev), tau=tau, block=block)
+    out8 = i8.sol_attn_int8(q.to(dev), k.to(dev), v.to(dev), tau=tau, block=block)
+    torch.cuda.synchronize()
+    ref = oracle.prepare(bits(q), bits(k), bits(v), block=block, tau=tau)
+    rows = _rows(B, H, ref["NT"], limit=12)
+    masked = oracle.forward_dense_block_mask(bits(q), bits(k), bits(v), ref, rows)
+    port = oracle.forward_port(bits(q), bits(k), bits(v), ref, rows)
+    e_p, c_p = compare_rows(out.float().cpu().numpy(), port, block)
+    e_m, c_m = compare_rows(out.float().cpu().numpy(), masked, block)
+    e8, c8 = compare_rows(out8.float().cpu().numpy(), masked, block)
+    print(f"[masked dense] block={block} bf16 vs closed form max|err|={e_p:.3e} cos={c_p:.6f}; "
+          f"bf16 vs masked dense max|err|={e_m:.3e} cos={c_m:.6f}; int8 vs masked dense "
+          f"max|err|={e8:.3e} cos={c8:.6f}", flush=True)
+    assert e_p < e_m and c_p > c_m
+
+
 def test_strided_qkv_view(pkg, dev):
     """An interleaved qkv buffer goes in as strided views, no copies needed."""
     tri = _mods(pkg)[1]
