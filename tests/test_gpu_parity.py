@@ -176,11 +176,10 @@ def test_fwd_int8_vs_port(pkg, dev, case, int8_pv):
 
 @pytest.mark.parametrize("block", [64, 128])
 def test_fwd_vs_dense_block_mask_diagnostic(pkg, dev, block):
-    """Dense SDPA restricted to the same block mask (the pooled term dropped),
-    the second comparison the task names. It is a diagnostic, not the
-    reference's output: the skipped blocks carry real mass, so the check is
-    only that both forwards sit much closer to their own closed form than to
-    the masked dense one; the gaps are printed."""
+    """Dense SDPA restricted to the same block mask (the pooled term dropped).
+    A diagnostic, not the reference's output: the skipped blocks carry real
+    mass, so the check is only that the forward sits much closer to its own
+    closed form than to the masked dense one; both forwards' gaps are printed."""
     tri, i8 = _mods(pkg)[1], _mods(pkg)[2]
     B, T, H, tau = 1, 2500, 2, 0.9
     q, k, v = (randn_bf16((B, T, H, 128), s) for s in (60, 61, 62))
