@@ -58,6 +58,7 @@ struct TileDesc {
 // workgroup takes the query block whose rank is its place in the window. Same
 // L2 footprint, shorter tail per window (4-9% faster forwards at cfg 2).
 constexpr int kLptWindow = 64;
+static_assert((kLptWindow & (kLptWindow - 1)) == 0, "window offsets are taken with masks");
 __device__ __forceinline__ void tile_coords_lpt(const int32_t* __restrict__ counts, int NT, int& bh,
                                                 int& qb) {
   __shared__ int s_cnt[kLptWindow];
@@ -74,10 +75,12 @@ __device__ __forceinline__ void tile_coords_lpt(const int32_t* __restrict__ coun
     r = w & (kLptWindow - 1u);
     nwin = min(static_cast<uint32_t>(kLptWindow), total - base);
   }
-  const int t = threadIdx.x;
-  if (t < kLptWindow) s_cnt[t] = t < static_cast<int>(nwin) ? counts[base + t] : -1;
+  // Strided over the workgroup so that every window slot is filled and ranked
+  // whatever the thread count; exactly one slot has rank r, so s_pick is set.
+  for (int t = threadIdx.x; t < kLptWindow; t += blockDim.x)
+    s_cnt[t] = t < static_cast<int>(nwin) ? counts[base + t] : -1;
   __syncthreads();
-  if (t < static_cast<int>(nwin)) {
+  for (int t = threadIdx.x; t < static_cast<int>(nwin); t += blockDim.x) {
     const int mine = s_cnt[t];
     int rank = 0;
     for (int u = 0; u < static_cast<int>(nwin); ++u) {
