@@ -167,7 +167,7 @@ fwd_bf16_sbuf_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t,
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int col = lane & 31, half = lane >> 5;
   int bh, qb;
-  tile_coords_lpt(counts, NT, bh, qb);
+  tile_coords_lpt<kLptTokens / BLK>(counts, NT, bh, qb);
   const int b = bh / H, h = bh % H;
   const int64_t row = static_cast<int64_t>(bh) * NT + qb;
 
@@ -303,7 +303,7 @@ fwd_bf16_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int col = lane & 31, half = lane >> 5;
   int bh, qb;
-  tile_coords_lpt(counts, NT, bh, qb);
+  tile_coords_lpt<kLptTokens / BLK>(counts, NT, bh, qb);
   const int b = bh / H, h = bh % H;
   const int64_t row = static_cast<int64_t>(bh) * NT + qb;
 

@@ -52,32 +52,36 @@ struct TileDesc {
 // Workgroup -> (batch*head, query block). Workgroups are dealt round-robin to
 // the 8 XCDs; they are remapped so that each XCD walks a contiguous run of
 // query blocks of the same heads, which keeps their K/V blocks in that XCD's
-// L2. Within each window of kLptWindow consecutive dispatches on an XCD (the
-// query blocks that run there together) the query blocks are taken longest
-// first, by exact-block count: the window's counts are ranked in LDS and this
+// L2. Within each window of WIN consecutive dispatches on an XCD (the query
+// blocks that run there together) the query blocks are taken longest first,
+// by exact-block count: the window's counts are ranked in LDS and this
 // workgroup takes the query block whose rank is its place in the window. Same
-// L2 footprint, shorter tail per window (4-9% faster forwards at cfg 2).
-constexpr int kLptWindow = 64;
-static_assert((kLptWindow & (kLptWindow - 1)) == 0, "window offsets are taken with masks");
+// L2 footprint, shorter tail per window (4-9% faster forwards at cfg 2). A
+// window spans kLptTokens query tokens: 64 dispatches at block 128, 128 at
+// block 64 (a 128-dispatch window is 3-4% faster than 64 at block 64, and
+// 256 is slower at both sizes).
+constexpr int kLptTokens = 8192;
+template <int WIN>
 __device__ __forceinline__ void tile_coords_lpt(const int32_t* __restrict__ counts, int NT, int& bh,
                                                 int& qb) {
-  __shared__ int s_cnt[kLptWindow];
+  static_assert(WIN > 0 && (WIN & (WIN - 1)) == 0, "window offsets are taken with masks");
+  __shared__ int s_cnt[WIN];
   __shared__ int s_pick;
   const uint32_t w = blockIdx.x, total = gridDim.x;
   uint32_t base, r, nwin;
   if ((total & 7u) == 0u) {
     const uint32_t per = total >> 3, li = w >> 3;
-    base = (w & 7u) * per + (li & ~(kLptWindow - 1u));
-    r = li & (kLptWindow - 1u);
-    nwin = min(static_cast<uint32_t>(kLptWindow), per - (li & ~(kLptWindow - 1u)));
+    base = (w & 7u) * per + (li & ~(WIN - 1u));
+    r = li & (WIN - 1u);
+    nwin = min(static_cast<uint32_t>(WIN), per - (li & ~(WIN - 1u)));
   } else {
-    base = w & ~(kLptWindow - 1u);
-    r = w & (kLptWindow - 1u);
-    nwin = min(static_cast<uint32_t>(kLptWindow), total - base);
+    base = w & ~(WIN - 1u);
+    r = w & (WIN - 1u);
+    nwin = min(static_cast<uint32_t>(WIN), total - base);
   }
   // Strided over the workgroup so that every window slot is filled and ranked
   // whatever the thread count; exactly one slot has rank r, so s_pick is set.
-  for (int t = threadIdx.x; t < kLptWindow; t += blockDim.x)
+  for (int t = threadIdx.x; t < WIN; t += blockDim.x)
     s_cnt[t] = t < static_cast<int>(nwin) ? counts[base + t] : -1;
   __syncthreads();
   for (int t = threadIdx.x; t < static_cast<int>(nwin); t += blockDim.x) {

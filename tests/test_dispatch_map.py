@@ -2,7 +2,8 @@
 
 The forwards (``csrc/fwd_common.hpp``, ``tile_coords_lpt``) deal workgroups
 to XCDs round-robin, give each XCD a contiguous run of query blocks, and
-inside each window of 64 dispatches take the query blocks longest first. The
+inside each window of 8192 query tokens (64 dispatches at block 128, 128 at
+block 64) take the query blocks longest first. The
 mapping must be a permutation of ``[0, grid)`` for every grid size and every
 count pattern, or a query block is computed twice and another never (or an
 index leaves the buffers). This restates the index arithmetic step by step
@@ -13,10 +14,8 @@ tests only see for the grid sizes they run.
 import numpy as np
 import pytest
 
-WINDOW = 64
 
-
-def _mapping(counts, threads):
+def _mapping(counts, threads, WINDOW):
     total = len(counts)
     out = np.empty(total, dtype=np.int64)
     for w in range(total):
@@ -47,18 +46,19 @@ def _mapping(counts, threads):
 
 
 @pytest.mark.parametrize("total", [1, 7, 8, 24, 63, 64, 65, 200, 512, 520, 1031, 2048 + 8])
-@pytest.mark.parametrize("threads", [128, 256])
-def test_dispatch_map_is_permutation(total, threads):
+@pytest.mark.parametrize("threads,window", [(256, 64), (128, 128), (128, 64), (256, 128)])
+def test_dispatch_map_is_permutation(total, threads, window):
     rng = np.random.default_rng(total * 7 + threads)
     counts = rng.integers(0, 5, size=total).tolist()  # many ties
-    m = _mapping(counts, threads)
+    m = _mapping(counts, threads, window)
     assert sorted(m.tolist()) == list(range(total))
 
 
-def test_dispatch_map_longest_first_within_window():
-    total = 8 * 128
+@pytest.mark.parametrize("threads,WINDOW", [(256, 64), (128, 128)])
+def test_dispatch_map_longest_first_within_window(threads, WINDOW):
+    total = 8 * 256
     counts = list(range(total))  # strictly increasing: every window reverses
-    m = _mapping(counts, 256)
+    m = _mapping(counts, threads, WINDOW)
     per = total // 8
     for xcd in range(8):
         for win in range(0, per, WINDOW):
