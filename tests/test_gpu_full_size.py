@@ -1,0 +1,114 @@
+"""GPU parity at the benchmark's full size (config 2: B=1, H=24, D=128,
+N=32760 from a 21x30x52 latent grid, Morton-reordered, tau 0.9; the same
+synthetic smooth-field inputs ``bench.py`` times), at block 128 (the
+benchmark's) and block 64.
+
+The permutation and the whole routing state (pooled keys, thresholds, counts,
+lists, bitmask) are compared with the oracle bit for bit over every head and
+query block; the forward outputs are compared with the oracle's restatement of
+the reference loop on a seeded sample of query blocks (the oracle is a scalar
+loop; 96 BF16 and 32 INT8 query blocks take seconds). The small-case tests
+cover ragged tails, sinks and edge sizes; these cover the sizes the kernels are measured at
+(grids of 6144 and 12288 workgroups, 256 and 512 blocks per head, the
+dispatch windows).
+"""
+
+import importlib
+
+import numpy as np
+import pytest
+import torch
+
+import bench
+import oracle
+from _util import bits, compare_rows, u32
+
+pytestmark = pytest.mark.gpu
+
+BF16_MAXABS, BF16_COS, INT8_COS = 2e-2, 0.9995, 0.999
+
+
+@pytest.fixture(scope="module")
+def video(pkg, dev):
+    """cfg 2 inputs, Morton-reordered on the GPU, plus their bf16 bits on the host."""
+    mort = importlib.import_module(f"{pkg.__name__}._morton")
+    cfg = dict(bench.CONFIGS[2])
+    print(f"[full size] cfg2 grid={cfg['grid']} H={cfg['H']}", flush=True)
+    q, k, v = bench.make_inputs(cfg, dev)
+    perm, inv = mort.morton_perm(cfg["grid"], dev, "3d")
+    ref_perm, ref_inv = oracle.morton_perm(cfg["grid"], "3d")
+    assert np.array_equal(perm.cpu().numpy(), ref_perm)
+    assert np.array_equal(inv.cpu().numpy(), ref_inv)
+    q, k, v = (mort.reorder_tokens(t, perm, dim=1) for t in (q, k, v))
+    torch.cuda.synchronize()
+    return cfg, (q, k, v), tuple(bits(t) for t in (q, k, v))
+
+
+def _route_equal(r, ref):
+    B, H, NT = ref["counts"].shape
+    assert np.array_equal(bits(r.kc), ref["kc"])
+    assert np.array_equal(bits(r.vc), ref["vc"])
+    assert np.array_equal(r.threshold.cpu().numpy().view(np.uint32), ref["thr"].view(np.uint32))
+    assert np.array_equal(r.counts.cpu().numpy(), ref["counts"])
+    assert np.array_equal(u32(r.mask), ref["mask"])
+    lists = r.lists.cpu().numpy()
+    n = ref["counts"]
+    valid = np.arange(NT)[None, None, None, :] < n[..., None]
+    assert np.array_equal(np.where(valid, lists, 0), np.where(valid, ref["lists"], 0))
+
+
+def _sample_rows(H, NT, n, seed):
+    rng = np.random.default_rng(seed)
+    picks = sorted(rng.choice(H * NT, n, replace=False))
+    return [(0, int(p) // NT, int(p) % NT) for p in picks]
+
+
+@pytest.mark.parametrize("block", [128, 64])
+def test_full_size_bf16(pkg, dev, video, block):
+    pre = importlib.import_module(f"{pkg.__name__}._preprocess")
+    tri = importlib.import_module(f"{pkg.__name__}._tri_fwd")
+    cfg, (q, k, v), (qb, kb, vb) = video
+    tau = cfg["tau"]
+    r = pre.route(q, k, v, scale=128 ** -0.5, tau=tau, block=block)
+    out = tri.sol_attn(q, k, v, tau=tau, block=block)
+    torch.cuda.synchronize()
+    ref = oracle.prepare(qb, kb, vb, block=block, tau=tau)
+    _route_equal(r, ref)
+    density = float(ref["counts"].sum()) / ref["counts"].size / ref["NT"]
+    print(f"[full size bf16 block {block}] routing bit-exact, exact-block density "
+          f"{density:.3f}", flush=True)
+    rows = _sample_rows(cfg["H"], ref["NT"], 96, seed=5)
+    port = oracle.forward_port(qb, kb, vb, ref, rows)
+    err, cos = compare_rows(out.float().cpu().numpy(), port, block)
+    print(f"[full size bf16 block {block}] {len(rows)} query blocks: max|err|={err:.3e} "
+          f"cos={cos:.6f}", flush=True)
+    assert err < BF16_MAXABS and cos >= BF16_COS
+
+
+@pytest.mark.parametrize("block", [128, 64])
+@pytest.mark.parametrize("int8_pv", [True, False])
+def test_full_size_int8(pkg, dev, video, int8_pv, block):
+    fp = importlib.import_module(f"{pkg.__name__}._fused_prep")
+    i8 = importlib.import_module(f"{pkg.__name__}._int8_fwd")
+    cfg, (q, k, v), (qb, kb, vb) = video
+    tau = cfg["tau"]
+    r, qi, qs, ki, ks, vi = fp.fused_preprocess_routing(q, k, v, tau=tau, scale=128 ** -0.5,
+                                                        block=block)
+    out = i8.forward_int8(q, v, r, qi, qs, ki, ks, vi, int8_pv=int8_pv)
+    torch.cuda.synchronize()
+    ref = oracle.prepare(qb, kb, vb, block=block, tau=tau, int8=True, int8_pv=int8_pv)
+    _route_equal(r, ref)
+    T = ref["T"]
+    assert np.array_equal(qi[:, :T].cpu().numpy(), ref["qi"][:, :T])
+    assert np.array_equal(ki[:, :T].cpu().numpy(), ref["ki"][:, :T])
+    assert np.array_equal(qs[:, :T].cpu().numpy().view(np.uint32), ref["qs"][:, :T].view(np.uint32))
+    assert np.array_equal(ks[:, :T].cpu().numpy().view(np.uint32), ref["ks"][:, :T].view(np.uint32))
+    if int8_pv:
+        assert np.array_equal(vi[:, :T].cpu().numpy(), ref["vi"][:, :T])
+    print(f"[full size int8 block {block} pv={int8_pv}] routing and codes bit-exact", flush=True)
+    rows = _sample_rows(cfg["H"], ref["NT"], 32, seed=6)
+    port = oracle.forward_int8_port(qb, vb, ref, rows, int8_pv=int8_pv)
+    err, cos = compare_rows(out.float().cpu().numpy(), port, block)
+    print(f"[full size int8 block {block} pv={int8_pv}] {len(rows)} query blocks: max|err|={err:.3e} "
+          f"cos={cos:.6f}", flush=True)
+    assert cos >= INT8_COS
