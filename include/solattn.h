@@ -153,7 +153,10 @@ int solattn_quant_v(const uint16_t* v, int64_t sv_b, int64_t sv_t, int64_t sv_h,
  * Sparse attention over exact blocks (flash attention on MFMA) plus the pooled
  * branch (one pooled key kc_j and value vc_j per approximate block, softmax
  * weight times len_j), one online softmax per query row.
- * counts/mask come from solattn_route. o: bf16, element (b, t, h, d) at
+ * counts/lists/mask come from solattn_route for the same B, T, H and block:
+ * the kernels clamp counts to [0, NT] but take list entries (block indices in
+ * [0, NT), ascending) and mask bits as given, so other contents read K/V rows
+ * outside the tensors. o: bf16, element (b, t, h, d) at
  * o + b*so_b + t*so_t + h*so_h + d; rows t >= T are not written.
  * Replaces: _forward_ptr + sol_attn, /root/reference/_tri_fwd.py:215-410. */
 int solattn_fwd_bf16(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
@@ -169,7 +172,8 @@ int solattn_fwd_bf16(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h
  * P per row against the block max (pe = exp2(s - rowmax_blk), code =
  * min(pe*127 + 0.5, 127)) and multiplies with vi, scaled by (beta/127)*vscale;
  * int8_pv == 0 runs P.V in bf16 against v. The pooled branch is BF16 as above
- * (q, kc, vc). qi/ki/vi int8 [B, TP, H, D]; qs/ks fp32 [B, TP, H].
+ * (q, kc, vc); routing inputs as for solattn_fwd_bf16. qi/ki/vi int8
+ * [B, TP, H, D]; qs/ks fp32 [B, TP, H].
  * Replaces: _forward_int8_ptr + sol_attn_int8, /root/reference/_int8_fwd.py:208-432. */
 int solattn_fwd_int8(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
                      const int8_t* qi, const float* qs, const int8_t* ki, const float* ks,
