@@ -28,12 +28,12 @@ pytestmark = pytest.mark.gpu
 BF16_MAXABS, BF16_COS, INT8_COS = 2e-2, 0.9995, 0.999
 
 
-@pytest.fixture(scope="module")
-def video(pkg, dev):
-    """cfg 2 inputs, Morton-reordered on the GPU, plus their bf16 bits on the host."""
+def _inputs(pkg, dev, config):
+    """Inputs of a bench config, Morton-reordered on the GPU, plus their bf16
+    bits on the host."""
     mort = importlib.import_module(f"{pkg.__name__}._morton")
-    cfg = dict(bench.CONFIGS[2])
-    print(f"[full size] cfg2 grid={cfg['grid']} H={cfg['H']}", flush=True)
+    cfg = dict(bench.CONFIGS[config])
+    print(f"[full size] cfg{config} grid={cfg['grid']} H={cfg['H']}", flush=True)
     q, k, v = bench.make_inputs(cfg, dev)
     perm, inv = mort.morton_perm(cfg["grid"], dev, "3d")
     ref_perm, ref_inv = oracle.morton_perm(cfg["grid"], "3d")
@@ -42,6 +42,11 @@ def video(pkg, dev):
     q, k, v = (mort.reorder_tokens(t, perm, dim=1) for t in (q, k, v))
     torch.cuda.synchronize()
     return cfg, (q, k, v), tuple(bits(t) for t in (q, k, v))
+
+
+@pytest.fixture(scope="module")
+def video(pkg, dev):
+    return _inputs(pkg, dev, 2)
 
 
 def _route_equal(r, ref):
@@ -112,3 +117,41 @@ def test_full_size_int8(pkg, dev, video, int8_pv, block):
     print(f"[full size int8 block {block} pv={int8_pv}] {len(rows)} query blocks: max|err|={err:.3e} "
           f"cos={cos:.6f}", flush=True)
     assert cos >= INT8_COS
+
+
+def test_full_size_long_video(pkg, dev):
+    """cfg 4 (B=1, H=40, N=75600 from 21x60x60, block 128: 591 blocks per head,
+    an 80-token last block, a grid of 23640 workgroups): routing bit-exact over
+    every query block, BF16 and INT8 (int8 P.V) forwards on sampled query
+    blocks, including the ragged last one, against the oracle loops."""
+    pre = importlib.import_module(f"{pkg.__name__}._preprocess")
+    tri = importlib.import_module(f"{pkg.__name__}._tri_fwd")
+    fp = importlib.import_module(f"{pkg.__name__}._fused_prep")
+    i8 = importlib.import_module(f"{pkg.__name__}._int8_fwd")
+    cfg, (q, k, v), (qb, kb, vb) = _inputs(pkg, dev, 4)
+    block, tau = cfg["block"], cfg["tau"]
+    r = pre.route(q, k, v, scale=128 ** -0.5, tau=tau, block=block)
+    out = tri.sol_attn(q, k, v, tau=tau, block=block)
+    torch.cuda.synchronize()
+    ref = oracle.prepare(qb, kb, vb, block=block, tau=tau)
+    _route_equal(r, ref)
+    NT = ref["NT"]
+    rows = _sample_rows(cfg["H"], NT, 32, seed=7) + [(0, 0, NT - 1), (0, cfg["H"] - 1, NT - 1)]
+    port = oracle.forward_port(qb, kb, vb, ref, rows)
+    err, cos = compare_rows(out.float().cpu().numpy(), port, block)
+    print(f"[full size cfg4 bf16] routing bit-exact; {len(rows)} query blocks: "
+          f"max|err|={err:.3e} cos={cos:.6f}", flush=True)
+    assert err < BF16_MAXABS and cos >= BF16_COS
+    del out, port, ref
+    r8, qi, qs, ki, ks, vi = fp.fused_preprocess_routing(q, k, v, tau=tau, scale=128 ** -0.5,
+                                                         block=block)
+    out8 = i8.forward_int8(q, v, r8, qi, qs, ki, ks, vi, int8_pv=True)
+    torch.cuda.synchronize()
+    ref8 = oracle.prepare(qb, kb, vb, block=block, tau=tau, int8=True, int8_pv=True)
+    _route_equal(r8, ref8)
+    rows8 = rows[::3] + rows[-2:]
+    port8 = oracle.forward_int8_port(qb, vb, ref8, rows8, int8_pv=True)
+    err8, cos8 = compare_rows(out8.float().cpu().numpy(), port8, block)
+    print(f"[full size cfg4 int8] routing bit-exact; {len(rows8)} query blocks: "
+          f"max|err|={err8:.3e} cos={cos8:.6f}", flush=True)
+    assert cos8 >= INT8_COS
