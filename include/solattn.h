@@ -168,12 +168,22 @@ int solattn_fwd_bf16(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h
                      uint16_t* o, int64_t so_b, int64_t so_t, int64_t so_h,
                      solattn_stream_t stream);
 
-/* INT8 exact branch: S = int32(qi . ki) * (qs * c) * ks; int8_pv != 0 quantises
- * P per row against the block max (pe = exp2(s - rowmax_blk), code =
- * min(pe*127 + 0.5, 127)) and multiplies with vi, scaled by (beta/127)*vscale;
- * int8_pv == 0 runs P.V in bf16 against v. The pooled branch is BF16 as above
- * (q, kc, vc); routing inputs as for solattn_fwd_bf16. qi/ki/vi int8
- * [B, TP, H, D]; qs/ks fp32 [B, TP, H].
+/* INT8 exact branch: S = int32(qi . ki) * (qs * c) * ks. int8_pv == 0 runs P.V
+ * in bf16 against v, with P rounded to bf16 as in solattn_fwd_bf16.
+ * int8_pv != 0 quantises P per row against the row max of each routed block:
+ *   code = v_cvt_pk_u8_f32(exp2(s + log2(127) - rowmax_blk))
+ * i.e. round to nearest, ties to even, of 127 * exp2(s - rowmax_blk) (at most
+ * 127 by construction); the products int32(code . vi) are scaled by
+ * (beta / 127) * vscale[d] with beta = exp2(rowmax_blk - m). The softmax
+ * denominator adds the integer codes themselves, times beta / 127, so it is
+ * the sum of the quantised P that the P.V multiplies.
+ * Deliberate departures from /root/reference/_int8_fwd.py:348-353, which
+ * rounds trunc(pe * 127 + 0.5) and sums the fp32 pe: the rounding rule and the
+ * code-sum denominator (both within the INT8 tolerance, cosine >= 0.999), and,
+ * at block 128, a ragged last block whose tiles take the max of each 64-key
+ * tile instead of the whole block's.
+ * The pooled branch is BF16 as above (q, kc, vc); routing inputs as for
+ * solattn_fwd_bf16. qi/ki/vi int8 [B, TP, H, D]; qs/ks fp32 [B, TP, H].
  * Replaces: _forward_int8_ptr + sol_attn_int8, /root/reference/_int8_fwd.py:208-432. */
 int solattn_fwd_int8(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
                      const int8_t* qi, const float* qs, const int8_t* ki, const float* ks,
