@@ -42,7 +42,13 @@ SIGNATURES = {
                                                            _p, _l, _l, _l, _p], _i),
     "solattn_sol_attn_int8": ([_p, _l, _l, _l] * 3 + [_l] * 5 + [_f, _f, _l, _l, _l, _l, _i, _p,
                                                                 _l, _p, _l, _l, _l, _p], _i),
+    "solattn_sol_attn_noalloc": ([_p, _l, _l, _l] * 3 + [_l] * 5 + [_f, _f, _l, _l, _l, _l,
+                                                                   _p, _l, _l, _l, _p], _i),
 }
+
+# Size of the per-device scratch array behind solattn_sol_attn_noalloc
+# (SOLATTN_NOALLOC_SCRATCH_BYTES).
+NOALLOC_SCRATCH_BYTES = 64 << 20
 
 
 def _load() -> ctypes.CDLL:

@@ -1,10 +1,13 @@
 // C ABI glue: thread-local error messages, the host-side Morton permutation,
 // and the one-call pipelines (pool -> moments -> route -> [quant] -> forward)
-// over a caller-owned workspace. The library allocates nothing.
+// over a caller-owned workspace, plus the BF16 pipeline over a fixed
+// per-device scratch array for callers that cannot allocate. The library
+// never calls an allocator.
 #include <stdarg.h>
 #include <stdio.h>
 
 #include <algorithm>
+#include <mutex>
 #include <numeric>
 #include <vector>
 
@@ -124,23 +127,19 @@ extern "C" int64_t solattn_sol_attn_workspace_bytes(int64_t B, int64_t T, int64_
   return Layout(B, T, H, D, block, int8 != 0).total;
 }
 
-extern "C" int solattn_sol_attn(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
-                                const uint16_t* k, int64_t sk_b, int64_t sk_t, int64_t sk_h,
-                                const uint16_t* v, int64_t sv_b, int64_t sv_t, int64_t sv_h,
-                                int64_t B, int64_t T, int64_t H, int64_t D, int64_t block,
-                                float scale, float tau, int64_t sink_kv_lo, int64_t sink_kv_hi,
-                                int64_t sink_q_lo, int64_t sink_q_hi, void* workspace,
-                                int64_t workspace_bytes, uint16_t* o, int64_t so_b, int64_t so_t,
-                                int64_t so_h, solattn_stream_t stream) {
-  clear_error();
-  SOLATTN_REQUIRE(B > 0 && T > 0 && H > 0 && block > 0, SOLATTN_EINVAL, "sol_attn: bad sizes");
-  const Layout L(B, T, H, D, block, false);
-  SOLATTN_REQUIRE(workspace && workspace_bytes >= L.total, SOLATTN_ESIZE,
-                  "sol_attn: workspace %lld < %lld bytes", (long long)workspace_bytes,
-                  (long long)L.total);
-  SOLATTN_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, SOLATTN_EINVAL,
-                  "sol_attn: workspace must be 256-byte aligned");
-  void* ws = workspace;
+namespace solattn {
+namespace {
+
+// pool -> moments -> route -> fwd_bf16 over the intermediates of `L` carved
+// out of ws (256-byte aligned, at least L.total bytes; nothing in it needs to
+// start zeroed: every byte a later stage reads is written by an earlier one).
+int run_bf16_pipeline(const Layout& L, void* ws, const uint16_t* q, int64_t sq_b, int64_t sq_t,
+                      int64_t sq_h, const uint16_t* k, int64_t sk_b, int64_t sk_t, int64_t sk_h,
+                      const uint16_t* v, int64_t sv_b, int64_t sv_t, int64_t sv_h, int64_t B,
+                      int64_t T, int64_t H, int64_t D, int64_t block, float scale, float tau,
+                      int64_t sink_kv_lo, int64_t sink_kv_hi, int64_t sink_q_lo,
+                      int64_t sink_q_hi, uint16_t* o, int64_t so_b, int64_t so_t, int64_t so_h,
+                      solattn_stream_t stream) {
   int rc = solattn_pool(q, sq_b, sq_t, sq_h, k, sk_b, sk_t, sk_h, v, sv_b, sv_t, sv_h, B, T, H, D,
                         block, at<uint16_t>(ws, L.kc), at<uint16_t>(ws, L.vc), L.npad,
                         at<float>(ws, L.qbar), nullptr, stream);
@@ -158,6 +157,94 @@ extern "C" int solattn_sol_attn(const uint16_t* q, int64_t sq_b, int64_t sq_t, i
                           at<int32_t>(ws, L.counts), at<int16_t>(ws, L.lists),
                           at<uint32_t>(ws, L.mask), B, T, H, D, block, scale, o, so_b, so_t, so_h,
                           stream);
+}
+
+// The allocation-free pipeline's intermediates: one fixed array per device,
+// loaded with the code object. In host code `scratch` names a host-side
+// stand-in, not device memory; only the address hipGetSymbolAddress returns
+// for the current device is ever handed to a kernel.
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+}  // namespace
+}  // namespace solattn
+
+static __device__ __align__(256) unsigned char scratch[SOLATTN_NOALLOC_SCRATCH_BYTES];
+
+namespace solattn {
+namespace {
+
+// This device's copy of `scratch`, looked up once per device (with that
+// device current) and kept for the life of the process.
+int scratch_for_current_device(void** out) {
+  int dev = -1;
+  const hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess)
+    return set_error(SOLATTN_ELAUNCH, "sol_attn_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+  SOLATTN_REQUIRE(dev >= 0 && dev < kMaxScratchDevices, SOLATTN_EUNSUPPORTED,
+                  "sol_attn_noalloc: device %d beyond the %d supported", dev, kMaxScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t r = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (r != hipSuccess || p == nullptr)
+      return set_error(SOLATTN_ELAUNCH, "sol_attn_noalloc: hipGetSymbolAddress(scratch): %s",
+                       hipGetErrorString(r));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return SOLATTN_OK;
+}
+
+}  // namespace
+}  // namespace solattn
+
+extern "C" int solattn_sol_attn(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
+                                const uint16_t* k, int64_t sk_b, int64_t sk_t, int64_t sk_h,
+                                const uint16_t* v, int64_t sv_b, int64_t sv_t, int64_t sv_h,
+                                int64_t B, int64_t T, int64_t H, int64_t D, int64_t block,
+                                float scale, float tau, int64_t sink_kv_lo, int64_t sink_kv_hi,
+                                int64_t sink_q_lo, int64_t sink_q_hi, void* workspace,
+                                int64_t workspace_bytes, uint16_t* o, int64_t so_b, int64_t so_t,
+                                int64_t so_h, solattn_stream_t stream) {
+  clear_error();
+  SOLATTN_REQUIRE(B > 0 && T > 0 && H > 0 && block > 0, SOLATTN_EINVAL, "sol_attn: bad sizes");
+  const Layout L(B, T, H, D, block, false);
+  SOLATTN_REQUIRE(workspace && workspace_bytes >= L.total, SOLATTN_ESIZE,
+                  "sol_attn: workspace %lld < %lld bytes", (long long)workspace_bytes,
+                  (long long)L.total);
+  SOLATTN_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, SOLATTN_EINVAL,
+                  "sol_attn: workspace must be 256-byte aligned");
+  return run_bf16_pipeline(L, workspace, q, sq_b, sq_t, sq_h, k, sk_b, sk_t, sk_h, v, sv_b, sv_t,
+                           sv_h, B, T, H, D, block, scale, tau, sink_kv_lo, sink_kv_hi, sink_q_lo,
+                           sink_q_hi, o, so_b, so_t, so_h, stream);
+}
+
+extern "C" int solattn_sol_attn_noalloc(const uint16_t* q, int64_t sq_b, int64_t sq_t,
+                                        int64_t sq_h, const uint16_t* k, int64_t sk_b,
+                                        int64_t sk_t, int64_t sk_h, const uint16_t* v,
+                                        int64_t sv_b, int64_t sv_t, int64_t sv_h, int64_t B,
+                                        int64_t T, int64_t H, int64_t D, int64_t block,
+                                        float scale, float tau, int64_t sink_kv_lo,
+                                        int64_t sink_kv_hi, int64_t sink_q_lo, int64_t sink_q_hi,
+                                        uint16_t* o, int64_t so_b, int64_t so_t, int64_t so_h,
+                                        solattn_stream_t stream) {
+  clear_error();
+  SOLATTN_REQUIRE(B > 0 && T > 0 && H > 0 && block > 0, SOLATTN_EINVAL,
+                  "sol_attn_noalloc: bad sizes");
+  const Layout L(B, T, H, D, block, false);
+  SOLATTN_REQUIRE(L.total <= SOLATTN_NOALLOC_SCRATCH_BYTES, SOLATTN_ESIZE,
+                  "sol_attn_noalloc: B=%lld T=%lld H=%lld block=%lld needs %lld bytes of "
+                  "intermediates, more than the %lld-byte scratch; use solattn_sol_attn with a "
+                  "workspace",
+                  (long long)B, (long long)T, (long long)H, (long long)block, (long long)L.total,
+                  (long long)SOLATTN_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if (int rc = scratch_for_current_device(&ws)) return rc;
+  return run_bf16_pipeline(L, ws, q, sq_b, sq_t, sq_h, k, sk_b, sk_t, sk_h, v, sv_b, sv_t, sv_h,
+                           B, T, H, D, block, scale, tau, sink_kv_lo, sink_kv_hi, sink_q_lo,
+                           sink_q_hi, o, so_b, so_t, so_h, stream);
 }
 
 extern "C" int solattn_sol_attn_int8(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h,

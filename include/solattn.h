@@ -224,6 +224,29 @@ int solattn_sol_attn_int8(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t
                           int64_t so_b, int64_t so_t, int64_t so_h,
                           solattn_stream_t stream);
 
+/* ------------------------------------------------ allocation-free BF16 --
+ * solattn_sol_attn without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops and
+ * harnesses that forbid hipMalloc). No counterpart in the reference: it exists
+ * for those callers only. The intermediates live in one fixed array of
+ * SOLATTN_NOALLOC_SCRATCH_BYTES per device (held from the library's first use
+ * on that device until the process ends); shapes whose intermediates exceed it
+ * (solattn_sol_attn_workspace_bytes(B, T, H, D, block, 0) >
+ * SOLATTN_NOALLOC_SCRATCH_BYTES) return SOLATTN_ESIZE. Every call on one
+ * device shares that array: calls that overlap on one device (different
+ * streams, or threads without ordering) race and must be serialised by the
+ * caller. Nothing in the array needs clearing between calls. Same arguments,
+ * results and errors as solattn_sol_attn otherwise; the device is the current
+ * one. Covers cfg-4-sized calls (B1 H40 T75600 at block 128). */
+#define SOLATTN_NOALLOC_SCRATCH_BYTES (64ll << 20)
+int solattn_sol_attn_noalloc(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
+                             const uint16_t* k, int64_t sk_b, int64_t sk_t, int64_t sk_h,
+                             const uint16_t* v, int64_t sv_b, int64_t sv_t, int64_t sv_h,
+                             int64_t B, int64_t T, int64_t H, int64_t D, int64_t block,
+                             float scale, float tau, int64_t sink_kv_lo, int64_t sink_kv_hi,
+                             int64_t sink_q_lo, int64_t sink_q_hi, uint16_t* o, int64_t so_b,
+                             int64_t so_t, int64_t so_h, solattn_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -63,6 +63,21 @@ def test_errors_are_reported(capi):
     assert rc == -4 and b"workspace" in L.solattn_last_error()
 
 
+def test_noalloc_rejects_oversize_before_device_work(capi):
+    """The allocation-free pipeline refuses shapes whose intermediates exceed
+    its fixed scratch, with SOLATTN_ESIZE, before it touches a device."""
+    L = capi.LIB
+    B, T, H, D, block = 1, 131072, 40, 128, 64
+    assert L.solattn_sol_attn_workspace_bytes(B, T, H, D, block, 0) > capi.NOALLOC_SCRATCH_BYTES
+    rc = L.solattn_sol_attn_noalloc(*([None, 0, 0, 0] * 3), B, T, H, D, block, 0.1, 1.0, 0, 0, 0,
+                                    0, None, 0, 0, 0, None)
+    assert rc == -4 and b"scratch" in L.solattn_last_error()
+    # cfg-4-sized calls fit
+    assert L.solattn_sol_attn_workspace_bytes(1, 75600, 40, 128, 128, 0) <= capi.NOALLOC_SCRATCH_BYTES
+    hdr = open(HEADER).read()
+    assert f"({capi.NOALLOC_SCRATCH_BYTES >> 20}ll << 20)" in hdr
+
+
 def test_workspace_bytes(capi):
     L = capi.LIB
     b0 = L.solattn_sol_attn_workspace_bytes(1, 32760, 24, 128, 128, 0)
