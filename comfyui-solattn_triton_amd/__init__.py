@@ -37,6 +37,7 @@ from ._dispatch import (  # noqa: F401  (re-exported API)
     parse_tau_profile,
     reset_sol_attn_stats,
     sol_attn_stats,
+    try_sparse_default,
 )
 
 try:
@@ -51,6 +52,86 @@ _BLOCK_CHOICES = ["64", "128"]
 
 
 if _COMFY_ERROR is None:
+
+    def _require_kernels(int8_qk):
+        if _sol_attn_kernel is None:
+            raise RuntimeError(f"Sol-Attn kernel unavailable: {_IMPORT_ERROR}")
+        if int8_qk and _sol_attn_int8_kernel is None:
+            raise RuntimeError(f"Sol-Attn INT8 kernel unavailable: {_INT8_IMPORT_ERROR}")
+
+    def _model_family(diffusion_model):
+        """'h3' (MiniMax-H3: rope_freqs + _forward), 'wan' (rope_encode + blocks) or None."""
+        if hasattr(diffusion_model, "rope_freqs") and hasattr(diffusion_model, "_forward"):
+            return "h3"
+        if hasattr(diffusion_model, "rope_encode") and hasattr(diffusion_model, "blocks"):
+            return "wan"
+        return None
+
+    def _install_reordering(diffusion_model, morton, sink_conditioning, block):
+        """Install the model's reorder hooks; True when tokens will be reordered.
+        H3's hooks also publish the video span the conditioning sink needs, so
+        they go in whenever the sink is on, reordering or not."""
+        family = _model_family(diffusion_model)
+        if family == "h3" and (morton or sink_conditioning != "off"):
+            from ._morton_h3 import install_h3_hooks
+            install_h3_hooks(diffusion_model, block=block)
+            return bool(morton)
+        if family == "wan" and morton:
+            from ._morton import install_wan_morton
+            install_wan_morton(diffusion_model)
+            return True
+        if morton:
+            logging.warning(f"[sol_attn] Morton reordering skipped: "
+                            f"{type(diffusion_model).__name__} is neither Wan-style nor "
+                            "MiniMax-H3. Sol-Attn itself still applies.")
+        return False
+
+    def _depth_controls(diffusion_model, dense_blocks, tau_profile, tau):
+        """(dense block set, {block: tau}) for this model, with the block-index
+        publisher installed when either is used."""
+        blocks = getattr(diffusion_model, "blocks", None)
+        count = 0 if blocks is None else len(blocks)
+        dense = parse_blocks(dense_blocks, count)
+        profile = parse_tau_profile(tau_profile or "", count)
+        if not (dense or profile):
+            return dense, profile
+        if not _install_block_index(diffusion_model):
+            logging.warning(f"[sol_attn] dense_blocks/tau_profile ignored: "
+                            f"{type(diffusion_model).__name__} has no .blocks list to index")
+            return frozenset(), {}
+        if dense:
+            logging.info(f"[sol_attn] keeping blocks {sorted(dense)} dense of {count}")
+        if profile:
+            by_level = {}
+            for index, level in profile.items():
+                by_level[level] = by_level.get(level, 0) + 1
+            summary = ", ".join(f"{level} on {n} block(s)" for level, n in sorted(by_level.items()))
+            logging.info(f"[sol_attn] per-block tau: {summary}; base {tau} elsewhere")
+        return dense, profile
+
+    def _is_self_attention_forward(key):
+        """Object-patch keys like 'diffusion_model.blocks.3.self_attn.forward'."""
+        if not key.endswith(".forward"):
+            return False
+        owner = key.rsplit(".", 2)[-2].lower()
+        return "attn" in owner and "cross" not in owner and owner != "attn2"
+
+    def _compose_object_patches(patched, diffusion_model):
+        """Gate every object-patched self-attention forward on the clone, and
+        hook the blocks so patches applied after this node compose too."""
+        keys = []
+        for key, forward in list(patched.object_patches.items()):
+            if not _is_self_attention_forward(key) or getattr(forward, "_uses_optimized_attention", False):
+                continue
+            module = patched.get_model_object(key[: -len(".forward")])
+            patched.add_object_patch(key, _compose_module_patch(module, forward))
+            keys.append(key)
+        if keys:
+            logging.info(f"[sol_attn] composed with {len(keys)} object-patched attention "
+                         f"forward(s) (e.g. {keys[0]})")
+        family = _model_family(diffusion_model)
+        if family is not None:
+            _install_compose_hooks(diffusion_model, "attn" if family == "h3" else "self_attn")
 
     class SolAttnPatch(io.ComfyNode):
         """The "Patch Sol-Attn" node (/root/reference/__init__.py:422-606)."""
@@ -120,95 +201,34 @@ if _COMFY_ERROR is None:
         def execute(cls, model, tau, start_percent, end_percent, min_tokens, int8_qk,
                     sink_conditioning, morton, morton_curve, dense_blocks, verbose,
                     tau_profile=None, use_tma=False, int8_pv=True, block_size="64") -> io.NodeOutput:
-            if _sol_attn_kernel is None:
-                raise RuntimeError(f"Sol-Attn kernel unavailable: {_IMPORT_ERROR}")
-            if int8_qk and _sol_attn_int8_kernel is None:
-                raise RuntimeError(f"Sol-Attn INT8 kernel unavailable: {_INT8_IMPORT_ERROR}")
+            _require_kernels(int8_qk)
             block = int(block_size)
-
             diffusion_model = model.get_model_object("diffusion_model")
-            is_h3 = hasattr(diffusion_model, "rope_freqs") and hasattr(diffusion_model, "_forward")
-            is_wan = hasattr(diffusion_model, "rope_encode") and hasattr(diffusion_model, "blocks")
+            reorder = _install_reordering(diffusion_model, morton, sink_conditioning, block)
+            dense, profile = _depth_controls(diffusion_model, dense_blocks, tau_profile, tau)
+            sampling = model.get_model_object("model_sampling")
+            window = (float(sampling.percent_to_sigma(start_percent)),
+                      float(sampling.percent_to_sigma(end_percent)))
 
-            # H3 publishes its segment layout from the same hooks Morton uses, so
-            # the conditioning sink needs them even when reordering is off.
-            reorder = False
-            if is_h3 and (morton or sink_conditioning != "off"):
-                from ._morton_h3 import install_h3_hooks
-                install_h3_hooks(diffusion_model, block=block)
-                reorder = morton
-            elif is_wan and morton:
-                from ._morton import install_wan_morton
-                install_wan_morton(diffusion_model)
-                reorder = True
-            elif morton:
-                logging.warning(f"[sol_attn] Morton reordering skipped: "
-                                f"{type(diffusion_model).__name__} is neither Wan-style nor "
-                                "MiniMax-H3. Sol-Attn itself still applies.")
-
-            blocks = getattr(diffusion_model, "blocks", None)
-            count = len(blocks) if blocks is not None else 0
-            dense = parse_blocks(dense_blocks, count)
-            profile = parse_tau_profile(tau_profile or "", count)
-            if (dense or profile) and not _install_block_index(diffusion_model):
-                logging.warning(f"[sol_attn] dense_blocks/tau_profile ignored: "
-                                f"{type(diffusion_model).__name__} has no .blocks list to index")
-                dense, profile = frozenset(), {}
-            if dense:
-                logging.info(f"[sol_attn] keeping blocks {sorted(dense)} dense of {count}")
-            if profile:
-                levels = {}
-                for blk, level in sorted(profile.items()):
-                    levels.setdefault(level, []).append(blk)
-                logging.info("[sol_attn] per-block tau: "
-                             + ", ".join(f"{lv} on {len(bs)} block(s)" for lv, bs in sorted(levels.items()))
-                             + f"; base {tau} elsewhere")
-
-            model_sampling = model.get_model_object("model_sampling")
-            sigma_start = float(model_sampling.percent_to_sigma(start_percent))
-            sigma_end = float(model_sampling.percent_to_sigma(end_percent))
-
-            m = model.clone()
-            options = m.model_options["transformer_options"]
+            patched = model.clone()
+            options = patched.model_options["transformer_options"]
             previous = options.get("optimized_attention_override")
             if previous is not None:
                 logging.info("[sol_attn] chaining onto an existing attention override; Sol-Attn "
                              "takes first refusal and delegates everything else to it")
-
-            # Forward-level patches bypass optimized_attention; gate each one.
-            composed = []
-            for key, patched in list(m.object_patches.items()):
-                if not key.endswith(".forward"):
-                    continue
-                owner = key.rsplit(".", 2)[-2].lower()
-                if "attn" not in owner or "cross" in owner or owner == "attn2":
-                    continue
-                if getattr(patched, "_uses_optimized_attention", False):
-                    continue
-                module = m.get_model_object(key[: -len(".forward")])
-                m.add_object_patch(key, _compose_module_patch(module, patched))
-                composed.append(key)
-            if composed:
-                logging.info(f"[sol_attn] composed with {len(composed)} object-patched attention "
-                             f"forward(s) (e.g. {composed[0]})")
-            if is_h3:
-                _install_compose_hooks(diffusion_model, "attn")
-            elif is_wan:
-                _install_compose_hooks(diffusion_model, "self_attn")
-
-            options["sol_compose"] = {"sigma_start": sigma_start, "sigma_end": sigma_end,
+            _compose_object_patches(patched, diffusion_model)
+            options["sol_compose"] = {"sigma_start": window[0], "sigma_end": window[1],
                                       "min_tokens": min_tokens}
             options["optimized_attention_override"] = make_override(
-                tau=tau, min_tokens=min_tokens, sigma_start=sigma_start, sigma_end=sigma_end,
+                tau=tau, min_tokens=min_tokens, sigma_start=window[0], sigma_end=window[1],
                 verbose=verbose, int8_qk=int8_qk, sink_conditioning=sink_conditioning,
                 use_tma=use_tma, dense_blocks=dense, tau_profile=profile, int8_pv=int8_pv,
                 previous=previous, block=block)
             options["sol_block_size"] = block
             if reorder:
-                options["sol_morton"] = True
-                options["sol_morton_curve"] = morton_curve
+                options.update(sol_morton=True, sol_morton_curve=morton_curve)
             reset_sol_attn_stats()
-            return io.NodeOutput(m)
+            return io.NodeOutput(patched)
 
     class SolAttnBlockProbe(io.ComfyNode):
         """Diagnostic node (/root/reference/__init__.py:609-646)."""
@@ -230,50 +250,51 @@ if _COMFY_ERROR is None:
 
         @classmethod
         def execute(cls, model) -> io.NodeOutput:
-            m = model.clone()
-            inner = m.model_options["transformer_options"].get("optimized_attention_override")
+            probed = model.clone()
+            options = probed.model_options["transformer_options"]
+            inner = options.get("optimized_attention_override")
             if inner is None:
                 raise RuntimeError("Sol-Attn Block Probe needs an attention override to measure; "
                                    "connect it after Patch Sol-Attn.")
-            diffusion_model = m.get_model_object("diffusion_model")
+            diffusion_model = probed.get_model_object("diffusion_model")
             if not _install_block_index(diffusion_model):
                 logging.warning(f"[sol_attn] probe: {type(diffusion_model).__name__} has no "
                                 ".blocks list, so every error lands under block 'None'")
-            m.model_options["transformer_options"]["optimized_attention_override"] = \
-                make_probe_override(inner)
+            options["optimized_attention_override"] = make_probe_override(inner)
             _probe.clear()
-            m.add_callback(CallbacksMP.ON_CLEANUP, log_probe_summary)
-            return io.NodeOutput(m)
+            probed.add_callback(CallbacksMP.ON_CLEANUP, log_probe_summary)
+            return io.NodeOutput(probed)
 
     @wrap_attn
     def attention_sol(q, k, v, heads, mask=None, attn_precision=None, skip_reshape=False,
                       skip_output_reshape=False, **kwargs):
-        """Registry entry point with the defaults (tau 1.0, min_tokens 4096, bf16,
-        no sigma window); /root/reference/__init__.py:649-663."""
-        if mask is None:
-            try:
-                out = _run(q, k, v, heads, skip_reshape, skip_output_reshape,
-                           kwargs.get("scale", None), 1.0, 4096, False)
-                if out is not None:
-                    return out
-            except Exception as exc:
-                _stats["errors"] += 1
-                from ._dispatch import _log_kernel_failure
-                _log_kernel_failure(exc)
+        """The "sol_attn" registry entry: the sparse path with the registry
+        defaults (tau 1.0, 4096 tokens, BF16, no sigma window), ComfyUI's
+        PyTorch attention otherwise (/root/reference/__init__.py:649-663)."""
+        out = try_sparse_default(q, k, v, heads, mask, skip_reshape, skip_output_reshape,
+                                 kwargs.get("scale"))
+        if out is not None:
+            return out
         return attention_pytorch(q, k, v, heads, mask=mask, skip_reshape=skip_reshape,
                                  skip_output_reshape=skip_output_reshape, **kwargs)
 
     register_attention_function("sol_attn", attention_sol)
 
-    if os.environ.get("SOL_ATTN", "0") not in ("0", "", "false"):
+    def _install_global_override(environ=os.environ):
+        """SOL_ATTN set (not '0', '' or 'false'): route every optimized
+        attention call through attention_sol, for CLI runs without the node."""
+        if environ.get("SOL_ATTN", "0") in ("0", "", "false"):
+            return False
         if _sol_attn_kernel is None:
             logging.error(f"[sol_attn] SOL_ATTN set but kernel import failed: {_IMPORT_ERROR}")
-        else:
-            import comfy.ldm.modules.attention as _attn_mod
+            return False
+        import comfy.ldm.modules.attention as attention_module
+        attention_module.optimized_attention = attention_sol
+        attention_module.optimized_attention_masked = attention_sol
+        logging.info("[sol_attn] global override active (node patch is preferred)")
+        return True
 
-            _attn_mod.optimized_attention = attention_sol
-            _attn_mod.optimized_attention_masked = attention_sol
-            logging.info("[sol_attn] global override active (node patch is preferred)")
+    _install_global_override()
 
     class SolAttnExtension(ComfyExtension):
         async def get_node_list(self):

@@ -22,13 +22,13 @@ from __future__ import annotations
 import ctypes
 import logging
 import math
+import weakref
 
 import torch
 
 from ._capi import LIB, SolAttnError, call, ptr, stream
 
 _PERM_CACHE: dict = {}
-_INSTALLED: set = set()
 
 __all__ = ["morton_perm", "reorder_tokens", "install_wan_morton"]
 
@@ -109,6 +109,75 @@ def reorder_tokens(x: torch.Tensor, index: torch.Tensor, dim: int = 1) -> torch.
     return out
 
 
+def _gather(x: torch.Tensor, index: torch.Tensor, dim: int) -> torch.Tensor:
+    """The hooks' row permutation: the gfx950 gather kernel."""
+    return reorder_tokens(x, index, dim=dim)
+
+
+class _WanReorder:
+    """Reorder state of one Wan-style model for one forward pass.
+
+    The block-0 pre-hook is the only place that decides (it holds the hidden
+    states and the RoPE table together): if the tokens are exactly the video
+    grid, both are permuted there, later blocks get the permuted table, and the
+    last block's output is put back in raster order. Any mismatch (reference
+    latents prepended, context latents appended) leaves the pass untouched.
+    """
+
+    installed = weakref.WeakSet()  # models with the hooks
+
+    def __init__(self, model):
+        self.first = model.blocks[0]
+        self.inverse = None  # set while a permuted pass is in flight
+        self.freqs = None
+
+    def _plan(self, x, freqs, options):
+        """(perm, inverse) when this pass can be reordered, else None (logged once)."""
+        grid = options.get("grid_sizes")
+        if grid is None:
+            _log_once("transformer_options has no grid_sizes; inactive")
+            return None
+        tokens = math.prod(int(g) for g in grid)
+        if not (torch.is_tensor(x) and x.ndim == 3 and x.shape[1] == tokens):
+            shape = tuple(x.shape) if torch.is_tensor(x) else type(x).__name__
+            _log_once(f"token count {shape} != video grid {tuple(grid)} ({tokens}); "
+                      "reference/context streams present, inactive")
+            return None
+        if not (torch.is_tensor(freqs) and freqs.ndim >= 2 and freqs.shape[1] == tokens):
+            shape = tuple(freqs.shape) if torch.is_tensor(freqs) else type(freqs).__name__
+            _log_once(f"rope table {shape} does not match the video grid ({tokens}); inactive")
+            return None
+        return morton_perm(grid, x.device, options.get("sol_morton_curve", "3d"))
+
+    def before_block(self, module, args, kwargs):
+        options = kwargs.get("transformer_options") or {}
+        if module is self.first:
+            self.inverse = self.freqs = None
+            if not options.get("sol_morton") or not args:
+                return None
+            plan = self._plan(args[0], kwargs.get("freqs"), options)
+            if plan is None:
+                return None
+            perm, self.inverse = plan
+            self.freqs = _gather(kwargs["freqs"], perm, 1)
+            return (_gather(args[0], perm, 1),) + tuple(args[1:]), {**kwargs, "freqs": self.freqs}
+        if self.inverse is None:
+            return None
+        # hidden states are already in Morton order; only the table is swapped in
+        return tuple(args), {**kwargs, "freqs": self.freqs}
+
+    def after_stack(self, _module, _args, _kwargs, output):
+        inverse, self.inverse, self.freqs = self.inverse, None, None
+        if inverse is None:
+            return None
+        if not (torch.is_tensor(output) and output.ndim >= 2 and output.shape[1] == inverse.numel()):
+            shape = tuple(output.shape) if torch.is_tensor(output) else type(output).__name__
+            logging.error(f"[sol_attn] Wan Morton: block stack changed the token count ({shape}); "
+                          "cannot restore order")
+            return None
+        return _gather(output, inverse, 1)
+
+
 _logged: set = set()
 
 
@@ -119,69 +188,15 @@ def _log_once(message):
 
 
 def install_wan_morton(diffusion_model):
-    """Idempotently install the reorder hooks (/root/reference/_morton.py:85-153).
-    Inert unless transformer_options["sol_morton"] is set."""
-    if id(diffusion_model) in _INSTALLED:
+    """Install the reorder hooks on a Wan-style model, once per model
+    (/root/reference/_morton.py:85-153). Inert unless
+    transformer_options["sol_morton"] is set for the pass."""
+    if diffusion_model in _WanReorder.installed:
         return
     if not hasattr(diffusion_model, "blocks"):
         raise RuntimeError("Morton reordering needs .blocks on the diffusion model")
-
-    model = diffusion_model
-    blocks = model.blocks
-    first, last = blocks[0], blocks[-1]
-
-    def _decide(x, freqs, transformer_options):
-        """(perm, inverse, permuted_freqs) or None: the single decision point."""
-        grid = transformer_options.get("grid_sizes")
-        if grid is None:
-            _log_once("transformer_options has no grid_sizes; inactive")
-            return None
-        tokens = int(math.prod(int(g) for g in grid))
-        if not torch.is_tensor(x) or x.ndim != 3 or x.shape[1] != tokens:
-            _log_once(f"token count {tuple(x.shape)} != video grid {tuple(grid)} "
-                      f"({tokens}); reference/context streams present, inactive")
-            return None
-        if not torch.is_tensor(freqs) or freqs.ndim < 2 or freqs.shape[1] != tokens:
-            _log_once(f"rope table {tuple(freqs.shape) if torch.is_tensor(freqs) else type(freqs)} "
-                      f"does not match the video grid ({tokens}); inactive")
-            return None
-        curve = transformer_options.get("sol_morton_curve", "3d")
-        perm, inverse = morton_perm(grid, x.device, curve)
-        return perm, inverse, reorder_tokens(freqs, perm, dim=1)
-
-    def pre_hook(module, args, kwargs):
-        transformer_options = kwargs.get("transformer_options") or {}
-        if not transformer_options.get("sol_morton") or not args:
-            return None
-        if module is first:
-            model._sol_morton_state = None
-            decision = _decide(args[0], kwargs.get("freqs"), transformer_options)
-            if decision is None:
-                return None
-            perm, inverse, freqs = decision
-            model._sol_morton_state = (perm, inverse, freqs)
-            kwargs = {**kwargs, "freqs": freqs}
-            return (reorder_tokens(args[0], perm, dim=1),) + tuple(args[1:]), kwargs
-        # Later blocks reuse the permuted rope table; hidden states flow through.
-        state = getattr(model, "_sol_morton_state", None)
-        if state is None:
-            return None
-        return args, {**kwargs, "freqs": state[2]}
-
-    def post_hook(_module, _args, _kwargs, output):
-        state = getattr(model, "_sol_morton_state", None)
-        if state is None:
-            return None
-        model._sol_morton_state = None
-        _perm, inverse, _freqs = state
-        if not torch.is_tensor(output) or output.ndim < 2 or output.shape[1] != inverse.numel():
-            logging.error("[sol_attn] Wan Morton: block stack changed the token count "
-                          f"({tuple(output.shape) if torch.is_tensor(output) else type(output)}); "
-                          "cannot restore order")
-            return None
-        return reorder_tokens(output, inverse, dim=1)
-
-    for block in blocks:
-        block.register_forward_pre_hook(pre_hook, with_kwargs=True)
-    last.register_forward_hook(post_hook, with_kwargs=True)
-    _INSTALLED.add(id(diffusion_model))
+    state = _WanReorder(diffusion_model)
+    for block in diffusion_model.blocks:
+        block.register_forward_pre_hook(state.before_block, with_kwargs=True)
+    diffusion_model.blocks[-1].register_forward_hook(state.after_stack, with_kwargs=True)
+    _WanReorder.installed.add(diffusion_model)
