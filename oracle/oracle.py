@@ -305,10 +305,21 @@ def forward_port(q, k, v, prep, rows, group: int = 64, round_p: bool = True):
     return out
 
 
-def forward_int8_port(q, v, prep, rows, int8_pv: bool = True, group: int = 64):
+def forward_int8_port(q, v, prep, rows, int8_pv: bool = True, group: int = 64,
+                      codes: str = "reference"):
     """The reference's INT8 forward loop, /root/reference/_int8_fwd.py:242-372:
     BF16 routing and pooled branch on centred kc; exact branch from qi/qs, ki/ks
-    (int32 dot), P.V in int8 against the block max (int8_pv) or in bf16."""
+    (int32 dot), P.V in int8 against the block max (int8_pv) or in bf16.
+
+    ``codes`` selects the int8 P.V arithmetic:
+      "reference": pi = trunc(min(pe*127 + 0.5, 127)), row sum += beta * sum(pe)
+                   (/root/reference/_int8_fwd.py:348-353);
+      "kernel":    pi = round-half-even(exp2(s + log2(127) - bm)), row sum +=
+                   beta/127 * sum(pi), and at block 128 a ragged last block of
+                   more than 64 keys quantised per 64-key tile, each against its
+                   own max -- the HIP kernel's documented departure (the softmax
+                   denominator is that of the quantised P the P.V multiplies)."""
+    assert codes in ("reference", "kernel")
     block, T, NT = prep["block"], prep["T"], prep["NT"]
     D = q.shape[3]
     c = np.float32(np.float32(prep["scale"]) * np.float32(LOG2E))
@@ -352,32 +363,43 @@ def forward_int8_port(q, v, prep, rows, int8_pv: bool = True, group: int = 64):
             for off in np.nonzero(exact)[0]:
                 j = g0 + int(off)
                 klo, kln = _rows(T, block, j)
-                ki = np.zeros((block, D), np.int64)
-                ki[:kln] = prep["ki"][b, klo:klo + kln, h]
-                ks = np.zeros(block, np.float32)
-                ks[:kln] = prep["ks"][b, klo:klo + kln, h]
-                a32 = (qi @ ki.T).astype(np.float32)
-                s = (a32 * (qs_log2[:, None] * ks[None, :])).astype(np.float32)
-                s[:, kln:] = -np.inf
-                bm = s.max(axis=1)
-                new_max = np.maximum(m, bm)
-                alpha = np.exp2(m - new_max).astype(np.float32)
-                if int8_pv:
-                    vi = np.zeros((block, D), np.int64)
-                    vi[:kln] = prep["vi"][b, klo:klo + kln, h]
-                    pe = np.exp2(s - bm[:, None]).astype(np.float32)
-                    beta = np.exp2(bm - new_max).astype(np.float32)
-                    l = l * alpha + beta * pe.sum(axis=1, dtype=np.float32)
-                    pi = np.minimum(pe * np.float32(127) + np.float32(0.5), np.float32(127)).astype(np.int64)
-                    pv = (pi @ vi).astype(np.float32) * ((beta * inv127)[:, None] * vsc[None, :])
-                else:
-                    vb = np.zeros((block, D), np.float32)
-                    vb[:kln] = bf16_to_f32(v[b, klo:klo + kln, h])
-                    p = np.exp2(s - new_max[:, None]).astype(np.float32)
-                    l = l * alpha + p.sum(axis=1, dtype=np.float32)
-                    pv = _bf16_round(p) @ vb
-                acc = acc * alpha[:, None] + pv
-                m = new_max
+                # key ranges quantised against one max: the block, or (kernel
+                # arithmetic, block 128) each 64-key tile of a ragged last block
+                split = (codes == "kernel" and int8_pv and block == 128 and j == NT - 1
+                         and 64 < kln < block)
+                for slo, sln in ((0, 64), (64, kln - 64)) if split else ((0, kln),):
+                    ki = np.zeros((block, D), np.int64)
+                    ki[:sln] = prep["ki"][b, klo + slo:klo + slo + sln, h]
+                    ks = np.zeros(block, np.float32)
+                    ks[:sln] = prep["ks"][b, klo + slo:klo + slo + sln, h]
+                    a32 = (qi @ ki.T).astype(np.float32)
+                    s = (a32 * (qs_log2[:, None] * ks[None, :])).astype(np.float32)
+                    s[:, sln:] = -np.inf
+                    bm = s.max(axis=1)
+                    new_max = np.maximum(m, bm)
+                    alpha = np.exp2(m - new_max).astype(np.float32)
+                    if int8_pv:
+                        vi = np.zeros((block, D), np.int64)
+                        vi[:sln] = prep["vi"][b, klo + slo:klo + slo + sln, h]
+                        beta = np.exp2(bm - new_max).astype(np.float32)
+                        if codes == "kernel":
+                            x127 = np.exp2(s + np.float32(np.log2(127.0)) - bm[:, None]).astype(np.float32)
+                            pi = np.clip(np.rint(x127), 0, 255).astype(np.int64)
+                            l = l * alpha + (beta * inv127) * pi.sum(axis=1).astype(np.float32)
+                        else:
+                            pe = np.exp2(s - bm[:, None]).astype(np.float32)
+                            l = l * alpha + beta * pe.sum(axis=1, dtype=np.float32)
+                            pi = np.minimum(pe * np.float32(127) + np.float32(0.5),
+                                            np.float32(127)).astype(np.int64)
+                        pv = (pi @ vi).astype(np.float32) * ((beta * inv127)[:, None] * vsc[None, :])
+                    else:
+                        vb = np.zeros((block, D), np.float32)
+                        vb[:sln] = bf16_to_f32(v[b, klo + slo:klo + slo + sln, h])
+                        p = np.exp2(s - new_max[:, None]).astype(np.float32)
+                        l = l * alpha + p.sum(axis=1, dtype=np.float32)
+                        pv = _bf16_round(p) @ vb
+                    acc = acc * alpha[:, None] + pv
+                    m = new_max
         out[(b, h, i)] = (acc / l[:, None])[:ln].astype(np.float32)
     return out
 

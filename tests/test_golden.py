@@ -10,7 +10,7 @@ import pytest
 import torch
 
 import oracle
-from _util import cosine, from_bits, u32
+from _util import check_int8_blocks, cosine, from_bits, u32
 
 FIXTURES = sorted(glob.glob(os.path.join(os.path.dirname(__file__), "golden", "*.npz")))
 
@@ -72,5 +72,11 @@ def test_gpu_matches_golden(pkg, dev, path):
     ref = g["out"].astype(np.float32)
     if int8:
         assert cosine(got, ref) >= 0.999
+        # per query block, against the reference and the kernel arithmetic
+        p = oracle.prepare(g["q"], g["k"], g["v"], block=block, tau=tau, int8=True,
+                           sink_kv=skv, sink_q=sq)
+        rows = [(0, h, i) for h in range(int(g["H"])) for i in range(NT)]
+        check_int8_blocks(f"golden {os.path.basename(path)}", out.float().cpu().numpy(), g["q"],
+                          g["v"], p, rows, True, block)
     else:
         assert np.abs(got - ref).max() < 2e-2 and cosine(got, ref) >= 0.9995

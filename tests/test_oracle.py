@@ -348,6 +348,90 @@ def test_forward_int8_port_vs_closed_form(int8_pv):
     assert cosine(got, ref) > (0.999 if int8_pv else 0.9999)
 
 
+@pytest.mark.parametrize("block,T", [(64, 600), (128, 700), (128, 2 * 128 + 100)])
+def test_forward_int8_kernel_codes_constant_v_is_exact(block, T):
+    """The kernel-arithmetic INT8 variant normalises by the sum of the codes it
+    multiplies, so with V the same vector on every token the output is exactly
+    that vector (weights sum to one); the reference arithmetic (fp32 pe sums,
+    trunc(pe*127+0.5) codes) is off by the quantisation of P. Every block is
+    exact here (the pooled branch rounds P to bf16 in both arithmetics). Covers
+    the block-128 ragged last block of more than 64 keys (T = 356) that the
+    kernel quantises per 64-key tile."""
+    B, H = 1, 2
+    q, k = (randn_bf16((B, T, H, 128), s) for s in (50, 51))
+    row = torch.linspace(-2, 2, 128).to(torch.bfloat16)
+    v = row.expand(B, T, H, 128).contiguous()
+    p = oracle.prepare(bits(q), bits(k), bits(v), block=block, tau=-1e30, int8=True, int8_pv=True)
+    rows = _rows(p, B, H)
+    want = row.float().numpy()
+    ker = oracle.forward_int8_port(bits(q), bits(v), p, rows, int8_pv=True, codes="kernel")
+    ref = oracle.forward_int8_port(bits(q), bits(v), p, rows, int8_pv=True, codes="reference")
+    ker_err = max(np.abs(ker[r] - want).max() for r in rows)
+    ref_err = max(np.abs(ref[r] - want).max() for r in rows)
+    assert ker_err < 2e-6, ker_err
+    assert ref_err > 50 * ker_err
+
+
+def test_forward_int8_kernel_codes_track_reference_per_block():
+    """Both INT8 arithmetics agree per query block to the INT8 tolerance, and
+    coincide wherever every code is 127 (all scores of a block equal)."""
+    B, T, H, block = 1, 1000, 2, 64
+    q, k, v = (randn_bf16((B, T, H, 128), s) for s in (52, 53, 54))
+    p = oracle.prepare(bits(q), bits(k), bits(v), block=block, tau=0.7, int8=True, int8_pv=True)
+    rows = _rows(p, B, H)
+    ker = oracle.forward_int8_port(bits(q), bits(v), p, rows, codes="kernel")
+    ref = oracle.forward_int8_port(bits(q), bits(v), p, rows, codes="reference")
+    assert min(cosine(ker[r], ref[r]) for r in rows) > 0.999
+    # identical keys within every block: pe = 1, both codes 127, same sums
+    kb = k.clone()
+    for j in range(0, T, block):
+        kb[:, j:j + block] = k[:, j:j + 1]
+    p2 = oracle.prepare(bits(q), bits(kb), bits(v), block=block, tau=0.7, int8=True, int8_pv=True)
+    ker2 = oracle.forward_int8_port(bits(q), bits(v), p2, rows, codes="kernel")
+    ref2 = oracle.forward_int8_port(bits(q), bits(v), p2, rows, codes="reference")
+    assert max(np.abs(ker2[r] - ref2[r]).max() for r in rows) < 1e-5
+
+
+def test_cfg0_plumbing_d64():
+    """BASELINE config 0 (B1 H4 D64, 4x32x32 grid -> N 4096, block 64, tau 0.9,
+    smooth field + 0.3 noise, Morton 3d) through the CPU path: the Morton
+    permutation against the brute-force bit loop, routing against the float64
+    closed form of the scores (decisions may differ only inside the tie band),
+    and the masked torch path and the reference loop against the float64
+    augmented-key closed form. Inputs are rounded to bf16, the kernels'
+    arithmetic type."""
+    import bench
+    cfg = bench.CONFIGS[0]
+    q, k, v = bench.make_inputs(cfg, "cpu", dtype=torch.float32)
+    perm, inv = oracle.morton_perm(cfg["grid"], "3d")
+    assert np.array_equal(perm, _brute_perm(cfg["grid"], "3d"))
+    assert np.array_equal(perm[inv], np.arange(perm.size))
+    q, k, v = (t[:, perm].to(torch.bfloat16) for t in (q, k, v))
+    B, T, H, D = q.shape
+    assert (B, T, H, D) == (1, 4096, 4, 64)
+    p = oracle.prepare(bits(q), bits(k), bits(v), block=cfg["block"], tau=cfg["tau"],
+                       want_scores=True)
+    NT = p["NT"]
+    R = oracle.route_scores(p["qbar"], p["kc"], p["scale"])
+    thr = np.transpose(p["thr"], (0, 2, 1))[..., None].astype(np.float64)
+    i, j = np.meshgrid(np.arange(NT), np.arange(NT), indexing="ij")
+    want = (R > thr) | (np.abs(i - j) <= 1)
+    got = oracle.exact_matrix(p["mask"], NT)
+    n_diff, in_band = oracle.tie_count(p["scores"], p["thr"], got, want)
+    assert in_band and n_diff <= 4
+    density = got.mean()
+    assert 0.05 < density < 0.6
+    rows = [(0, h, ii) for h in range(H) for ii in range(0, NT, 7)]
+    cf = oracle.forward_closed_form(bits(q), bits(k), bits(v), p, rows)
+    mt = oracle.masked_attention_torch(q.float(), k.float(), v.float(), p, heads=list(range(H)),
+                                       qblocks=list(range(0, NT, 7)))
+    port = oracle.forward_port(bits(q), bits(k), bits(v), p, rows)
+    for r in rows:
+        assert np.abs(mt[r].numpy() - cf[r]).max() < 1e-5
+        assert np.abs(port[r] - cf[r]).max() < 2e-2
+        assert cosine(port[r], cf[r]) > 0.9995
+
+
 def test_masked_attention_torch_matches_closed_form():
     B, T, H = 1, 333, 2
     q, k, v = (randn_bf16((B, T, H, 128), s) for s in (37, 38, 39))
