@@ -259,6 +259,13 @@ def run_kernel_only(args, mods, cfg, q, k, v):
             fq.quantize_bthd(q)
             fq.quantize_bthd(k, mean=r.kc_mean.reshape(-1, D))
             fq.quantize_v_per_channel(v)
+    elif args.kernel_only in ("int8_call", "int8_bf16pv_call"):
+        pv = args.kernel_only == "int8_call"
+        for _ in range(args.steps):
+            mods["_int8_fwd"].sol_attn_int8(q, k, v, tau=tau, block=block, int8_pv=pv)
+    elif args.kernel_only == "bf16_call":
+        for _ in range(args.steps):
+            mods["_tri_fwd"].sol_attn(q, k, v, tau=tau, block=block)
     elif args.kernel_only == "prep":
         for _ in range(args.steps):
             mods["_preprocess"].route(q, k, v, scale=D ** -0.5, tau=tau, block=block)
@@ -270,6 +277,47 @@ def run_kernel_only(args, mods, cfg, q, k, v):
     print(f"[bench] kernel-only {args.kernel_only} x{args.steps} done", file=sys.stderr, flush=True)
 
 
+# Sequence lengths for the dense/sparse crossover (the node's min_tokens):
+# video-like smooth fields on latent grids of these token counts.
+SWEEP_GRIDS = [(1, 32, 32), (2, 32, 32), (4, 32, 32), (8, 32, 32), (16, 32, 32), (21, 30, 52)]
+SWEEP_TAUS = (0.8, 0.9, 1.3)
+
+
+def run_sweep(args, mods, dev):
+    """Dense PyTorch SDPA (the path the node declines to) against the sparse
+    calls (prep included) per sequence length and tau, at both block sizes:
+    one JSON line per (N, block). Morton reordering is per model, not per
+    call, so it is done before timing."""
+    sol_attn = mods["_tri_fwd"].sol_attn
+    i8 = mods["_int8_fwd"].sol_attn_int8
+    steps = max(3, args.steps // 2)
+    for grid in SWEEP_GRIDS:
+        cfg = dict(CONFIGS[2], grid=grid, coarse=(min(4, grid[0]), 6, 8))
+        q, k, v = make_inputs(cfg, dev)
+        perm, _ = mods["_morton"].morton_perm(grid, dev, "3d")
+        q, k, v = (mods["_morton"].reorder_tokens(t, perm, dim=1) for t in (q, k, v))
+        B, T, H, D = q.shape
+        dflops = dense_flops(B, H, T, D)
+        sdpa = torch_sdpa(q, k, v, dflops, steps)
+        for block in (64, 128):
+            line = {"N": T, "H": H, "block": block, "sdpa_ms": sdpa.get("ms"),
+                    "sdpa_backend": sdpa.get("backend"), "bf16_ms": {}, "int8_pv_ms": {},
+                    "int8_bf16pv_ms": {}, "density": {}}
+            for tau in SWEEP_TAUS:
+                line["bf16_ms"][str(tau)] = round(time_cuda(
+                    lambda: sol_attn(q, k, v, tau=tau, block=block), steps, 2), 4)
+                line["int8_pv_ms"][str(tau)] = round(time_cuda(
+                    lambda: i8(q, k, v, tau=tau, block=block, int8_pv=True), steps, 2), 4)
+                line["int8_bf16pv_ms"][str(tau)] = round(time_cuda(
+                    lambda: i8(q, k, v, tau=tau, block=block, int8_pv=False), steps, 2), 4)
+                r = mods["_preprocess"].route(q, k, v, scale=D ** -0.5, tau=tau, block=block)
+                NT = r.counts.shape[-1]
+                line["density"][str(tau)] = round(float(r.counts.double().sum() / (B * H * NT * NT)), 4)
+            print(json.dumps(line), flush=True)
+        del q, k, v
+        torch.cuda.empty_cache()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -279,12 +327,16 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--extra", action="store_true", help="also time the INT8 forward (cfg 3)")
+    ap.add_argument("--sweep", action="store_true",
+                    help="dense SDPA vs the sparse calls over sequence lengths and tau (the "
+                         "min_tokens crossover); JSON lines, not the metric")
     ap.add_argument("--block", type=int, choices=[64, 128],
                     help="routing block size instead of the config's (a diagnostic, not the metric)")
     ap.add_argument("--heads", type=int,
                     help="number of heads instead of the config's, e.g. 3 = one GPU's share of an "
                          "8-way head split at cfg 2 (not the metric)")
-    ap.add_argument("--kernel-only", choices=["fwd", "fwd_int8", "fwd_int8_bf16pv", "prep", "quant", "reorder"],
+    ap.add_argument("--kernel-only", choices=["fwd", "fwd_int8", "fwd_int8_bf16pv", "prep", "quant",
+                                              "reorder", "int8_call", "int8_bf16pv_call", "bf16_call"],
                     help="profiling driver: run only this kernel --steps times (after a "
                          "512 MiB device copy used to calibrate memory counters); no JSON")
     args = ap.parse_args()
@@ -298,6 +350,9 @@ def main():
 
     mods = _pkg()
     dev = torch.device("cuda:0")
+    if args.sweep:
+        run_sweep(args, mods, dev)
+        return
     cfg = dict(CONFIGS[args.config])
     if args.block:
         cfg["block"] = args.block

@@ -279,16 +279,11 @@ extern "C" int solattn_sol_attn_int8(const uint16_t* q, int64_t sq_b, int64_t sq
                      sink_kv_hi, sink_q_lo, sink_q_hi, at<float>(ws, L.thr), at<int32_t>(ws, L.counts),
                      at<int16_t>(ws, L.lists), at<uint32_t>(ws, L.mask), stream);
   if (rc) return rc;
-  rc = solattn_quant_rows(q, sq_b, sq_t, sq_h, B, T, H, D, nullptr, at<int8_t>(ws, L.qi),
-                          at<float>(ws, L.qs), L.TP, stream);
+  rc = quant_qkv(q, sq_b, sq_t, sq_h, k, sk_b, sk_t, sk_h, v, sv_b, sv_t, sv_h, B, T, H, D,
+                 at<float>(ws, L.kc_mean), vscale, at<int8_t>(ws, L.qi), at<float>(ws, L.qs),
+                 at<int8_t>(ws, L.ki), at<float>(ws, L.ks), int8_pv ? at<int8_t>(ws, L.vi) : nullptr,
+                 L.TP, reinterpret_cast<hipStream_t>(stream));
   if (rc) return rc;
-  rc = solattn_quant_rows(k, sk_b, sk_t, sk_h, B, T, H, D, at<float>(ws, L.kc_mean),
-                          at<int8_t>(ws, L.ki), at<float>(ws, L.ks), L.TP, stream);
-  if (rc) return rc;
-  if (int8_pv) {
-    rc = solattn_quant_v(v, sv_b, sv_t, sv_h, B, T, H, D, vscale, at<int8_t>(ws, L.vi), L.TP, stream);
-    if (rc) return rc;
-  }
   return solattn_fwd_int8(q, sq_b, sq_t, sq_h, at<int8_t>(ws, L.qi), at<float>(ws, L.qs),
                           at<int8_t>(ws, L.ki), at<float>(ws, L.ks),
                           int8_pv ? at<int8_t>(ws, L.vi) : nullptr, vscale, v, sv_b, sv_t, sv_h,

@@ -12,15 +12,6 @@ constexpr int kQD = 128;
 constexpr int kQuantThreads = 256;
 constexpr int kRowsPerWG = kQuantThreads / 16;
 
-// trunc(val + copysign(0.5, val)) clamped to [-127, 127]: the reference's
-// val >= 0 ? trunc(val + 0.5) : trunc(val - 0.5) as an integer for every
-// float (at val = -0 both give 0).
-__device__ __forceinline__ int8_t round_half_away_clamp(float val) {
-  float r = truncf(val + copysignf(0.5f, val));
-  r = fminf(fmaxf(r, -127.f), 127.f);
-  return static_cast<int8_t>(static_cast<int>(r));
-}
-
 __device__ __forceinline__ uint32_t pack_i8x4(int8_t a, int8_t b, int8_t c, int8_t d) {
   return static_cast<uint32_t>(static_cast<uint8_t>(a)) |
          (static_cast<uint32_t>(static_cast<uint8_t>(b)) << 8) |
@@ -28,144 +19,201 @@ __device__ __forceinline__ uint32_t pack_i8x4(int8_t a, int8_t b, int8_t c, int8
          (static_cast<uint32_t>(static_cast<uint8_t>(d)) << 24);
 }
 
-// /root/reference/_fused_quant.py:8-42 (per token, optional smoothing mean)
-// and /root/reference/_fused_prep.py:42-48 (Q; clamp-then-round gives the
-// same codes). vscale != nullptr switches to the per-channel V rule,
-// /root/reference/_fused_quant.py:61-88. Each 16-lane group handles kRowsPerGroup
-// rows, kQuantThreads / 16 groups apart, with every row's load issued before
-// any arithmetic (more bytes in flight per lane).
-constexpr int kRowsPerGroup = 4;
-constexpr int kRowsPerChunk = kRowsPerGroup * kRowsPerWG;  // rows of one workgroup pass
+// One launch quantises up to three BTHD tensors (blockIdx.z picks the
+// tensor): per token with an optional smoothing mean (Q, K;
+// /root/reference/_fused_quant.py:8-42 and the Q half of
+// /root/reference/_fused_prep.py:42-48, whose clamp-then-round gives the same
+// codes) or per channel against vscale (V; /root/reference/_fused_quant.py:61-88).
+// A workgroup owns kQuantTok tokens of one (batch, head): its 16 lane groups
+// take tokens t0 + g, t0 + g + 16, ... and each lane 8 channels, so the mean
+// or channel scales sit in registers for the whole workgroup and every lane
+// has kQuantR 16-byte row loads in flight before any arithmetic.
+//
+// Codes are trunc(fl(q + copysign(0.5, q))) of the IEEE quotient q = fl(x / s),
+// clamped to [-127, 127], exactly as the CPU oracle rounds. The kernel forms
+// q' = x * rcp(s) instead (v_rcp_f32, within 1 ulp of 1/s), within 2 ulp of q;
+// trunc(fl(. + 0.5)) can only differ between q and q' when fl(q' + 0.5) lies
+// within 4e-5 of an integer (|q| <= 127.5, so an ulp is at most 7.7e-6), and a
+// lane holding such a value recomputes its eight codes by IEEE division.
+constexpr int kQuantR = 8;                       // tokens per lane group
+constexpr int kQuantTok = kQuantR * kRowsPerWG;  // tokens per workgroup
 
-// The rows of one chunk a lane group owns: 16-byte loads and their (b, t, h).
-struct QuantRows {
-  uint32_t rw[kRowsPerGroup], hh[kRowsPerGroup], tt[kRowsPerGroup], bb[kRowsPerGroup];
-  uint4 raw[kRowsPerGroup];
+struct QuantTensor {
+  const uint16_t* x;
+  int64_t sb, st, sh;     // element strides of x
+  const float* mean;      // [B, H, D] smoothing mean, or null
+  const float* vscale;    // [B, H, D] per-channel scale (V rule), or null
+  int8_t* xi;             // [B, TP, H, D]
+  float* xs;              // [B, TP, H] per-token scales (not written by the V rule)
 };
 
-__device__ __forceinline__ void quant_load(QuantRows& R, uint32_t chunk, const uint16_t* __restrict__ x,
-                                           int64_t sx_b, int64_t sx_t, int64_t sx_h, uint32_t T,
-                                           uint32_t H, uint32_t rows, int c8) {
-  // (b, t, h) of the first row by division, of the others by stepping
-  // kRowsPerWG rows forward (rows are ordered b, t, h with h fastest).
-  const uint32_t row0 = chunk * kRowsPerChunk + (threadIdx.x >> 4);
-  uint32_t hc = row0 % H, bt = row0 / H;
-  uint32_t tc = bt % T, bc = bt / T;
+struct QuantArgs {
+  QuantTensor t[3];
+  uint32_t T, H;
+  int64_t TP;
+};
+
+// t = fl(q + copysign(0.5, q)) -> trunc(t) clamped to [-127, 127]
+// (v_cvt_i32_f32 truncates).
+__device__ __forceinline__ int code_of(float t) {
+  return static_cast<int>(__builtin_amdgcn_fmed3f(t, -127.f, 127.f));
+}
+
+__device__ __forceinline__ bool near_integer(float t) {
+  return fabsf(t - __builtin_rintf(t)) <= 4e-5f;
+}
+
+// fl(a / 127) for a >= 0 without a division: q0 = a * fl(1/127) corrected by
+// one fma residual step. Equal to the IEEE quotient for every non-negative
+// finite float (checked exhaustively on the CPU, tests/test_oracle.py).
+__device__ __forceinline__ float div127(float a) {
+  const float c = 1.0f / 127.0f;
+  const float q0 = a * c;
+  const float r = __builtin_fmaf(-q0, 127.0f, a);
+  return __builtin_fmaf(r, c, q0);
+}
+
+// Max over the 16 lanes of a lane group through DPP lane moves (no LDS):
+// swap neighbours, swap pairs, mirror within 8 lanes, mirror within 16.
+__device__ __forceinline__ float group16_max(float x) {
+  x = fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1, 0xf, 0xf, false)));
+  x = fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x4E, 0xf, 0xf, false)));
+  x = fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x141, 0xf, 0xf, false)));
+  x = fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x140, 0xf, 0xf, false)));
+  return x;
+}
+
+// PER_CHANNEL: V against vscale[d]; otherwise per token, smoothed by mean
+// when the tensor has one.
+template <bool PER_CHANNEL>
+__device__ __forceinline__ void quant_rows_of(const QuantTensor& A, uint32_t T, uint32_t H,
+                                              int64_t TP) {
+  const uint32_t bh = blockIdx.x, b = bh / H, h = bh % H;
+  const int c8 = (threadIdx.x & 15) * 8;
+  const uint32_t t0 = blockIdx.y * kQuantTok + (threadIdx.x >> 4);
+  const uint16_t* xb = A.x + b * A.sb + h * A.sh + c8;
+
+  uint4 raw[kQuantR];
 #pragma unroll
-  for (int k = 0; k < kRowsPerGroup; ++k) {
-    R.rw[k] = row0 + k * kRowsPerWG;
-    const bool in = R.rw[k] < rows;
-    // rows past the end re-read the last row (loads stay in bounds; nothing is stored)
-    R.hh[k] = in ? hc : H - 1;
-    R.tt[k] = in ? tc : T - 1;
-    R.bb[k] = in ? bc : (rows / H) / T - 1;
-    R.raw[k] = *reinterpret_cast<const uint4*>(x + R.bb[k] * sx_b +
-                                               static_cast<int64_t>(R.tt[k]) * sx_t + R.hh[k] * sx_h + c8);
-    hc += kRowsPerWG;
-    while (hc >= H) {  // at most kRowsPerWG / H + 1 steps
-      hc -= H;
-      if (++tc == T) {
-        tc = 0;
-        ++bc;
+  for (int r = 0; r < kQuantR; ++r) {  // tokens past T re-read token T-1; nothing is stored
+    const uint32_t t = min(t0 + r * kRowsPerWG, T - 1);
+    raw[r] = *reinterpret_cast<const uint4*>(xb + static_cast<int64_t>(t) * A.st);
+  }
+  const int64_t chan = static_cast<int64_t>(bh) * kQD + c8;
+  float m[8], sv[8], rs[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    m[e] = (!PER_CHANNEL && A.mean) ? A.mean[chan + e] : 0.f;
+    sv[e] = PER_CHANNEL ? A.vscale[chan + e] : 1.f;
+    rs[e] = PER_CHANNEL ? __builtin_amdgcn_rcpf(sv[e]) : 1.f;
+  }
+
+#pragma unroll
+  for (int r = 0; r < kQuantR; ++r) {
+    const uint32_t t = t0 + r * kRowsPerWG;
+    const uint32_t w[4] = {raw[r].x, raw[r].y, raw[r].z, raw[r].w};
+    float y[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      y[2 * e] = lo_bf16(w[e]) - m[2 * e];
+      y[2 * e + 1] = hi_bf16(w[e]) - m[2 * e + 1];
+    }
+    float ss = 1.f;
+    if (!PER_CHANNEL) {
+      float amax = fmaxf(fmaxf(fabsf(y[0]), fabsf(y[1])), fmaxf(fabsf(y[2]), fabsf(y[3])));
+      amax = fmaxf(amax, fmaxf(fmaxf(fabsf(y[4]), fabsf(y[5])), fmaxf(fabsf(y[6]), fabsf(y[7]))));
+      const float sc = div127(group16_max(amax));
+      ss = sc > 1e-8f ? sc : 1e-8f;
+      const float rr = __builtin_amdgcn_rcpf(ss);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) rs[e] = rr;
+    }
+    int code[8];
+    bool near = false;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float q1 = y[e] * rs[e];
+      const float tq = q1 + copysignf(0.5f, q1);
+      near |= near_integer(tq);
+      code[e] = code_of(tq);
+    }
+    if (near) {
+      asm volatile("");  // keeps the divisions on this rare path
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float q = y[e] / (PER_CHANNEL ? sv[e] : ss);
+        code[e] = code_of(q + copysignf(0.5f, q));
       }
+    }
+    if (t < T) {
+      const int64_t row = (static_cast<int64_t>(b) * TP + t) * H + h;
+      uint2 o;
+      o.x = pack_i8x4(code[0], code[1], code[2], code[3]);
+      o.y = pack_i8x4(code[4], code[5], code[6], code[7]);
+      *reinterpret_cast<uint2*>(A.xi + row * kQD + c8) = o;
+      if (!PER_CHANNEL && (threadIdx.x & 15) == 0) A.xs[row] = ss;
     }
   }
 }
 
-// One chunk of kRowsPerChunk rows per workgroup.
 __global__ void __launch_bounds__(kQuantThreads)
-quant_kernel(const uint16_t* __restrict__ x, int64_t sx_b, int64_t sx_t, int64_t sx_h,
-             uint32_t T, uint32_t H, uint32_t rows, const float* __restrict__ mean,
-             const float* __restrict__ vscale, int8_t* __restrict__ xi, float* __restrict__ xs,
-             int64_t TP) {
-  const int c8 = (threadIdx.x & 15) * 8;
-  {
-    QuantRows cur;
-    quant_load(cur, blockIdx.x, x, sx_b, sx_t, sx_h, T, H, rows, c8);
-    const uint32_t* rw = cur.rw;
-    const uint32_t* hh = cur.hh;
-    const uint32_t* tt = cur.tt;
-    const uint32_t* bb = cur.bb;
-    const uint4* raw = cur.raw;
-#pragma unroll
-    for (int k = 0; k < kRowsPerGroup; ++k) {
-      const uint32_t b = bb[k], t = tt[k], h = hh[k];
-      const uint32_t w[4] = {raw[k].x, raw[k].y, raw[k].z, raw[k].w};
-      float y[8];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        y[2 * e] = lo_bf16(w[e]);
-        y[2 * e + 1] = hi_bf16(w[e]);
-      }
-      const int64_t bh = static_cast<int64_t>(b) * H + h;
-      int8_t code[8];
-      if (vscale) {
-        const float4* sp = reinterpret_cast<const float4*>(vscale + bh * kQD + c8);
-        const float4 s0 = sp[0], s1 = sp[1];
-        const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-#pragma unroll
-        for (int e = 0; e < 8; ++e) code[e] = round_half_away_clamp(y[e] / sv[e]);
-      } else {
-        if (mean) {
-          const float4* mp = reinterpret_cast<const float4*>(mean + bh * kQD + c8);
-          const float4 m0 = mp[0], m1 = mp[1];
-          const float m[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
-#pragma unroll
-          for (int e = 0; e < 8; ++e) y[e] = y[e] - m[e];
-        }
-        float amax = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(y[e]));
-#pragma unroll
-        for (int sh = 1; sh < 16; sh <<= 1) amax = fmaxf(amax, __shfl_xor(amax, sh));
-        const float sc = amax / 127.0f;
-        const float ss = sc > 1e-8f ? sc : 1e-8f;
-        // y * fl(1/ss) is within 2.3e-5 of the IEEE quotient fl(y/ss) (|y/ss| <=
-        // 127.5; fl(1/ss), the product and the quotient each round by <= 2^-24
-        // relative), so the codes agree unless that quotient lies within 3e-5 of
-        // k + 0.5; lanes with such a value redo their 8 channels by IEEE division.
-        const float r = 1.0f / ss;
-        bool near = false;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float q1 = y[e] * r;
-          const float a = fabsf(q1);
-          near |= fabsf((a - truncf(a)) - 0.5f) <= 3e-5f;
-          code[e] = round_half_away_clamp(q1);
-        }
-        if (near) {
-          asm volatile("");  // keeps the divisions on this rare path
-#pragma unroll
-          for (int e = 0; e < 8; ++e) code[e] = round_half_away_clamp(y[e] / ss);
-        }
-        if ((threadIdx.x & 15) == 0 && rw[k] < rows) xs[(static_cast<int64_t>(b) * TP + t) * H + h] = ss;
-      }
-      if (rw[k] < rows) {
-        uint2 o;
-        o.x = pack_i8x4(code[0], code[1], code[2], code[3]);
-        o.y = pack_i8x4(code[4], code[5], code[6], code[7]);
-        *reinterpret_cast<uint2*>(xi + ((static_cast<int64_t>(b) * TP + t) * H + h) * kQD + c8) = o;
-      }
-    }
+quant3_kernel(const QuantArgs args) {
+  // Heads vary fastest over the grid, so the workgroups in flight read
+  // neighbouring tokens of every head: contiguous memory for a BTHD tensor.
+  const QuantTensor& A = args.t[blockIdx.z];
+  if (A.vscale != nullptr)
+    quant_rows_of<true>(A, args.T, args.H, args.TP);
+  else
+    quant_rows_of<false>(A, args.T, args.H, args.TP);
+}
+
+int check_quant_tensor(const QuantTensor& q, int64_t B, int64_t T, int64_t H, int64_t TP,
+                       const char* what) {
+  SOLATTN_REQUIRE(B > 0 && T > 0 && H > 0 && TP >= T, SOLATTN_EINVAL, "%s: bad sizes", what);
+  SOLATTN_REQUIRE(B * H < (1ll << 31) && cdiv(T, kQuantTok) <= 65535, SOLATTN_EUNSUPPORTED,
+                  "%s: too many rows", what);
+  SOLATTN_REQUIRE(q.x && q.xi && (q.vscale || q.xs), SOLATTN_EINVAL, "%s: null pointer", what);
+  SOLATTN_REQUIRE(reinterpret_cast<uintptr_t>(q.x) % 16 == 0 && q.sb % 8 == 0 && q.st % 8 == 0 &&
+                      q.sh % 8 == 0 && reinterpret_cast<uintptr_t>(q.xi) % 8 == 0,
+                  SOLATTN_EINVAL, "%s: unaligned input or strides", what);
+  return 0;
+}
+
+// Quantises n (1..3) tensors of the same B, T, H in one launch.
+int launch_quant3(const QuantTensor* ts, int n, int64_t B, int64_t T, int64_t H, int64_t D,
+                  int64_t TP, hipStream_t stream, const char* what) {
+  SOLATTN_REQUIRE(D == kQD, SOLATTN_EUNSUPPORTED, "%s: head_dim %lld != 128", what, (long long)D);
+  SOLATTN_REQUIRE(n >= 1 && n <= 3, SOLATTN_EINVAL, "%s: %d tensors", what, n);
+  QuantArgs args{};
+  for (int i = 0; i < n; ++i) {
+    if (int rc = check_quant_tensor(ts[i], B, T, H, TP, what)) return rc;
+    args.t[i] = ts[i];
   }
+  args.T = static_cast<uint32_t>(T);
+  args.H = static_cast<uint32_t>(H);
+  args.TP = TP;
+  dim3 grid(static_cast<uint32_t>(B * H), static_cast<uint32_t>(cdiv(T, kQuantTok)),
+            static_cast<uint32_t>(n));
+  hipLaunchKernelGGL(quant3_kernel, grid, dim3(kQuantThreads), 0, stream, args);
+  return check_launch(what);
 }
 
 int launch_quant(const uint16_t* x, int64_t sx_b, int64_t sx_t, int64_t sx_h, int64_t B,
                  int64_t T, int64_t H, int64_t D, const float* mean, const float* vscale,
                  int8_t* xi, float* xs, int64_t TP, hipStream_t stream, const char* what) {
-  SOLATTN_REQUIRE(D == kQD, SOLATTN_EUNSUPPORTED, "%s: head_dim %lld != 128", what, (long long)D);
-  SOLATTN_REQUIRE(B > 0 && T > 0 && H > 0 && TP >= T, SOLATTN_EINVAL, "%s: bad sizes", what);
-  SOLATTN_REQUIRE(B * T * H < (1ll << 31), SOLATTN_EUNSUPPORTED, "%s: too many rows", what);
-  SOLATTN_REQUIRE(x && xi && (vscale || xs), SOLATTN_EINVAL, "%s: null pointer", what);
-  SOLATTN_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && sx_b % 8 == 0 && sx_t % 8 == 0 &&
-                      sx_h % 8 == 0 && reinterpret_cast<uintptr_t>(xi) % 8 == 0,
-                  SOLATTN_EINVAL, "%s: unaligned input or strides", what);
-  const uint32_t rows = static_cast<uint32_t>(B * T * H);
-  hipLaunchKernelGGL(quant_kernel, dim3(static_cast<uint32_t>(cdiv(rows, kRowsPerChunk))),
-                     dim3(kQuantThreads), 0, stream, x, sx_b, sx_t, sx_h,
-                     static_cast<uint32_t>(T), static_cast<uint32_t>(H), rows, mean, vscale, xi,
-                     xs, TP);
-  return check_launch(what);
+  const QuantTensor t{x, sx_b, sx_t, sx_h, mean, vscale, xi, xs};
+  return launch_quant3(&t, 1, B, T, H, D, TP, stream, what);
+}
+
+int quant_qkv(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h, const uint16_t* k,
+              int64_t sk_b, int64_t sk_t, int64_t sk_h, const uint16_t* v, int64_t sv_b,
+              int64_t sv_t, int64_t sv_h, int64_t B, int64_t T, int64_t H, int64_t D,
+              const float* k_mean, const float* vscale, int8_t* qi, float* qs, int8_t* ki,
+              float* ks, int8_t* vi, int64_t TP, hipStream_t stream) {
+  const QuantTensor ts[3] = {{q, sq_b, sq_t, sq_h, nullptr, nullptr, qi, qs},
+                             {k, sk_b, sk_t, sk_h, k_mean, nullptr, ki, ks},
+                             {v, sv_b, sv_t, sv_h, nullptr, vscale, vi, nullptr}};
+  return launch_quant3(ts, vscale ? 3 : 2, B, T, H, D, TP, stream, "quant_qkv");
 }
 
 }  // namespace solattn

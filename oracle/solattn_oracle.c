@@ -339,3 +339,23 @@ void or_quant_v(const uint16_t* v, int64_t sv_b, int64_t sv_t, int64_t sv_h, int
               round_half_away_clamp(val / vscale[(b * H + h) * D + d]);
         }
 }
+
+/* ------------------------------------------------------------ test helper --
+ * The INT8 kernels form a per-token scale fl(amax / 127) without a division,
+ * as fma(fma(-q0, 127, a), c, q0) with q0 = a * c and c = fl(1/127). Counts the
+ * non-negative finite floats a (bit patterns start, start + step, ... below
+ * stop) for which that differs from the IEEE quotient. */
+uint64_t or_div127_mismatches(uint32_t start, uint32_t stop, uint32_t step) {
+  const float c = 1.0f / 127.0f;
+  uint64_t bad = 0;
+  if (stop > 0x7f800000u) stop = 0x7f800000u;
+  for (uint64_t u = start; u < stop; u += step) {
+    uint32_t bits = (uint32_t)u;
+    float a;
+    memcpy(&a, &bits, sizeof a);
+    const float q0 = a * c;
+    const float q1 = fmaf(fmaf(-q0, 127.0f, a), c, q0);
+    if (q1 != a / 127.0f) ++bad;
+  }
+  return bad;
+}
