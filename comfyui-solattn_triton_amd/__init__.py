@@ -18,6 +18,7 @@ import os
 from ._dispatch import (  # noqa: F401  (re-exported API)
     BLOCK_SIZE,
     HEAD_DIM,
+    MIN_TOKENS,
     _IMPORT_ERROR,
     _INT8_IMPORT_ERROR,
     _compose_module_patch,
@@ -156,8 +157,9 @@ if _COMFY_ERROR is None:
                     io.Float.Input("start_percent", default=0.2, min=0.0, max=1.0, step=0.01,
                                    tooltip="Run dense before this point. The paper uses 0.2."),
                     io.Float.Input("end_percent", default=0.9, min=0.0, max=1.0, step=0.01),
-                    io.Int.Input("min_tokens", default=4096, min=0, max=1 << 20, step=512,
-                                 tooltip="Sequences shorter than this stay dense."),
+                    io.Int.Input("min_tokens", default=MIN_TOKENS, min=0, max=1 << 20, step=512,
+                                 tooltip="Sequences shorter than this stay dense. On MI355X "
+                                         "the sparse path beats dense SDPA from 2048 tokens."),
                     io.Boolean.Input("int8_qk", default=True,
                                      tooltip="INT8 QK in the exact branch (smoothed K, per-token "
                                              "scales) on the int8 matrix cores."),
@@ -269,7 +271,7 @@ if _COMFY_ERROR is None:
     def attention_sol(q, k, v, heads, mask=None, attn_precision=None, skip_reshape=False,
                       skip_output_reshape=False, **kwargs):
         """The "sol_attn" registry entry: the sparse path with the registry
-        defaults (tau 1.0, 4096 tokens, BF16, no sigma window), ComfyUI's
+        defaults (tau 1.0, MIN_TOKENS tokens, BF16, no sigma window), ComfyUI's
         PyTorch attention otherwise (/root/reference/__init__.py:649-663)."""
         out = try_sparse_default(q, k, v, heads, mask, skip_reshape, skip_output_reshape,
                                  kwargs.get("scale"))

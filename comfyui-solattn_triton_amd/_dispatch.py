@@ -44,9 +44,14 @@ except Exception as exc:
     _INT8_IMPORT_ERROR = exc
 
 HEAD_DIM = 128
+# Shortest sequence the sparse path takes by default: on MI355X every sparse
+# call (BF16 and both INT8 modes, prep included) beats the dense PyTorch SDPA
+# from 2048 tokens on; the INT8 calls lose to it at 1024 (the reference's
+# default, tuned for its own kernels, is 4096).
+MIN_TOKENS = 2048
 BLOCK_SIZE = 64  # default routing block (the reference's); 128 is also supported
 # Query/key blocks per head the forward kernels take; longer sequences stay dense.
-MAX_BLOCKS = 2048
+MAX_BLOCKS = 16384
 
 STAT_KEYS = ("sparse", "dense_fallback", "outside_range", "dense_block", "errors")
 _stats = dict.fromkeys(STAT_KEYS, 0)
@@ -277,7 +282,7 @@ class SparsePolicy:
     """What the Patch Sol-Attn node configured for one model."""
 
     tau: float = 1.0
-    min_tokens: int = 4096
+    min_tokens: int = MIN_TOKENS
     sigma_start: Optional[float] = None
     sigma_end: Optional[float] = None
     verbose: bool = False
@@ -359,7 +364,7 @@ class SolAttnOverride:
         return self.dense(func, call, attn_precision) if out is None else out
 
 
-def make_override(tau=1.0, min_tokens=4096, sigma_start=None, sigma_end=None, verbose=False,
+def make_override(tau=1.0, min_tokens=MIN_TOKENS, sigma_start=None, sigma_end=None, verbose=False,
                   int8_qk=False, sink_conditioning="exact_kv", use_tma=False,
                   dense_blocks=frozenset(), tau_profile=None, int8_pv=True, previous=None,
                   block=BLOCK_SIZE):
@@ -372,7 +377,7 @@ def make_override(tau=1.0, min_tokens=4096, sigma_start=None, sigma_end=None, ve
     return SolAttnOverride(policy, previous)
 
 
-# The registry entry's policy: tau 1.0, 4096 tokens, BF16, no window, no sink
+# The registry entry's policy: tau 1.0, MIN_TOKENS, BF16, no window, no sink
 # (/root/reference/__init__.py:649-663).
 REGISTRY_POLICY = SparsePolicy()
 

@@ -22,7 +22,7 @@ BLOCK_SIZE = 64
 GROUP_PAD = 64
 HEAD_DIM = 128
 SUPPORTED_BLOCKS = (64, 128)
-MAX_BLOCKS = 2048  # query/key blocks per head the forward kernels accept
+MAX_BLOCKS = 16384  # query/key blocks per head the forward kernels accept
 
 __all__ = ["prepare", "route", "Routing", "BLOCK_SIZE", "tau_vector"]
 

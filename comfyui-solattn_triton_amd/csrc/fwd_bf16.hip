@@ -477,12 +477,12 @@ extern "C" int solattn_fwd_bf16(const uint16_t* q, int64_t sq_b, int64_t sq_t, i
   const uint32_t grid = static_cast<uint32_t>(B * H * NT);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (block == 128) {
-    hipLaunchKernelGGL((bf16fwd::fwd_bf16_kernel<128>), dim3(grid), dim3(256), 0, s,
+    hipLaunchKernelGGL((bf16fwd::fwd_bf16_kernel<128>), dim3(grid), dim3(256), blist_lds_bytes(NT), s,
                        q, sq_b, sq_t, sq_h, k, sk_b, sk_t, sk_h, v, sv_b, sv_t, sv_h, kc, vc, npad,
                        counts, lists, mask, static_cast<int>(T), static_cast<int>(H),
                        static_cast<int>(NT), W, c, o, so_b, so_t, so_h);
   } else {
-    hipLaunchKernelGGL((bf16fwd::fwd_bf16_sbuf_kernel<64>), dim3(grid), dim3(128), 0, s, q,
+    hipLaunchKernelGGL((bf16fwd::fwd_bf16_sbuf_kernel<64>), dim3(grid), dim3(128), blist_lds_bytes(NT), s, q,
                        sq_b, sq_t, sq_h, k, sk_b, sk_t, sk_h, v, sv_b, sv_t, sv_h, kc, vc, npad,
                        counts, lists, mask, static_cast<int>(T), static_cast<int>(H),
                        static_cast<int>(NT), W, c, o, so_b, so_t, so_h);

@@ -19,7 +19,7 @@ namespace solattn {
 
 constexpr int kKeys = 64;             // keys per tile
 constexpr int kD = 128;               // head dim
-constexpr int kMaxNT = 2048;          // query/key blocks per head
+constexpr int kMaxNT = 16384;         // query/key blocks per head
 constexpr int kMaxPool = kMaxNT / 64; // pooled tiles per query block
 constexpr float kMaxSlack = 8.f;      // lazy running max (log2 units)
 
@@ -27,10 +27,18 @@ constexpr float kMaxSlack = 8.f;      // lazy running max (log2 units)
 struct TileList {
   uint64_t pmask[kMaxPool];  // approximate-block mask of each pooled tile
   int16_t pchunk[kMaxPool];  // pooled tile -> chunk of 64 pooled keys
-  int16_t blist[kMaxNT];     // exact key blocks, ascending
   int npool;
   int nexact;
 };
+
+// The exact key blocks of the workgroup's query block, ascending, live in the
+// launch's dynamic LDS (blist_lds_bytes(NT) bytes), so a short sequence does
+// not pay LDS for the longest one.
+__device__ __forceinline__ int16_t* blist_lds() {
+  extern __shared__ __align__(16) int16_t solattn_blist[];
+  return solattn_blist;
+}
+inline size_t blist_lds_bytes(int64_t NT) { return static_cast<size_t>(cdiv(NT * 2, 16) * 16); }
 
 struct KVSource {
   const uint16_t* k;  // token rows (this batch/head)
@@ -104,7 +112,8 @@ __device__ int build_tile_list(TileList& tl, const int32_t* __restrict__ counts,
                                const int16_t* __restrict__ lists, const uint32_t* __restrict__ mask,
                                int64_t row, int NT, int W, int T) {
   const int cnt = min(max(counts[row], 0), NT);
-  for (int e = threadIdx.x; e < cnt; e += blockDim.x) tl.blist[e] = lists[row * NT + e];
+  int16_t* blist = blist_lds();
+  for (int e = threadIdx.x; e < cnt; e += blockDim.x) blist[e] = lists[row * NT + e];
   if (threadIdx.x == 0) {
     const uint32_t* mrow = mask + row * W;
     int np = 0;
@@ -136,7 +145,7 @@ __device__ int build_tile_list(TileList& tl, const int32_t* __restrict__ counts,
 __device__ __forceinline__ int ragged_tiles(const TileList& tl, const int32_t* __restrict__ counts,
                                             int64_t row, int NT, int T) {
   const int cnt = min(max(counts[row], 0), NT);
-  return (tl.nexact > 0 && tl.blist[cnt - 1] == NT - 1 && (T % kKeys) != 0) ? 1 : 0;
+  return (tl.nexact > 0 && blist_lds()[cnt - 1] == NT - 1 && (T % kKeys) != 0) ? 1 : 0;
 }
 
 // Pooled tile p.
@@ -153,7 +162,7 @@ __device__ __forceinline__ TileDesc pooled_desc(const TileList& tl, int p, int N
 template <int BLK>
 __device__ __forceinline__ TileDesc exact_desc(const TileList& tl, int e, int T, int NT) {
   constexpr int S = BLK / kKeys;
-  const int j = min(max(static_cast<int>(tl.blist[e / S]), 0), NT - 1);
+  const int j = min(max(static_cast<int>(blist_lds()[e / S]), 0), NT - 1);
   TileDesc td;
   td.pooled = 0;
   td.first = j * BLK + (e % S) * kKeys;
@@ -166,7 +175,7 @@ __device__ __forceinline__ TileDesc exact_desc(const TileList& tl, int e, int T,
 template <int BLK>
 __device__ __forceinline__ int exact_first(const TileList& tl, int e) {
   constexpr int S = BLK / kKeys;
-  const int j = tl.blist[e / S];
+  const int j = blist_lds()[e / S];
   return __builtin_amdgcn_readfirstlane(j * BLK + (e % S) * kKeys);
 }
 

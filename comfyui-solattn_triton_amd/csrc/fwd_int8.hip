@@ -723,7 +723,7 @@ fwd_int8_b128_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t,
   const int cnt = min(max(counts[row], 0), NT);
   // full exact blocks: list entries [0, nfb); a ragged last block (T not a
   // multiple of 128) keeps its tiles [2 nfb, nexact) for the plain path
-  const int nfb = cnt - ((cnt > 0 && tl.blist[cnt - 1] == NT - 1 && (T % BLK) != 0) ? 1 : 0);
+  const int nfb = cnt - ((cnt > 0 && blist_lds()[cnt - 1] == NT - 1 && (T % BLK) != 0) ? 1 : 0);
 
   const int64_t bhD = (static_cast<int64_t>(b) * npad * H + h) * kD;
   const KVSource src{nullptr, 0, nullptr, 0, kc + bhD, static_cast<int64_t>(H) * kD, vc + bhD};
@@ -737,7 +737,7 @@ fwd_int8_b128_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t,
   const uint32_t kb = lds_addr(arena);
   const auto kbuf_at = [&](int i) { return kb + i * kBlkKStride; };
   const auto vbuf_at = [&](int i) { return kb + 2 * kBlkKStride + i * kBlkVStride; };
-  const auto blk_first = [&](int e) { return __builtin_amdgcn_readfirstlane(tl.blist[e] * BLK); };
+  const auto blk_first = [&](int e) { return __builtin_amdgcn_readfirstlane(blist_lds()[e] * BLK); };
   const auto issue_k = [&](int e, int i) { issue_blk<true>(kbuf_at(i), is.ki, is, blk_first(e), ioff.k, ks_blk); };
   const auto issue_v = [&](int e, int i) { issue_blk<false>(vbuf_at(i), is.vi, is, blk_first(e), ioff.v, 0u); };
 
@@ -873,7 +873,7 @@ void launch_i8(uint32_t grid, hipStream_t s, const uint16_t* q, int64_t sq_b, in
                int64_t npad, const int32_t* counts, const int16_t* lists, const uint32_t* mask,
                int T, int H, int NT, int W, float c, uint16_t* o, int64_t so_b, int64_t so_t,
                int64_t so_h) {
-  hipLaunchKernelGGL((fwd_int8_kernel<BLK, PV>), dim3(grid), dim3(BLK * 2), 0, s, q, sq_b, sq_t,
+  hipLaunchKernelGGL((fwd_int8_kernel<BLK, PV>), dim3(grid), dim3(BLK * 2), blist_lds_bytes(NT), s, q, sq_b, sq_t,
                      sq_h, qi, qs, ki, ks, vi, vscale, v, sv_b, sv_t, sv_h, TP, kc, vc, npad,
                      counts, lists, mask, T, H, NT, W, c, o, so_b, so_t, so_h);
 }
@@ -922,7 +922,7 @@ extern "C" int solattn_fwd_int8(const uint16_t* q, int64_t sq_b, int64_t sq_t, i
       so_b, so_t, so_h
   if (block == 128) {
     if (int8_pv)
-      hipLaunchKernelGGL(int8fwd::fwd_int8_b128_kernel, dim3(grid), dim3(256), 0, s, q, sq_b, sq_t,
+      hipLaunchKernelGGL(int8fwd::fwd_int8_b128_kernel, dim3(grid), dim3(256), blist_lds_bytes(NT), s, q, sq_b, sq_t,
                          sq_h, qi, qs, ki, ks, vi, vscale, TP, kc, vc, npad, counts, lists, mask,
                          static_cast<int>(T), static_cast<int>(H), static_cast<int>(NT), W, c, o,
                          so_b, so_t, so_h);

@@ -242,7 +242,7 @@ moments_kernel(uint16_t* __restrict__ kc, int64_t npad, int NT, int H, int centr
 // for kQB query blocks per workgroup; thread t scores key block j0 + t.
 constexpr int kQB = 8;
 constexpr int kRouteThreads = 256;
-constexpr int kMaxWords = 128;  // NT <= 4096
+constexpr int kMaxWords = 512;  // NT <= 16384 (the forwards' limit)
 constexpr int kKcStride = kHeadDim + 4;  // bf16 per staged kc row (264 B): conflict-free 8-byte reads
 constexpr int kKcLoads = kHeadDim / 8;   // 16-byte loads per thread to stage 256 kc rows
 
@@ -258,7 +258,9 @@ route_kernel(const float* __restrict__ qbar, const uint16_t* __restrict__ kc, in
   __shared__ __align__(16) float sq[kQB][kHeadDim];
   __shared__ float smk[kHeadDim], svk[kHeadDim];
   __shared__ float sthr[kQB];
-  __shared__ uint32_t smask[kQB][kMaxWords];
+  // exact bits of the kQB query blocks, W words each, in dynamic LDS
+  extern __shared__ __align__(16) uint32_t smask_lds[];
+  const auto smask = [&](int i, int w) -> uint32_t& { return smask_lds[i * W + w]; };
   __shared__ __align__(16) uint16_t skc[kRouteThreads * kKcStride];
   const int64_t bh = static_cast<int64_t>(b) * H + h;
   // The prologue's global loads are all issued before any of them is used:
@@ -279,7 +281,7 @@ route_kernel(const float* __restrict__ qbar, const uint16_t* __restrict__ kc, in
       svk[t] = vk;
     }
   }
-  for (int e = t; e < kQB * kMaxWords; e += kRouteThreads) smask[e / kMaxWords][e % kMaxWords] = 0u;
+  for (int e = t; e < kQB * W; e += kRouteThreads) smask_lds[e] = 0u;
   __syncthreads();
   if (t < kQB) {
     float mu = 0.f, var = 0.f;
@@ -361,8 +363,8 @@ route_kernel(const float* __restrict__ qbar, const uint16_t* __restrict__ kc, in
       const uint64_t bal = __ballot(exact);
       const int w0 = (j0 + wave * 64) >> 5;
       if (lane == 0 && w0 < W) {
-        smask[i][w0] = static_cast<uint32_t>(bal);
-        if (w0 + 1 < W) smask[i][w0 + 1] = static_cast<uint32_t>(bal >> 32);
+        smask(i, w0) = static_cast<uint32_t>(bal);
+        if (w0 + 1 < W) smask(i, w0 + 1) = static_cast<uint32_t>(bal >> 32);
       }
     }
   }
@@ -376,7 +378,7 @@ route_kernel(const float* __restrict__ qbar, const uint16_t* __restrict__ kc, in
     int base = 0;
     for (int w0 = 0; w0 < W; w0 += 64) {
       const int w = w0 + lane;
-      const uint32_t word = w < W ? smask[i][w] : 0u;
+      const uint32_t word = w < W ? smask(i, w) : 0u;
       if (w < W) mask[row * W + w] = word;
       const int cnt = __popc(word);
       int incl = cnt;
@@ -492,7 +494,8 @@ extern "C" int solattn_route(const float* qbar, const uint16_t* kc, int64_t npad
   const float c2 = c * c;
   dim3 grid(static_cast<uint32_t>(cdiv(NT, kQB)), static_cast<uint32_t>(H),
             static_cast<uint32_t>(B));
-  hipLaunchKernelGGL(route_kernel, grid, dim3(kRouteThreads), 0,
+  hipLaunchKernelGGL(route_kernel, grid, dim3(kRouteThreads),
+                     static_cast<size_t>(kQB * W * sizeof(uint32_t)),
                      reinterpret_cast<hipStream_t>(stream), qbar, kc, npad,
                      mode == 0 ? kc_mean : kc_var, kc_var, static_cast<int>(H),
                      static_cast<int>(NT), static_cast<int>(W), c, c2, tau, mode, sink_kv_lo,

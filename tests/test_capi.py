@@ -51,9 +51,12 @@ def test_errors_are_reported(capi):
     rc = L.solattn_route(null, null, 1, null, null, 1, 10, 1, 128, 64, 0.1, 1.0, 0, 0, 0, 0, 0,
                          null, null, null, null, null)
     assert rc == -1
-    # more than 2048 query blocks: rejected as unsupported (the node then goes dense)
-    rc = L.solattn_fwd_bf16(*([null, 0, 0, 0] * 3), null, null, 4096, null, null, null,
-                            1, 2049 * 64, 1, 128, 64, 0.1, null, 0, 0, 0, null)
+    # more than 16384 query blocks: rejected as unsupported (the node keeps such calls dense)
+    rc = L.solattn_fwd_bf16(*([null, 0, 0, 0] * 3), null, null, 16448, null, null, null,
+                            1, 16385 * 64, 1, 128, 64, 0.1, null, 0, 0, 0, null)
+    assert rc == -2 and b"exceed" in L.solattn_last_error()
+    rc = L.solattn_route(null, null, 16448, null, null, 1, 16385 * 64, 1, 128, 64, 0.1, 1.0, 0,
+                         0, 0, 0, 0, null, null, null, null, null)
     assert rc == -2 and b"exceed" in L.solattn_last_error()
     with pytest.raises(capi.SolAttnError, match="null pointer"):
         capi.call("solattn_reorder_rows", null, 1, 0, 16, null, 0, 16, 1, 1, 16, null, null)

@@ -249,13 +249,13 @@ def _block_constant_closed_form(q, kb, vb, T, block, dev, chunk=16384):
     return out
 
 
-@pytest.mark.parametrize("block", [64, 128])
-def test_fwd_max_blocks_closed_form(pkg, dev, block):
-    """The largest supported sequence (2048 query/key blocks, ragged last block)
-    with K and V constant inside each block, against the closed form; size-
-    independent, so it runs at the full block count."""
+@pytest.mark.parametrize("block,NT", [(64, 2048), (128, 2048), (64, 16384), (128, 16384)])
+def test_fwd_max_blocks_closed_form(pkg, dev, block, NT):
+    """Long sequences up to the largest supported (16384 query/key blocks:
+    1M tokens at block 64, 2M at block 128; ragged last block) with K and V
+    constant inside each block, against the closed form; size-independent, so
+    it runs at the full block count."""
     tri, i8 = _mods(pkg)[1], _mods(pkg)[2]
-    NT = 2048
     T = NT * block - 17
     print(f"[fwd max NT] block={block} T={T}", flush=True)
     g = torch.Generator().manual_seed(70)
