@@ -10,14 +10,25 @@ from __future__ import annotations
 import torch
 
 from ._capi import call, ptr, stream
-from ._preprocess import BLOCK_SIZE, Routing, as_kernel_input, route
+from ._preprocess import BLOCK_SIZE, HEAD_DIM, Routing, as_kernel_input, pad_heads, route
 
 __all__ = ["fused_preprocess", "fused_preprocess_routing"]
 
 
 def fused_preprocess_routing(q, k, v, *, tau, scale, int8_pv=True, block=BLOCK_SIZE,
                              sink_blocks=(0, 0), sink_q=(0, 0)):
-    """(Routing, qi, qs, ki, ks, vi) -- the INT8 path's inputs to the forward."""
+    """(Routing, qi, qs, ki, ks, vi) -- the INT8 path's inputs to the forward.
+    Head dims below 128 run zero-padded; codes come back for the first D
+    channels (the padded ones are 0)."""
+    D0 = q.shape[-1]
+    if D0 != HEAD_DIM:
+        r, qi, qs, ki, ks, vi = fused_preprocess_routing(
+            pad_heads(q), pad_heads(k), pad_heads(v), tau=tau, scale=scale, int8_pv=int8_pv,
+            block=block, sink_blocks=sink_blocks, sink_q=sink_q)
+        cut = lambda t: None if t is None else t[..., :D0]  # noqa: E731
+        r = r._replace(kc=cut(r.kc), vc=cut(r.vc), qbar=cut(r.qbar), kc_mean=cut(r.kc_mean),
+                       kc_var=cut(r.kc_var), vamax_part=cut(r.vamax_part), vscale=cut(r.vscale))
+        return r, cut(qi), qs, cut(ki), ks, cut(vi)
     r: Routing = route(q, k, v, scale=scale, tau=tau, block=block, int8=True, v_absmax=int8_pv,
                        sink_blocks=sink_blocks, sink_q=sink_q)
     q, k, v = as_kernel_input(q), as_kernel_input(k), as_kernel_input(v)

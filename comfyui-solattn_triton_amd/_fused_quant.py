@@ -11,15 +11,16 @@ from __future__ import annotations
 import torch
 
 from ._capi import call, ptr, stream
-from ._preprocess import HEAD_DIM, as_kernel_input
+from ._preprocess import HEAD_DIM, as_kernel_input, head_dim_ok, pad_heads
 
 __all__ = ["quantize_bthd", "quantize_v_per_channel"]
 
 
 def _check(x):
-    if x.device.type != "cuda" or x.dtype != torch.bfloat16 or x.dim() != 4 or x.shape[-1] != HEAD_DIM:
-        raise ValueError(f"expected a bf16 GPU BTHD tensor with head_dim {HEAD_DIM}, "
-                         f"got {x.dtype} {tuple(x.shape)} on {x.device}")
+    if x.device.type != "cuda" or x.dtype != torch.bfloat16 or x.dim() != 4 or \
+            not head_dim_ok(x.shape[-1]):
+        raise ValueError(f"expected a bf16 GPU BTHD tensor with a head_dim of 8..{HEAD_DIM} "
+                         f"(multiple of 8), got {x.dtype} {tuple(x.shape)} on {x.device}")
 
 
 def quantize_bthd(x, mean=None, rows=16, num_warps=4, out_rows=None):
@@ -27,6 +28,12 @@ def quantize_bthd(x, mean=None, rows=16, num_warps=4, out_rows=None):
     first. ``rows`` / ``num_warps`` are the reference's launch knobs, accepted
     and unused. /root/reference/_fused_quant.py:45-58."""
     _check(x)
+    D0 = x.shape[-1]
+    if D0 != HEAD_DIM:  # padded channels are 0 after smoothing by a 0 mean: same row max
+        if mean is not None:
+            mean = torch.nn.functional.pad(mean.reshape(-1, D0).float(), (0, HEAD_DIM - D0))
+        xi, xs = quantize_bthd(pad_heads(x), mean=mean, out_rows=out_rows)
+        return xi[..., :D0], xs
     x = as_kernel_input(x)
     B, T, H, D = x.shape
     TP = T if out_rows is None else int(out_rows)
@@ -47,6 +54,12 @@ def quantize_v_per_channel(v, rows=16, num_warps=4, out_rows=None, absmax=None):
     [B*H, D]). /root/reference/_fused_quant.py:91-113. ``absmax`` [B, H, D]
     comes from a pass that already read V (the pooling pass does)."""
     _check(v)
+    D0 = v.shape[-1]
+    if D0 != HEAD_DIM:  # padded channels: absmax 0 -> scale 1e-8, codes 0
+        vi, scale = quantize_v_per_channel(pad_heads(v), out_rows=out_rows,
+                                           absmax=None if absmax is None else
+                                           torch.nn.functional.pad(absmax, (0, HEAD_DIM - D0)))
+        return vi[..., :D0], scale[:, :D0]
     v = as_kernel_input(v)
     B, T, H, D = v.shape
     TP = T if out_rows is None else int(out_rows)

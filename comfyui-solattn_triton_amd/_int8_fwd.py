@@ -40,8 +40,9 @@ def sol_attn_int8(q, k, v, *, scale=None, tau=1.0, sink_blocks=(0, 0), sink_q=(0
 
 def forward_int8(q, v, routing: Routing, qi, qs, ki, ks, vi=None, *, scale=None, int8_pv=True,
                  out=None):
-    """The INT8 forward kernel alone, on the outputs of ``fused_preprocess_routing``."""
-    check_inputs(q, q, q, routing.block)
+    """The INT8 forward kernel alone (head dim 128), on the outputs of
+    ``fused_preprocess_routing``."""
+    check_inputs(q, q, q, routing.block, padded_ok=False)
     scale = q.shape[-1] ** -0.5 if scale is None else float(scale)
     q, v = as_kernel_input(q), as_kernel_input(v)
     B, T, H, D = q.shape

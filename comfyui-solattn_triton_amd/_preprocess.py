@@ -20,7 +20,7 @@ BLOCK_SIZE = 64
 # kc/vc are zero-padded to whole chunks of this many blocks
 # (/root/reference/_preprocess.py:15).
 GROUP_PAD = 64
-HEAD_DIM = 128
+HEAD_DIM = 128  # the kernels' head dim; smaller heads are zero-padded to it
 SUPPORTED_BLOCKS = (64, 128)
 MAX_BLOCKS = 16384  # query/key blocks per head the forward kernels accept
 
@@ -50,7 +50,20 @@ def as_kernel_input(t: torch.Tensor) -> torch.Tensor:
     return t if kernel_ready(t) else t.contiguous()
 
 
-def check_inputs(q, k, v, block: int):
+def head_dim_ok(d: int) -> bool:
+    """Head dims the pipelines take: multiples of 8 up to 128 (heads below 128
+    run zero-padded; the padding adds exact zeros to every dot product)."""
+    return 8 <= d <= HEAD_DIM and d % 8 == 0
+
+
+def pad_heads(t: torch.Tensor) -> torch.Tensor:
+    """A BTHD tensor with its head dim zero-padded to HEAD_DIM (on the device)."""
+    if t.shape[-1] == HEAD_DIM:
+        return t
+    return torch.nn.functional.pad(t, (0, HEAD_DIM - t.shape[-1]))
+
+
+def check_inputs(q, k, v, block: int, padded_ok: bool = True):
     if block not in SUPPORTED_BLOCKS:
         raise ValueError(f"block {block} not in {SUPPORTED_BLOCKS}")
     for name, t in (("q", q), ("k", k), ("v", v)):
@@ -62,8 +75,9 @@ def check_inputs(q, k, v, block: int):
             raise ValueError(f"{name} must be BTHD, got shape {tuple(t.shape)}")
     if q.shape != k.shape or k.shape != v.shape:
         raise ValueError(f"q/k/v shapes differ: {tuple(q.shape)} {tuple(k.shape)} {tuple(v.shape)}")
-    if q.shape[-1] != HEAD_DIM:
-        raise ValueError(f"head_dim {q.shape[-1]} != {HEAD_DIM}")
+    if not (head_dim_ok(q.shape[-1]) if padded_ok else q.shape[-1] == HEAD_DIM):
+        raise ValueError(f"head_dim {q.shape[-1]} not supported (multiples of 8 up to {HEAD_DIM}"
+                         f"{'' if padded_ok else '; this entry point takes 128 only'})")
     nt = num_blocks(q.shape[1], block)
     if nt > MAX_BLOCKS:
         raise ValueError(f"{q.shape[1]} tokens make {nt} blocks of {block}; at most {MAX_BLOCKS}")
@@ -101,6 +115,14 @@ def route(q, k, v, *, scale: float, tau: float, block: int = BLOCK_SIZE, int8: b
     also produces the per-channel V scale from the same pass.
     """
     check_inputs(q, k, v, block)
+    D0 = q.shape[-1]
+    if D0 != HEAD_DIM:  # run padded, hand back the first D0 channels
+        r = route(pad_heads(q), pad_heads(k), pad_heads(v), scale=scale, tau=tau, block=block,
+                  int8=int8, v_absmax=v_absmax, sink_blocks=sink_blocks, sink_q=sink_q)
+        cut = lambda t: None if t is None else t[..., :D0]  # noqa: E731
+        return r._replace(kc=cut(r.kc), vc=cut(r.vc), qbar=cut(r.qbar), kc_mean=cut(r.kc_mean),
+                          kc_var=cut(r.kc_var), vamax_part=cut(r.vamax_part),
+                          vscale=cut(r.vscale))
     q, k, v = as_kernel_input(q), as_kernel_input(k), as_kernel_input(v)
     B, T, H, D = q.shape
     NT = num_blocks(T, block)

@@ -36,7 +36,8 @@ def sol_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, scale: float 
              use_tma: bool = False, block: int = BLOCK) -> torch.Tensor:
     """Run Sol-Attn on BTHD bf16 inputs; returns a fresh BTHD bf16 tensor.
 
-    Each query block attends exactly to its routed blocks (score above the
+    Head dims below 128 (multiples of 8) run zero-padded to 128 inside the
+    library call. Each query block attends exactly to its routed blocks (score above the
     Gaussian threshold mu + tau*sigma, the diagonal band |i-j| <= 1 and the
     ``sink_blocks`` KV range) and to one pooled key/value per remaining block;
     query blocks inside ``sink_q`` attend everything exactly.
@@ -58,8 +59,9 @@ def sol_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, scale: float 
 
 def forward_bf16(q, k, v, routing: Routing, *, scale: float | None = None,
                  out: torch.Tensor | None = None) -> torch.Tensor:
-    """The forward kernel alone, on routing produced by ``_preprocess.route``."""
-    check_inputs(q, k, v, routing.block)
+    """The forward kernel alone (head dim 128), on routing produced by
+    ``_preprocess.route``."""
+    check_inputs(q, k, v, routing.block, padded_ok=False)
     scale = q.shape[-1] ** -0.5 if scale is None else float(scale)
     q, k, v = as_kernel_input(q), as_kernel_input(k), as_kernel_input(v)
     B, T, H, D = q.shape

@@ -43,41 +43,57 @@ uint64_t spread3(uint64_t v) {
   return out;
 }
 
+// Head dims the one-call pipelines take: multiples of 8 up to the kernels'
+// 128; smaller heads are zero-padded to 128 in the workspace.
+constexpr int64_t kKernelD = 128;
+inline bool pipeline_head_dim_ok(int64_t D) { return D >= 8 && D <= kKernelD && D % 8 == 0; }
+
 // Carves the pipeline's intermediates out of one workspace.
 struct Layout {
   int64_t NT, npad, W, TP;
   int64_t kc, vc, qbar, kc_mean, kc_var, thr, counts, lists, mask;   // byte offsets
   int64_t vamax, vscale, qi, qs, ki, ks, vi;                          // INT8 only
+  int64_t qp, kp, vp, op;  // zero-padded [B, T, H, 128] q, k, v, o (head dims < 128)
+  bool padded;
   int64_t total;
   Layout(int64_t B, int64_t T, int64_t H, int64_t D, int64_t block, bool int8) {
+    const int64_t Dk = kKernelD;
     NT = cdiv(T, block);
     npad = cdiv(NT, 64) * 64;
     W = cdiv(NT, 32);
     TP = T;
+    padded = D != Dk;
     int64_t off = 0;
     auto take = [&](int64_t bytes) {
       const int64_t at = off;
       off += cdiv(bytes, 256) * 256;
       return at;
     };
-    kc = take(B * npad * H * D * 2);
-    vc = take(B * npad * H * D * 2);
-    qbar = take(B * H * NT * D * 4);
-    kc_mean = take(B * H * D * 4);
-    kc_var = take(B * H * D * 4);
+    kc = take(B * npad * H * Dk * 2);
+    vc = take(B * npad * H * Dk * 2);
+    qbar = take(B * H * NT * Dk * 4);
+    kc_mean = take(B * H * Dk * 4);
+    kc_var = take(B * H * Dk * 4);
     thr = take(B * NT * H * 4);
     counts = take(B * H * NT * 4);
     lists = take(B * H * NT * NT * 2);
     mask = take(B * H * NT * W * 4);
     vamax = vscale = qi = qs = ki = ks = vi = -1;
     if (int8) {
-      vamax = take(B * NT * H * D * 4);
-      vscale = take(B * H * D * 4);
-      qi = take(B * TP * H * D);
+      vamax = take(B * NT * H * Dk * 4);
+      vscale = take(B * H * Dk * 4);
+      qi = take(B * TP * H * Dk);
       qs = take(B * TP * H * 4);
-      ki = take(B * TP * H * D);
+      ki = take(B * TP * H * Dk);
       ks = take(B * TP * H * 4);
-      vi = take(B * TP * H * D);
+      vi = take(B * TP * H * Dk);
+    }
+    qp = kp = vp = op = -1;
+    if (padded) {
+      qp = take(B * T * H * Dk * 2);
+      kp = take(B * T * H * Dk * 2);
+      vp = take(B * T * H * Dk * 2);
+      op = take(B * T * H * Dk * 2);
     }
     total = off;
   }
@@ -130,33 +146,110 @@ extern "C" int64_t solattn_sol_attn_workspace_bytes(int64_t B, int64_t T, int64_
 namespace solattn {
 namespace {
 
+// One call's operands: BTHD q, k, v (element strides), the output and the
+// problem sizes and routing parameters.
+struct Call {
+  const uint16_t* q; int64_t sq_b, sq_t, sq_h;
+  const uint16_t* k; int64_t sk_b, sk_t, sk_h;
+  const uint16_t* v; int64_t sv_b, sv_t, sv_h;
+  uint16_t* o; int64_t so_b, so_t, so_h;
+  int64_t B, T, H, D, block;
+  float scale, tau;
+  int64_t skv_lo, skv_hi, sq_lo, sq_hi;
+};
+
+// Runs fn on the call as the D = 128 kernels see it: unchanged when D is 128,
+// else on zero-padded copies of q, k, v in the workspace with the output
+// sliced back into the caller's o afterwards (zero channels add exact zeros
+// to every dot product and sum).
+template <typename F>
+int with_kernel_head_dim(const Layout& L, void* ws, const Call& c, hipStream_t s, F&& fn) {
+  if (!L.padded) return fn(c);
+  const int64_t Dk = kKernelD, st = c.H * Dk, sb = c.T * st;
+  Call p = c;
+  uint16_t* qp = at<uint16_t>(ws, L.qp);
+  uint16_t* kp = at<uint16_t>(ws, L.kp);
+  uint16_t* vp = at<uint16_t>(ws, L.vp);
+  uint16_t* op = at<uint16_t>(ws, L.op);
+  int rc = pad_heads(c.q, c.sq_b, c.sq_t, c.sq_h, qp, sb, st, Dk, c.B, c.T, c.H, c.D, Dk, s);
+  if (!rc) rc = pad_heads(c.k, c.sk_b, c.sk_t, c.sk_h, kp, sb, st, Dk, c.B, c.T, c.H, c.D, Dk, s);
+  if (!rc) rc = pad_heads(c.v, c.sv_b, c.sv_t, c.sv_h, vp, sb, st, Dk, c.B, c.T, c.H, c.D, Dk, s);
+  if (rc) return rc;
+  p.q = qp; p.k = kp; p.v = vp; p.o = op;
+  p.sq_b = p.sk_b = p.sv_b = p.so_b = sb;
+  p.sq_t = p.sk_t = p.sv_t = p.so_t = st;
+  p.sq_h = p.sk_h = p.sv_h = p.so_h = Dk;
+  p.D = Dk;
+  if ((rc = fn(p))) return rc;
+  return pad_heads(op, sb, st, Dk, c.o, c.so_b, c.so_t, c.so_h, c.B, c.T, c.H, Dk, c.D, s);
+}
+
 // pool -> moments -> route -> fwd_bf16 over the intermediates of `L` carved
 // out of ws (256-byte aligned, at least L.total bytes; nothing in it needs to
 // start zeroed: every byte a later stage reads is written by an earlier one).
-int run_bf16_pipeline(const Layout& L, void* ws, const uint16_t* q, int64_t sq_b, int64_t sq_t,
-                      int64_t sq_h, const uint16_t* k, int64_t sk_b, int64_t sk_t, int64_t sk_h,
-                      const uint16_t* v, int64_t sv_b, int64_t sv_t, int64_t sv_h, int64_t B,
-                      int64_t T, int64_t H, int64_t D, int64_t block, float scale, float tau,
-                      int64_t sink_kv_lo, int64_t sink_kv_hi, int64_t sink_q_lo,
-                      int64_t sink_q_hi, uint16_t* o, int64_t so_b, int64_t so_t, int64_t so_h,
+int run_bf16_pipeline(const Layout& L, void* ws, const Call& call, solattn_stream_t stream) {
+  return with_kernel_head_dim(L, ws, call, reinterpret_cast<hipStream_t>(stream), [&](const Call& c) {
+    int rc = solattn_pool(c.q, c.sq_b, c.sq_t, c.sq_h, c.k, c.sk_b, c.sk_t, c.sk_h, c.v, c.sv_b,
+                          c.sv_t, c.sv_h, c.B, c.T, c.H, c.D, c.block, at<uint16_t>(ws, L.kc),
+                          at<uint16_t>(ws, L.vc), L.npad, at<float>(ws, L.qbar), nullptr, stream);
+    if (rc) return rc;
+    rc = solattn_moments(at<uint16_t>(ws, L.kc), L.npad, c.B, L.NT, c.H, c.D, 0,
+                         at<float>(ws, L.kc_mean), at<float>(ws, L.kc_var), nullptr, nullptr, stream);
+    if (rc) return rc;
+    rc = solattn_route(at<float>(ws, L.qbar), at<uint16_t>(ws, L.kc), L.npad,
+                       at<float>(ws, L.kc_mean), at<float>(ws, L.kc_var), c.B, c.T, c.H, c.D,
+                       c.block, c.scale, c.tau, 0, c.skv_lo, c.skv_hi, c.sq_lo, c.sq_hi,
+                       at<float>(ws, L.thr), at<int32_t>(ws, L.counts), at<int16_t>(ws, L.lists),
+                       at<uint32_t>(ws, L.mask), stream);
+    if (rc) return rc;
+    return solattn_fwd_bf16(c.q, c.sq_b, c.sq_t, c.sq_h, c.k, c.sk_b, c.sk_t, c.sk_h, c.v, c.sv_b,
+                            c.sv_t, c.sv_h, at<uint16_t>(ws, L.kc), at<uint16_t>(ws, L.vc), L.npad,
+                            at<int32_t>(ws, L.counts), at<int16_t>(ws, L.lists),
+                            at<uint32_t>(ws, L.mask), c.B, c.T, c.H, c.D, c.block, c.scale, c.o,
+                            c.so_b, c.so_t, c.so_h, stream);
+  });
+}
+
+// pool -> moments(centre) -> route(mode 1) -> quant(q, k smoothed, v) -> fwd_int8.
+int run_int8_pipeline(const Layout& L, void* ws, const Call& call, int int8_pv,
                       solattn_stream_t stream) {
-  int rc = solattn_pool(q, sq_b, sq_t, sq_h, k, sk_b, sk_t, sk_h, v, sv_b, sv_t, sv_h, B, T, H, D,
-                        block, at<uint16_t>(ws, L.kc), at<uint16_t>(ws, L.vc), L.npad,
-                        at<float>(ws, L.qbar), nullptr, stream);
-  if (rc) return rc;
-  rc = solattn_moments(at<uint16_t>(ws, L.kc), L.npad, B, L.NT, H, D, 0, at<float>(ws, L.kc_mean),
-                       at<float>(ws, L.kc_var), nullptr, nullptr, stream);
-  if (rc) return rc;
-  rc = solattn_route(at<float>(ws, L.qbar), at<uint16_t>(ws, L.kc), L.npad, at<float>(ws, L.kc_mean),
-                     at<float>(ws, L.kc_var), B, T, H, D, block, scale, tau, 0, sink_kv_lo,
-                     sink_kv_hi, sink_q_lo, sink_q_hi, at<float>(ws, L.thr), at<int32_t>(ws, L.counts),
-                     at<int16_t>(ws, L.lists), at<uint32_t>(ws, L.mask), stream);
-  if (rc) return rc;
-  return solattn_fwd_bf16(q, sq_b, sq_t, sq_h, k, sk_b, sk_t, sk_h, v, sv_b, sv_t, sv_h,
-                          at<uint16_t>(ws, L.kc), at<uint16_t>(ws, L.vc), L.npad,
-                          at<int32_t>(ws, L.counts), at<int16_t>(ws, L.lists),
-                          at<uint32_t>(ws, L.mask), B, T, H, D, block, scale, o, so_b, so_t, so_h,
-                          stream);
+  hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
+  return with_kernel_head_dim(L, ws, call, hs, [&](const Call& c) {
+    float* vamax = int8_pv ? at<float>(ws, L.vamax) : nullptr;
+    float* vscale = int8_pv ? at<float>(ws, L.vscale) : nullptr;
+    int rc = solattn_pool(c.q, c.sq_b, c.sq_t, c.sq_h, c.k, c.sk_b, c.sk_t, c.sk_h, c.v, c.sv_b,
+                          c.sv_t, c.sv_h, c.B, c.T, c.H, c.D, c.block, at<uint16_t>(ws, L.kc),
+                          at<uint16_t>(ws, L.vc), L.npad, at<float>(ws, L.qbar), vamax, stream);
+    if (rc) return rc;
+    rc = solattn_moments(at<uint16_t>(ws, L.kc), L.npad, c.B, L.NT, c.H, c.D, 1,
+                         at<float>(ws, L.kc_mean), at<float>(ws, L.kc_var), vamax, vscale, stream);
+    if (rc) return rc;
+    rc = solattn_route(at<float>(ws, L.qbar), at<uint16_t>(ws, L.kc), L.npad, nullptr,
+                       at<float>(ws, L.kc_var), c.B, c.T, c.H, c.D, c.block, c.scale, c.tau, 1,
+                       c.skv_lo, c.skv_hi, c.sq_lo, c.sq_hi, at<float>(ws, L.thr),
+                       at<int32_t>(ws, L.counts), at<int16_t>(ws, L.lists),
+                       at<uint32_t>(ws, L.mask), stream);
+    if (rc) return rc;
+    rc = quant_qkv(c.q, c.sq_b, c.sq_t, c.sq_h, c.k, c.sk_b, c.sk_t, c.sk_h, c.v, c.sv_b, c.sv_t,
+                   c.sv_h, c.B, c.T, c.H, c.D, at<float>(ws, L.kc_mean), vscale,
+                   at<int8_t>(ws, L.qi), at<float>(ws, L.qs), at<int8_t>(ws, L.ki),
+                   at<float>(ws, L.ks), int8_pv ? at<int8_t>(ws, L.vi) : nullptr, L.TP, hs);
+    if (rc) return rc;
+    return solattn_fwd_int8(c.q, c.sq_b, c.sq_t, c.sq_h, at<int8_t>(ws, L.qi), at<float>(ws, L.qs),
+                            at<int8_t>(ws, L.ki), at<float>(ws, L.ks),
+                            int8_pv ? at<int8_t>(ws, L.vi) : nullptr, vscale, c.v, c.sv_b, c.sv_t,
+                            c.sv_h, L.TP, at<uint16_t>(ws, L.kc), at<uint16_t>(ws, L.vc), L.npad,
+                            at<int32_t>(ws, L.counts), at<int16_t>(ws, L.lists),
+                            at<uint32_t>(ws, L.mask), c.B, c.T, c.H, c.D, c.block, c.scale,
+                            int8_pv, c.o, c.so_b, c.so_t, c.so_h, stream);
+  });
+}
+
+int check_pipeline(int64_t B, int64_t T, int64_t H, int64_t D, int64_t block, const char* what) {
+  SOLATTN_REQUIRE(B > 0 && T > 0 && H > 0 && block > 0, SOLATTN_EINVAL, "%s: bad sizes", what);
+  SOLATTN_REQUIRE(pipeline_head_dim_ok(D), SOLATTN_EUNSUPPORTED,
+                  "%s: head_dim %lld (multiples of 8 up to 128)", what, (long long)D);
+  return 0;
 }
 
 // The allocation-free pipeline's intermediates: one fixed array per device,
@@ -209,16 +302,16 @@ extern "C" int solattn_sol_attn(const uint16_t* q, int64_t sq_b, int64_t sq_t, i
                                 int64_t workspace_bytes, uint16_t* o, int64_t so_b, int64_t so_t,
                                 int64_t so_h, solattn_stream_t stream) {
   clear_error();
-  SOLATTN_REQUIRE(B > 0 && T > 0 && H > 0 && block > 0, SOLATTN_EINVAL, "sol_attn: bad sizes");
+  if (int rc = check_pipeline(B, T, H, D, block, "sol_attn")) return rc;
   const Layout L(B, T, H, D, block, false);
   SOLATTN_REQUIRE(workspace && workspace_bytes >= L.total, SOLATTN_ESIZE,
                   "sol_attn: workspace %lld < %lld bytes", (long long)workspace_bytes,
                   (long long)L.total);
   SOLATTN_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, SOLATTN_EINVAL,
                   "sol_attn: workspace must be 256-byte aligned");
-  return run_bf16_pipeline(L, workspace, q, sq_b, sq_t, sq_h, k, sk_b, sk_t, sk_h, v, sv_b, sv_t,
-                           sv_h, B, T, H, D, block, scale, tau, sink_kv_lo, sink_kv_hi, sink_q_lo,
-                           sink_q_hi, o, so_b, so_t, so_h, stream);
+  const Call c{q, sq_b, sq_t, sq_h, k, sk_b, sk_t, sk_h, v, sv_b, sv_t, sv_h, o, so_b, so_t, so_h,
+               B, T, H, D, block, scale, tau, sink_kv_lo, sink_kv_hi, sink_q_lo, sink_q_hi};
+  return run_bf16_pipeline(L, workspace, c, stream);
 }
 
 extern "C" int solattn_sol_attn_noalloc(const uint16_t* q, int64_t sq_b, int64_t sq_t,
@@ -231,8 +324,7 @@ extern "C" int solattn_sol_attn_noalloc(const uint16_t* q, int64_t sq_b, int64_t
                                         uint16_t* o, int64_t so_b, int64_t so_t, int64_t so_h,
                                         solattn_stream_t stream) {
   clear_error();
-  SOLATTN_REQUIRE(B > 0 && T > 0 && H > 0 && block > 0, SOLATTN_EINVAL,
-                  "sol_attn_noalloc: bad sizes");
+  if (int rc = check_pipeline(B, T, H, D, block, "sol_attn_noalloc")) return rc;
   const Layout L(B, T, H, D, block, false);
   SOLATTN_REQUIRE(L.total <= SOLATTN_NOALLOC_SCRATCH_BYTES, SOLATTN_ESIZE,
                   "sol_attn_noalloc: B=%lld T=%lld H=%lld block=%lld needs %lld bytes of "
@@ -242,9 +334,9 @@ extern "C" int solattn_sol_attn_noalloc(const uint16_t* q, int64_t sq_b, int64_t
                   (long long)SOLATTN_NOALLOC_SCRATCH_BYTES);
   void* ws = nullptr;
   if (int rc = scratch_for_current_device(&ws)) return rc;
-  return run_bf16_pipeline(L, ws, q, sq_b, sq_t, sq_h, k, sk_b, sk_t, sk_h, v, sv_b, sv_t, sv_h,
-                           B, T, H, D, block, scale, tau, sink_kv_lo, sink_kv_hi, sink_q_lo,
-                           sink_q_hi, o, so_b, so_t, so_h, stream);
+  const Call c{q, sq_b, sq_t, sq_h, k, sk_b, sk_t, sk_h, v, sv_b, sv_t, sv_h, o, so_b, so_t, so_h,
+               B, T, H, D, block, scale, tau, sink_kv_lo, sink_kv_hi, sink_q_lo, sink_q_hi};
+  return run_bf16_pipeline(L, ws, c, stream);
 }
 
 extern "C" int solattn_sol_attn_int8(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
@@ -257,38 +349,14 @@ extern "C" int solattn_sol_attn_int8(const uint16_t* q, int64_t sq_b, int64_t sq
                                      uint16_t* o, int64_t so_b, int64_t so_t, int64_t so_h,
                                      solattn_stream_t stream) {
   clear_error();
-  SOLATTN_REQUIRE(B > 0 && T > 0 && H > 0 && block > 0, SOLATTN_EINVAL, "sol_attn_int8: bad sizes");
+  if (int rc = check_pipeline(B, T, H, D, block, "sol_attn_int8")) return rc;
   const Layout L(B, T, H, D, block, true);
   SOLATTN_REQUIRE(workspace && workspace_bytes >= L.total, SOLATTN_ESIZE,
                   "sol_attn_int8: workspace %lld < %lld bytes", (long long)workspace_bytes,
                   (long long)L.total);
   SOLATTN_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, SOLATTN_EINVAL,
                   "sol_attn_int8: workspace must be 256-byte aligned");
-  void* ws = workspace;
-  float* vamax = int8_pv ? at<float>(ws, L.vamax) : nullptr;
-  float* vscale = int8_pv ? at<float>(ws, L.vscale) : nullptr;
-  int rc = solattn_pool(q, sq_b, sq_t, sq_h, k, sk_b, sk_t, sk_h, v, sv_b, sv_t, sv_h, B, T, H, D,
-                        block, at<uint16_t>(ws, L.kc), at<uint16_t>(ws, L.vc), L.npad,
-                        at<float>(ws, L.qbar), vamax, stream);
-  if (rc) return rc;
-  rc = solattn_moments(at<uint16_t>(ws, L.kc), L.npad, B, L.NT, H, D, 1, at<float>(ws, L.kc_mean),
-                       at<float>(ws, L.kc_var), vamax, vscale, stream);
-  if (rc) return rc;
-  rc = solattn_route(at<float>(ws, L.qbar), at<uint16_t>(ws, L.kc), L.npad, nullptr,
-                     at<float>(ws, L.kc_var), B, T, H, D, block, scale, tau, 1, sink_kv_lo,
-                     sink_kv_hi, sink_q_lo, sink_q_hi, at<float>(ws, L.thr), at<int32_t>(ws, L.counts),
-                     at<int16_t>(ws, L.lists), at<uint32_t>(ws, L.mask), stream);
-  if (rc) return rc;
-  rc = quant_qkv(q, sq_b, sq_t, sq_h, k, sk_b, sk_t, sk_h, v, sv_b, sv_t, sv_h, B, T, H, D,
-                 at<float>(ws, L.kc_mean), vscale, at<int8_t>(ws, L.qi), at<float>(ws, L.qs),
-                 at<int8_t>(ws, L.ki), at<float>(ws, L.ks), int8_pv ? at<int8_t>(ws, L.vi) : nullptr,
-                 L.TP, reinterpret_cast<hipStream_t>(stream));
-  if (rc) return rc;
-  return solattn_fwd_int8(q, sq_b, sq_t, sq_h, at<int8_t>(ws, L.qi), at<float>(ws, L.qs),
-                          at<int8_t>(ws, L.ki), at<float>(ws, L.ks),
-                          int8_pv ? at<int8_t>(ws, L.vi) : nullptr, vscale, v, sv_b, sv_t, sv_h,
-                          L.TP, at<uint16_t>(ws, L.kc), at<uint16_t>(ws, L.vc), L.npad,
-                          at<int32_t>(ws, L.counts), at<int16_t>(ws, L.lists),
-                          at<uint32_t>(ws, L.mask), B, T, H, D, block, scale, int8_pv, o, so_b,
-                          so_t, so_h, stream);
+  const Call c{q, sq_b, sq_t, sq_h, k, sk_b, sk_t, sk_h, v, sv_b, sv_t, sv_h, o, so_b, so_t, so_h,
+               B, T, H, D, block, scale, tau, sink_kv_lo, sink_kv_hi, sink_q_lo, sink_q_hi};
+  return run_int8_pipeline(L, workspace, c, int8_pv, stream);
 }

@@ -53,6 +53,13 @@ constexpr float kLog2e = 1.4426950408889634f;
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Copies BTHD rows of din bf16 channels into rows of dout channels, zero
+// filled (din < dout), or the first dout channels back out (din > dout)
+// (reorder.hip).
+int pad_heads(const uint16_t* src, int64_t s_b, int64_t s_t, int64_t s_h, uint16_t* dst,
+              int64_t d_b, int64_t d_t, int64_t d_h, int64_t B, int64_t T, int64_t H, int64_t din,
+              int64_t dout, hipStream_t stream);
+
 // Per-token INT8 of q and of k smoothed by k_mean, and (vscale != null)
 // per-channel INT8 of v, in one launch (quant.hip); same codes and scales as
 // solattn_quant_rows / solattn_quant_v.

@@ -50,6 +50,46 @@ reorder_rows_kernel(const char* __restrict__ src, int64_t src_stride_b, int64_t 
   }
 }
 
+// ------------------------------------------------------------- head padding
+// dst[b, t, h, :] = (src[b, t, h, 0:din], zeros) for a dense [B, T, H, dout]
+// destination (pad, din < dout), or the reverse slice src[..., 0:dout] into a
+// strided destination (unpad, din > dout): the one-call pipelines run head
+// dims below 128 on the D = 128 kernels. Zero channels add exact zeros to
+// every dot product and pooled sum, so routing, codes and outputs are those of
+// the unpadded problem. One thread moves 8 bf16 (16 bytes).
+__global__ void __launch_bounds__(256)
+pad_heads_kernel(const uint16_t* __restrict__ src, int64_t s_b, int64_t s_t, int64_t s_h,
+                 uint16_t* __restrict__ dst, int64_t d_b, int64_t d_t, int64_t d_h, int64_t T,
+                 int H, int din, int dout, int64_t rows) {
+  const int per_row = dout / 8;
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (e >= rows * per_row) return;
+  const int64_t row = e / per_row;
+  const int c8 = static_cast<int>(e - row * per_row) * 8;
+  const int64_t h = row % H, bt = row / H, t = bt % T, b = bt / T;
+  uint4 v = make_uint4(0u, 0u, 0u, 0u);
+  if (c8 < din) v = *reinterpret_cast<const uint4*>(src + b * s_b + t * s_t + h * s_h + c8);
+  *reinterpret_cast<uint4*>(dst + b * d_b + t * d_t + h * d_h + c8) = v;
+}
+
+int pad_heads(const uint16_t* src, int64_t s_b, int64_t s_t, int64_t s_h, uint16_t* dst,
+              int64_t d_b, int64_t d_t, int64_t d_h, int64_t B, int64_t T, int64_t H, int64_t din,
+              int64_t dout, hipStream_t stream) {
+  SOLATTN_REQUIRE(src && dst && din % 8 == 0 && dout % 8 == 0, SOLATTN_EINVAL,
+                  "pad_heads: bad arguments");
+  SOLATTN_REQUIRE(reinterpret_cast<uintptr_t>(src) % 16 == 0 && reinterpret_cast<uintptr_t>(dst) % 16 == 0 &&
+                      s_b % 8 == 0 && s_t % 8 == 0 && s_h % 8 == 0 && d_b % 8 == 0 &&
+                      d_t % 8 == 0 && d_h % 8 == 0,
+                  SOLATTN_EINVAL, "pad_heads: rows must be 16-byte aligned");
+  const int64_t rows = B * T * H;
+  const int64_t work = rows * (dout / 8);
+  SOLATTN_REQUIRE(cdiv(work, 256) < (1ll << 31), SOLATTN_EUNSUPPORTED, "pad_heads: too large");
+  hipLaunchKernelGGL(pad_heads_kernel, dim3(static_cast<uint32_t>(cdiv(work, 256))), dim3(256), 0,
+                     stream, src, s_b, s_t, s_h, dst, d_b, d_t, d_h, T, static_cast<int>(H),
+                     static_cast<int>(din), static_cast<int>(dout), rows);
+  return check_launch("pad_heads");
+}
+
 }  // namespace solattn
 
 using namespace solattn;
@@ -87,3 +127,4 @@ extern "C" int solattn_reorder_rows(const void* src, int64_t src_rows, int64_t s
                      static_cast<uint32_t>(rows), cpr, rows_per_wg);
   return check_launch("reorder_rows");
 }
+

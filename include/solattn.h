@@ -14,8 +14,14 @@
  *    records a message readable with solattn_last_error() (thread-local).
  *  - The library never allocates device memory and never synchronises: every
  *    launch goes on the hipStream_t passed in (NULL = the null stream).
- *  - head_dim must be 128 on the device paths (the reference's only eligible
- *    head size, /root/reference/__init__.py:41,178).
+ *  - head_dim must be 128 for the per-kernel entry points (the reference
+ *    node's only eligible head size, /root/reference/__init__.py:41,178); the
+ *    one-call pipelines (solattn_sol_attn*) also take head dims that are
+ *    multiples of 8 below 128 (the reference kernels' D = 64 configs,
+ *    /root/reference/_tri_fwd.py:209), running them zero-padded to 128 in the
+ *    workspace: zero channels add exact zeros to every dot product and sum,
+ *    so routing, codes and outputs are those of the unpadded problem, at the
+ *    cost of a D = 128 call.
  *
  * Arithmetic contract (the CPU oracle restates the same operation order, so
  * pooled keys, thresholds, routing lists and INT8 codes are bit-exact):

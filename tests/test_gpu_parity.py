@@ -320,3 +320,57 @@ def test_wan_hooks_neutral_through_gather_kernel(pkg, dev, curve):
     print(f"[wan hooks] max |hooked - plain| = {err:.3e}", flush=True)
     assert err < BF16_MAXABS
     assert cosine(hooked.float().cpu().numpy(), plain.float().cpu().numpy()) >= BF16_COS
+
+
+@pytest.mark.parametrize("mode", ["bf16", "int8_pv", "int8_bf16pv"])
+@pytest.mark.parametrize("case", ["cfg0", "random"])
+def test_head_dim_64(pkg, dev, mode, case):
+    """Head dim 64 (BASELINE config 0's shape, and a ragged random case): the
+    one-call pipelines run the heads zero-padded to 128, so routing and INT8
+    codes must equal the oracle's D = 64 computation bit for bit and the
+    forward must meet the usual tolerances against the reference loop."""
+    import importlib
+    import bench
+    prep, tri, i8 = _mods(pkg)[0], _mods(pkg)[1], _mods(pkg)[2]
+    fp = importlib.import_module(f"{pkg.__name__}._fused_prep")
+    if case == "cfg0":
+        cfg = bench.CONFIGS[0]
+        q, k, v = bench.make_inputs(cfg, "cpu", dtype=torch.float32)
+        perm, _ = oracle.morton_perm(cfg["grid"], "3d")
+        q, k, v = (t[:, perm].to(torch.bfloat16).contiguous() for t in (q, k, v))
+        block, tau = cfg["block"], cfg["tau"]
+    else:
+        q, k, v = (randn_bf16((2, 1000, 3, 64), s) for s in (80, 81, 82))
+        block, tau = 128, 0.7
+    B, T, H, D = q.shape
+    print(f"[d64] case={case} mode={mode} shape={tuple(q.shape)} block={block}", flush=True)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    int8 = mode != "bf16"
+    pv = mode == "int8_pv"
+    ref = oracle.prepare(bits(q), bits(k), bits(v), block=block, tau=tau, int8=int8, int8_pv=pv)
+    if int8:
+        r, qi, qs, ki, ks, vi = fp.fused_preprocess_routing(qd, kd, vd, tau=tau, scale=D ** -0.5,
+                                                            int8_pv=pv, block=block)
+        assert np.array_equal(qi.cpu().numpy(), ref["qi"]) and np.array_equal(ki.cpu().numpy(), ref["ki"])
+        assert np.array_equal(ks.cpu().numpy().view(np.uint32), ref["ks"].view(np.uint32))
+        if pv:
+            assert np.array_equal(vi.cpu().numpy(), ref["vi"])
+        out = i8.sol_attn_int8(qd, kd, vd, tau=tau, block=block, int8_pv=pv)
+    else:
+        r = prep.route(qd, kd, vd, scale=D ** -0.5, tau=tau, block=block)
+        out = tri.sol_attn(qd, kd, vd, tau=tau, block=block)
+    torch.cuda.synchronize()
+    assert out.shape == (B, T, H, D)
+    NT = ref["NT"]
+    assert np.array_equal(bits(r.kc)[:, :NT], ref["kc"][:, :NT])
+    assert np.array_equal(r.threshold.cpu().numpy().view(np.uint32), ref["thr"].view(np.uint32))
+    assert np.array_equal(u32(r.mask), ref["mask"]) and np.array_equal(r.counts.cpu().numpy(), ref["counts"])
+    rows = _rows(B, H, NT, limit=48, seed=3)
+    if int8:
+        check_int8_blocks(f"d64 {case} {mode}", out.float().cpu().numpy(), bits(q), bits(v), ref,
+                          rows, pv, block)
+    else:
+        port = oracle.forward_port(bits(q), bits(k), bits(v), ref, rows)
+        err, cos = compare_rows(out.float().cpu().numpy(), port, block)
+        print(f"[d64 {case} bf16] max|err|={err:.3e} cos={cos:.6f}", flush=True)
+        assert err < BF16_MAXABS and cos >= BF16_COS
