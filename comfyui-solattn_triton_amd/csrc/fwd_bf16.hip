@@ -319,14 +319,14 @@ fwd_bf16_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
   CopyOffsets<NTHREADS> off;
   off.init(sk_t, sv_t);
   const uint32_t kb = lds_addr(kbuf[0]), vb = lds_addr(vbuf[0]);  // LDS byte addresses
-  const auto issue_k = [&](int e, int buf) {
-    const int first = exact_first<BLK>(tl, e);
+  const auto issue_k_at = [&](int first, int buf) {
     issue_full<NTHREADS>(kb + buf * kTileBytes, src.k + static_cast<int64_t>(first) * src.sk, src.sk, off.k);
   };
-  const auto issue_v = [&](int e, int buf) {
-    const int first = exact_first<BLK>(tl, e);
+  const auto issue_v_at = [&](int first, int buf) {
     issue_full<NTHREADS>(vb + buf * kTileBytes, src.v + static_cast<int64_t>(first) * src.sv, src.sv, off.v);
   };
+  const auto issue_k = [&](int e, int buf) { issue_k_at(exact_first<BLK>(tl, e), buf); };
+  const auto issue_v = [&](int e, int buf) { issue_v_at(exact_first<BLK>(tl, e), buf); };
   // Plain tile p: the ragged exact tile (p < nrag), then the pooled tiles.
   const auto plain_desc = [&](int p) {
     return p < nrag ? exact_desc<BLK>(tl, tl.nexact - 1, T, NT) : pooled_desc(tl, p - nrag, NT);
@@ -387,16 +387,25 @@ fwd_bf16_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
       const uint32_t vl0 = v_lane(vb, lane);
       bf16x8 pa[4], pb[4];
       issue_k(min(2, E - 1), 0);
+      // First token rows of the tiles the next step copies, read from the LDS
+      // list one step ahead: each step issues its copies from scalars it
+      // already holds instead of waiting on an LDS read first.
+      int kf = exact_first<BLK>(tl, min(3, E - 1)), vf = exact_first<BLK>(tl, 1);
       step3<true, false>(st, sa, sb, pb, pa, kl0 + kTileBytes, 0u, qreg, c);
       wait_tile_copies();
       __syncthreads();
       int n = 1;  // S(n) in sb, P(n-1) in pa
       const auto gstep = [&](const f32x16 (&sc)[2], f32x16 (&sn)[2], const bf16x8 (&pp)[4],
                              bf16x8 (&pn)[4]) {
-        issue_k(min(n + 2, E - 1), n & 1);
-        issue_v(n, n & 1);
+        issue_k_at(kf, n & 1);  // K(min(n + 2, E - 1))
+        issue_v_at(vf, n & 1);  // V(n)
         step3<true, true>(st, sc, sn, pp, pn, kl0 + ((n + 1) & 1) * kTileBytes,
                           vl0 + ((n - 1) & 1) * kTileBytes, qreg, c);
+        // after the MFMA stream, so the read's latency overlaps the copy wait
+        // and the barrier below rather than delaying this step's first MFMAs
+        asm volatile("" ::: "memory");
+        kf = exact_first<BLK>(tl, min(n + 3, E - 1));
+        vf = exact_first<BLK>(tl, n + 1);
         wait_tile_copies();
         __syncthreads();
         ++n;
@@ -406,7 +415,7 @@ fwd_bf16_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
       const auto last = [&](const f32x16 (&sc)[2], f32x16 (&dummy)[2], const bf16x8 (&pp)[4],
                             bf16x8 (&pn)[4]) {
         pbuf = (n - 1) & 1;
-        issue_v(n, n & 1);
+        issue_v_at(vf, n & 1);  // V(n)
         if (nplain > 0) issue_plain_k(0, pbuf);
         step3<false, true>(st, sc, dummy, pp, pn, 0u, vl0 + pbuf * kTileBytes, qreg, c);
         if (nplain > 0)
