@@ -184,14 +184,15 @@ fwd_bf16_sbuf_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t,
   CopyOffsets<NTHREADS> off;
   off.init(sk_t, sv_t);
   const uint32_t kb = lds_addr(kbuf), vb = lds_addr(vbuf);  // LDS byte addresses
-  const auto issue_k = [&](int n) {
-    const int first = exact_first<BLK>(tl, n - nplain);
+  const auto first_of = [&](int n) { return exact_first<BLK>(tl, n - nplain); };
+  const auto issue_k_at = [&](int first) {
     issue_full<NTHREADS>(kb, src.k + static_cast<int64_t>(first) * src.sk, src.sk, off.k);
   };
-  const auto issue_v = [&](int n) {
-    const int first = exact_first<BLK>(tl, n - nplain);
+  const auto issue_v_at = [&](int first) {
     issue_full<NTHREADS>(vb, src.v + static_cast<int64_t>(first) * src.sv, src.sv, off.v);
   };
+  const auto issue_k = [&](int n) { issue_k_at(first_of(n)); };
+  const auto issue_v = [&](int n) { issue_v_at(first_of(n)); };
   const auto issue_tile = [&](int n) {
     if (n >= nplain) {
       issue_k(n);
@@ -246,16 +247,24 @@ fwd_bf16_sbuf_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t,
     wait_tile_copies();
     __syncthreads();  // K(F+1) and V(F) in LDS
     // Step n computes S(n+1) and needs n + 1 < ntiles. On entry kbuf holds
-    // K(n+1), vbuf V(n) (copy possibly in flight).
+    // K(n+1), vbuf V(n) (copy possibly in flight). The first token rows of
+    // the step's two copies were read from the LDS list in the step before
+    // (kf, vf), so no copy waits on an LDS read.
+    int kf = first_of(min(n + 2, ntiles - 1)), vf = first_of(n + 1);
     const auto step = [&](f32x16 (&sc)[2], f32x16 (&sn)[2]) {
       fast_step(st, sc, sn, kbuf, vbuf, qreg, c, lane, [&] {
         wait_tile_copies();  // V(n)
         __syncthreads();     // every wave is done with K(n+1)
-        issue_k(min(n + 2, ntiles - 1));
+        issue_k_at(kf);      // K(min(n + 2, ntiles - 1))
       });
+      asm volatile("" ::: "memory");  // the list reads stay behind the MFMA stream
+      const int kf_next = first_of(min(n + 3, ntiles - 1));
+      const int vf_next = first_of(min(n + 2, ntiles - 1));
       wait_tile_copies();  // K(n+2)
       __syncthreads();     // every wave is done with V(n)
-      issue_v(n + 1);
+      issue_v_at(vf);      // V(n + 1)
+      kf = kf_next;
+      vf = vf_next;
       ++n;
     };
     // Pairs of steps, so the S buffers swap roles without register copies.
