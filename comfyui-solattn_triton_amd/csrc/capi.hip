@@ -217,9 +217,12 @@ int run_int8_pipeline(const Layout& L, void* ws, const Call& call, int int8_pv,
   return with_kernel_head_dim(L, ws, call, hs, [&](const Call& c) {
     float* vamax = int8_pv ? at<float>(ws, L.vamax) : nullptr;
     float* vscale = int8_pv ? at<float>(ws, L.vscale) : nullptr;
-    int rc = solattn_pool(c.q, c.sq_b, c.sq_t, c.sq_h, c.k, c.sk_b, c.sk_t, c.sk_h, c.v, c.sv_b,
+    // the pooling pass also quantises Q (the only tensor whose codes need no
+    // statistic over the whole head), so Q is read once
+    int rc = pool_checked(c.q, c.sq_b, c.sq_t, c.sq_h, c.k, c.sk_b, c.sk_t, c.sk_h, c.v, c.sv_b,
                           c.sv_t, c.sv_h, c.B, c.T, c.H, c.D, c.block, at<uint16_t>(ws, L.kc),
-                          at<uint16_t>(ws, L.vc), L.npad, at<float>(ws, L.qbar), vamax, stream);
+                          at<uint16_t>(ws, L.vc), L.npad, at<float>(ws, L.qbar), vamax,
+                          at<int8_t>(ws, L.qi), at<float>(ws, L.qs), L.TP, hs);
     if (rc) return rc;
     rc = solattn_moments(at<uint16_t>(ws, L.kc), L.npad, c.B, L.NT, c.H, c.D, 1,
                          at<float>(ws, L.kc_mean), at<float>(ws, L.kc_var), vamax, vscale, stream);
@@ -230,7 +233,7 @@ int run_int8_pipeline(const Layout& L, void* ws, const Call& call, int int8_pv,
                        at<int32_t>(ws, L.counts), at<int16_t>(ws, L.lists),
                        at<uint32_t>(ws, L.mask), stream);
     if (rc) return rc;
-    rc = quant_qkv(c.q, c.sq_b, c.sq_t, c.sq_h, c.k, c.sk_b, c.sk_t, c.sk_h, c.v, c.sv_b, c.sv_t,
+    rc = quant_qkv(nullptr, c.sq_b, c.sq_t, c.sq_h, c.k, c.sk_b, c.sk_t, c.sk_h, c.v, c.sv_b, c.sv_t,
                    c.sv_h, c.B, c.T, c.H, c.D, at<float>(ws, L.kc_mean), vscale,
                    at<int8_t>(ws, L.qi), at<float>(ws, L.qs), at<int8_t>(ws, L.ki),
                    at<float>(ws, L.ks), int8_pv ? at<int8_t>(ws, L.vi) : nullptr, L.TP, hs);

@@ -53,6 +53,20 @@ constexpr float kLog2e = 1.4426950408889634f;
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// The pooling pass (prep.hip) with, when qi != null, the per-token INT8 of q
+// (codes qi [B, TP, H, 128], scales qs [B, TP, H]) in the same read;
+// pool_checked validates the arguments as solattn_pool does.
+int pool_checked(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h, const uint16_t* k,
+                 int64_t sk_b, int64_t sk_t, int64_t sk_h, const uint16_t* v, int64_t sv_b,
+                 int64_t sv_t, int64_t sv_h, int64_t B, int64_t T, int64_t H, int64_t D,
+                 int64_t block, uint16_t* kc, uint16_t* vc, int64_t npad, float* qbar,
+                 float* vamax_part, int8_t* qi, float* qs, int64_t TP, hipStream_t s);
+int launch_pool(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h, const uint16_t* k,
+                int64_t sk_b, int64_t sk_t, int64_t sk_h, const uint16_t* v, int64_t sv_b,
+                int64_t sv_t, int64_t sv_h, int64_t B, int64_t T, int64_t H, int64_t block,
+                uint16_t* kc, uint16_t* vc, int64_t npad, float* qbar, float* vamax_part,
+                int8_t* qi, float* qs, int64_t TP, hipStream_t s);
+
 // Copies BTHD rows of din bf16 channels into rows of dout channels, zero
 // filled (din < dout), or the first dout channels back out (din > dout)
 // (reorder.hip).
@@ -60,9 +74,9 @@ int pad_heads(const uint16_t* src, int64_t s_b, int64_t s_t, int64_t s_h, uint16
               int64_t d_b, int64_t d_t, int64_t d_h, int64_t B, int64_t T, int64_t H, int64_t din,
               int64_t dout, hipStream_t stream);
 
-// Per-token INT8 of q and of k smoothed by k_mean, and (vscale != null)
-// per-channel INT8 of v, in one launch (quant.hip); same codes and scales as
-// solattn_quant_rows / solattn_quant_v.
+// Per-token INT8 of q (skipped when q is null) and of k smoothed by k_mean,
+// and (vscale != null) per-channel INT8 of v, in one launch (quant.hip); same
+// codes and scales as solattn_quant_rows / solattn_quant_v.
 int quant_qkv(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h, const uint16_t* k,
               int64_t sk_b, int64_t sk_t, int64_t sk_h, const uint16_t* v, int64_t sv_b,
               int64_t sv_t, int64_t sv_h, int64_t B, int64_t T, int64_t H, int64_t D,

@@ -4,13 +4,16 @@
 // where it is written, so the CPU oracle (oracle/solattn_oracle.c) reproduces
 // kc, vc, qbar, thresholds and routing lists bit for bit.
 //
-//  pool    one pass over q, k, v per (block, head): 3 waves, one per tensor,
-//          each lane holding 8 channels of one row in 16-byte loads; HBM-bound.
+//  pool    one pass over q, k, v: four waves per (block, tensor, 4 heads),
+//          wave w summing rows w (mod 4), each lane 8 channels of one head in
+//          16-byte loads; HBM-bound; optionally quantises Q on the way (the
+//          INT8 path).
 //  moments per-head kc mean / variance over blocks (+ INT8 centring, V scale).
 //  route   thresholds, scores R[i][j] and per-query-block exact lists / masks.
 #include <algorithm>
 
 #include "common.hpp"
+#include "quant_common.hpp"
 
 namespace solattn {
 
@@ -18,74 +21,151 @@ constexpr int kHeadDim = 128;
 
 // ------------------------------------------------------------------ pool --
 // /root/reference/_preprocess.py:23-113 (kc = sum/len, vc = sum, |v| max) and
-// the q centroid of :140-149. Rows r of a block are split over 4 lane groups
-// (r % 4 == lane / 16), each summing its rows in ascending order; the partials
-// are combined (p0 + p1) + (p2 + p3) with two xor shuffles.
-template <int BLK>
-__global__ void __launch_bounds__(192)
+// the q centroid of :140-149. A workgroup is four waves over (block j, tensor,
+// four heads): lane l holds head 4g + l/16 and channels 8(l%16)..+7, so each
+// 16-byte load instruction of a wave reads four adjacent heads of one token
+// (1 KiB contiguous for a dense BTHD tensor). Wave w sums the rows r = w
+// (mod 4) of the block in ascending order, the partial p_w of the arithmetic
+// contract; the partials meet in LDS and wave 0 combines (p0 + p1) + (p2 + p3).
+// The three tensors of one (block, head group) are adjacent in the grid.
+// With qi != null the Q workgroups also quantise each Q row per token
+// (/root/reference/_fused_prep.py:42-48, the codes of quant_common.hpp), so
+// the INT8 path reads Q once.
+constexpr int kPoolHeads = 4;   // heads per workgroup
+constexpr int kPoolWaves = 4;   // = the contract's 4 partials
+constexpr int kPoolUnroll = 8;  // rows in flight per lane
+
+// The eight bf16 of a 16-byte load as floats.
+__device__ __forceinline__ void unpack8(const uint4& w, float (&x)[8]) {
+  x[0] = lo_bf16(w.x); x[1] = hi_bf16(w.x); x[2] = lo_bf16(w.y); x[3] = hi_bf16(w.y);
+  x[4] = lo_bf16(w.z); x[5] = hi_bf16(w.z); x[6] = lo_bf16(w.w); x[7] = hi_bf16(w.w);
+}
+
+// p += x and (AMAX) am = max(am, |x|) for a row inside the block; a row past
+// T adds 0.0f (p + 0.0f == p: a partial that starts at +0.0f never becomes
+// -0.0f).
+template <bool AMAX>
+__device__ __forceinline__ void pool_row(const float (&x)[8], bool valid, float (&p)[8],
+                                         float (&am)[8]) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float y = valid ? x[e] : 0.f;
+    p[e] = p[e] + y;
+    if (AMAX) am[e] = fmaxf(am[e], fabsf(y));
+  }
+}
+
+template <int BLK, bool QUANT>
+__global__ void __launch_bounds__(64 * kPoolWaves)
 pool_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
             const uint16_t* __restrict__ k, int64_t sk_b, int64_t sk_t, int64_t sk_h,
             const uint16_t* __restrict__ v, int64_t sv_b, int64_t sv_t, int64_t sv_h, int64_t T,
             int H, int NT, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int64_t npad,
-            float* __restrict__ qbar, float* __restrict__ vamax_part) {
-  const int j = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int g = lane >> 4;
+            float* __restrict__ qbar, float* __restrict__ vamax_part, int8_t* __restrict__ qi,
+            float* __restrict__ qs, int64_t TP) {
+  constexpr int kRows = BLK / kPoolWaves;  // rows per wave
+  static_assert(kRows % kPoolUnroll == 0, "rows per wave");
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int HG = (H + kPoolHeads - 1) / kPoolHeads;
+  const int tensor = static_cast<int>(blockIdx.x % 3);  // 0 K, 1 V, 2 Q
+  const int cell = static_cast<int>(blockIdx.x / 3);
+  const int j = cell / HG;
+  const int h_lane = (cell % HG) * kPoolHeads + (lane >> 4);
+  const int h = min(h_lane, H - 1);  // lanes past the last head re-read it and store nothing
+  const int b = blockIdx.y;
   const int c8 = (lane & 15) * 8;
   const uint16_t* base;
   int64_t st;
-  if (wave == 0) {
+  if (tensor == 0) {
     base = k + b * sk_b + h * sk_h + c8;
     st = sk_t;
-  } else if (wave == 1) {
+  } else if (tensor == 1) {
     base = v + b * sv_b + h * sv_h + c8;
     st = sv_t;
   } else {
     base = q + b * sq_b + h * sq_h + c8;
     st = sq_t;
   }
+  const bool quant = QUANT && tensor == 2;
   const int64_t t0 = static_cast<int64_t>(j) * BLK;
+  const int len = static_cast<int>(min<int64_t>(BLK, T - t0));
   float p[8], am[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) p[e] = am[e] = 0.f;
-#pragma unroll 8
-  for (int it = 0; it < BLK / 4; ++it) {
-    const int64_t t = t0 + it * 4 + g;
-    uint4 raw = make_uint4(0u, 0u, 0u, 0u);
-    if (t < T) raw = *reinterpret_cast<const uint4*>(base + t * st);
-    const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll 1
+  for (int i0 = 0; i0 < kRows; i0 += kPoolUnroll) {
+    uint4 raw[kPoolUnroll];
+    // unconditional loads (a row past T re-reads the last row) so the eight
+    // are in flight together; the rows past T then add 0.0f
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float lo = lo_bf16(w[e]), hi = hi_bf16(w[e]);
-      p[2 * e] = p[2 * e] + lo;
-      p[2 * e + 1] = p[2 * e + 1] + hi;
-      am[2 * e] = fmaxf(am[2 * e], fabsf(lo));
-      am[2 * e + 1] = fmaxf(am[2 * e + 1], fabsf(hi));
+    for (int u = 0; u < kPoolUnroll; ++u) {
+      const int r = w + kPoolWaves * (i0 + u);
+      raw[u] = *reinterpret_cast<const uint4*>(base + (t0 + min(r, len - 1)) * st);
+    }
+    if (quant) {  // uniform per workgroup
+#pragma unroll
+      for (int u = 0; u < kPoolUnroll; ++u) {
+        const int r = w + kPoolWaves * (i0 + u);
+        float x[8];
+        unpack8(raw[u], x);
+        pool_row<false>(x, r < len, p, am);
+        // A row past T holds row T-1 and a lane past H head H-1: both store
+        // the bytes the owning lane stores, so no store needs a branch.
+        uint2 codes;
+        const float ss = quant_token_row(x, codes);
+        const int64_t row = (static_cast<int64_t>(b) * TP + t0 + min(r, len - 1)) * H + h;
+        *reinterpret_cast<uint2*>(qi + row * kHeadDim + c8) = codes;
+        qs[row] = ss;
+      }
+    } else {  // (|max| is kept for V; K and unquantised Q ignore it)
+#pragma unroll
+      for (int u = 0; u < kPoolUnroll; ++u) {
+        float x[8];
+        unpack8(raw[u], x);
+        pool_row<true>(x, w + kPoolWaves * (i0 + u) < len, p, am);
+      }
     }
   }
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    p[e] = p[e] + __shfl_xor(p[e], 16);
-    p[e] = p[e] + __shfl_xor(p[e], 32);
-    am[e] = fmaxf(am[e], __shfl_xor(am[e], 16));
-    am[e] = fmaxf(am[e], __shfl_xor(am[e], 32));
+  // partials of waves 1..3 (and their |max|) through LDS to wave 0
+  __shared__ float4 part[kPoolWaves - 1][4][64];
+  if (w > 0) {
+    part[w - 1][0][lane] = make_float4(p[0], p[1], p[2], p[3]);
+    part[w - 1][1][lane] = make_float4(p[4], p[5], p[6], p[7]);
+    part[w - 1][2][lane] = make_float4(am[0], am[1], am[2], am[3]);
+    part[w - 1][3][lane] = make_float4(am[4], am[5], am[6], am[7]);
   }
-  if (g != 0) return;
-  const float flen = static_cast<float>(min<int64_t>(BLK, T - t0));
+  __syncthreads();
+  if (w > 0 || h_lane >= H) return;
+  float pw[kPoolWaves - 1][8];
+#pragma unroll
+  for (int i = 0; i < kPoolWaves - 1; ++i) {
+    const float4 lo = part[i][0][lane], hi = part[i][1][lane];
+    const float4 alo = part[i][2][lane], ahi = part[i][3][lane];
+    pw[i][0] = lo.x, pw[i][1] = lo.y, pw[i][2] = lo.z, pw[i][3] = lo.w;
+    pw[i][4] = hi.x, pw[i][5] = hi.y, pw[i][6] = hi.z, pw[i][7] = hi.w;
+    am[0] = fmaxf(am[0], alo.x), am[1] = fmaxf(am[1], alo.y);
+    am[2] = fmaxf(am[2], alo.z), am[3] = fmaxf(am[3], alo.w);
+    am[4] = fmaxf(am[4], ahi.x), am[5] = fmaxf(am[5], ahi.y);
+    am[6] = fmaxf(am[6], ahi.z), am[7] = fmaxf(am[7], ahi.w);
+  }
+  float sum[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) sum[e] = (p[e] + pw[0][e]) + (pw[1][e] + pw[2][e]);
+  const float flen = static_cast<float>(len);
   const int64_t kv_off = ((b * npad + j) * H + h) * kHeadDim + c8;
-  if (wave == 0) {
+  if (tensor == 0) {
     uint4 o;
-    o.x = pack_bf16x2(p[0] / flen, p[1] / flen);
-    o.y = pack_bf16x2(p[2] / flen, p[3] / flen);
-    o.z = pack_bf16x2(p[4] / flen, p[5] / flen);
-    o.w = pack_bf16x2(p[6] / flen, p[7] / flen);
+    o.x = pack_bf16x2(sum[0] / flen, sum[1] / flen);
+    o.y = pack_bf16x2(sum[2] / flen, sum[3] / flen);
+    o.z = pack_bf16x2(sum[4] / flen, sum[5] / flen);
+    o.w = pack_bf16x2(sum[6] / flen, sum[7] / flen);
     *reinterpret_cast<uint4*>(kc + kv_off) = o;
-  } else if (wave == 1) {
+  } else if (tensor == 1) {
     uint4 o;
-    o.x = pack_bf16x2(p[0], p[1]);
-    o.y = pack_bf16x2(p[2], p[3]);
-    o.z = pack_bf16x2(p[4], p[5]);
-    o.w = pack_bf16x2(p[6], p[7]);
+    o.x = pack_bf16x2(sum[0], sum[1]);
+    o.y = pack_bf16x2(sum[2], sum[3]);
+    o.z = pack_bf16x2(sum[4], sum[5]);
+    o.w = pack_bf16x2(sum[6], sum[7]);
     *reinterpret_cast<uint4*>(vc + kv_off) = o;
     if (vamax_part) {
       float4* dst = reinterpret_cast<float4*>(
@@ -96,8 +176,8 @@ pool_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int64_t 
   } else {
     float4* dst = reinterpret_cast<float4*>(
         qbar + ((static_cast<int64_t>(b) * H + h) * NT + j) * kHeadDim + c8);
-    dst[0] = make_float4(p[0] / flen, p[1] / flen, p[2] / flen, p[3] / flen);
-    dst[1] = make_float4(p[4] / flen, p[5] / flen, p[6] / flen, p[7] / flen);
+    dst[0] = make_float4(sum[0] / flen, sum[1] / flen, sum[2] / flen, sum[3] / flen);
+    dst[1] = make_float4(sum[4] / flen, sum[5] / flen, sum[6] / flen, sum[7] / flen);
   }
 }
 
@@ -116,11 +196,6 @@ __device__ __forceinline__ float tree8(const float (*part)[kHeadDim], int d) {
 // order as a plain loop.
 constexpr int kMomThreads = 128;
 constexpr int kMomU = 16;
-__device__ __forceinline__ void unpack8(const uint4& w, float (&x)[8]) {
-  x[0] = lo_bf16(w.x); x[1] = hi_bf16(w.x); x[2] = lo_bf16(w.y); x[3] = hi_bf16(w.y);
-  x[4] = lo_bf16(w.z); x[5] = hi_bf16(w.z); x[6] = lo_bf16(w.w); x[7] = hi_bf16(w.w);
-}
-
 __global__ void __launch_bounds__(kMomThreads)
 moments_kernel(uint16_t* __restrict__ kc, int64_t npad, int NT, int H, int centre,
                float* __restrict__ kc_mean, float* __restrict__ kc_var,
@@ -417,13 +492,39 @@ int check_bthd(const void* p, int64_t sb, int64_t st, int64_t sh, const char* na
 
 }  // namespace
 
-extern "C" int solattn_pool(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
-                            const uint16_t* k, int64_t sk_b, int64_t sk_t, int64_t sk_h,
-                            const uint16_t* v, int64_t sv_b, int64_t sv_t, int64_t sv_h, int64_t B,
-                            int64_t T, int64_t H, int64_t D, int64_t block, uint16_t* kc,
-                            uint16_t* vc, int64_t npad, float* qbar, float* vamax_part,
-                            solattn_stream_t stream) {
-  clear_error();
+namespace solattn {
+
+int launch_pool(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h, const uint16_t* k,
+                int64_t sk_b, int64_t sk_t, int64_t sk_h, const uint16_t* v, int64_t sv_b,
+                int64_t sv_t, int64_t sv_h, int64_t B, int64_t T, int64_t H, int64_t block,
+                uint16_t* kc, uint16_t* vc, int64_t npad, float* qbar, float* vamax_part,
+                int8_t* qi, float* qs, int64_t TP, hipStream_t s) {
+  const int64_t NT = cdiv(T, block);
+  const int64_t HG = cdiv(H, kPoolHeads);
+  SOLATTN_REQUIRE(3 * NT * HG < (1ll << 31) && B <= 65535, SOLATTN_EUNSUPPORTED,
+                  "pool: %lld blocks of %lld x %lld heads", (long long)NT, (long long)block,
+                  (long long)H);
+  SOLATTN_REQUIRE(!qi || (qs && TP >= T && reinterpret_cast<uintptr_t>(qi) % 8 == 0),
+                  SOLATTN_EINVAL, "pool: bad Q quantisation outputs");
+  dim3 grid(static_cast<uint32_t>(3 * NT * HG), static_cast<uint32_t>(B));
+  const dim3 wg(64 * kPoolWaves);
+  const auto kern = block == 64 ? (qi ? pool_kernel<64, true> : pool_kernel<64, false>)
+                                 : (qi ? pool_kernel<128, true> : pool_kernel<128, false>);
+  hipLaunchKernelGGL(kern, grid, wg, 0, s, q, sq_b, sq_t, sq_h, k, sk_b, sk_t, sk_h, v, sv_b, sv_t,
+                     sv_h, T, static_cast<int>(H), static_cast<int>(NT), kc, vc, npad, qbar,
+                     vamax_part, qi, qs, TP);
+  return check_launch("pool");
+}
+
+}  // namespace solattn
+
+namespace solattn {
+
+int pool_checked(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h, const uint16_t* k,
+                 int64_t sk_b, int64_t sk_t, int64_t sk_h, const uint16_t* v, int64_t sv_b,
+                 int64_t sv_t, int64_t sv_h, int64_t B, int64_t T, int64_t H, int64_t D,
+                 int64_t block, uint16_t* kc, uint16_t* vc, int64_t npad, float* qbar,
+                 float* vamax_part, int8_t* qi, float* qs, int64_t TP, hipStream_t s) {
   SOLATTN_REQUIRE(D == kHeadDim, SOLATTN_EUNSUPPORTED, "pool: head_dim %lld != 128", (long long)D);
   SOLATTN_REQUIRE(block == 64 || block == 128, SOLATTN_EUNSUPPORTED, "pool: block %lld not in {64, 128}",
                   (long long)block);
@@ -436,17 +537,22 @@ extern "C" int solattn_pool(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64
   if (int rc = check_bthd(q, sq_b, sq_t, sq_h, "pool q")) return rc;
   if (int rc = check_bthd(k, sk_b, sk_t, sk_h, "pool k")) return rc;
   if (int rc = check_bthd(v, sv_b, sv_t, sv_h, "pool v")) return rc;
-  dim3 grid(static_cast<uint32_t>(NT), static_cast<uint32_t>(H), static_cast<uint32_t>(B));
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (block == 64)
-    hipLaunchKernelGGL(pool_kernel<64>, grid, dim3(192), 0, s, q, sq_b, sq_t, sq_h, k, sk_b, sk_t,
-                       sk_h, v, sv_b, sv_t, sv_h, T, static_cast<int>(H), static_cast<int>(NT), kc,
-                       vc, npad, qbar, vamax_part);
-  else
-    hipLaunchKernelGGL(pool_kernel<128>, grid, dim3(192), 0, s, q, sq_b, sq_t, sq_h, k, sk_b, sk_t,
-                       sk_h, v, sv_b, sv_t, sv_h, T, static_cast<int>(H), static_cast<int>(NT), kc,
-                       vc, npad, qbar, vamax_part);
-  return check_launch("pool");
+  return launch_pool(q, sq_b, sq_t, sq_h, k, sk_b, sk_t, sk_h, v, sv_b, sv_t, sv_h, B, T, H, block,
+                     kc, vc, npad, qbar, vamax_part, qi, qs, TP, s);
+}
+
+}  // namespace solattn
+
+extern "C" int solattn_pool(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
+                            const uint16_t* k, int64_t sk_b, int64_t sk_t, int64_t sk_h,
+                            const uint16_t* v, int64_t sv_b, int64_t sv_t, int64_t sv_h, int64_t B,
+                            int64_t T, int64_t H, int64_t D, int64_t block, uint16_t* kc,
+                            uint16_t* vc, int64_t npad, float* qbar, float* vamax_part,
+                            solattn_stream_t stream) {
+  clear_error();
+  return pool_checked(q, sq_b, sq_t, sq_h, k, sk_b, sk_t, sk_h, v, sv_b, sv_t, sv_h, B, T, H, D,
+                      block, kc, vc, npad, qbar, vamax_part, nullptr, nullptr, 0,
+                      reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int solattn_moments(uint16_t* kc, int64_t npad, int64_t B, int64_t NT, int64_t H,

@@ -3,21 +3,15 @@
 // Built with -ffp-contract=off; divisions are IEEE (HIP's default correctly
 // rounded fp32 divide), so codes and scales match the CPU oracle bit for bit.
 // One row (token, head) of 128 channels is held by 16 lanes x 8 channels; the
-// row's |max| is reduced with 4 xor shuffles inside the 16-lane group.
+// row's |max| is reduced with DPP lane moves inside the 16-lane group.
 #include "common.hpp"
+#include "quant_common.hpp"
 
 namespace solattn {
 
 constexpr int kQD = 128;
 constexpr int kQuantThreads = 256;
 constexpr int kRowsPerWG = kQuantThreads / 16;
-
-__device__ __forceinline__ uint32_t pack_i8x4(int8_t a, int8_t b, int8_t c, int8_t d) {
-  return static_cast<uint32_t>(static_cast<uint8_t>(a)) |
-         (static_cast<uint32_t>(static_cast<uint8_t>(b)) << 8) |
-         (static_cast<uint32_t>(static_cast<uint8_t>(c)) << 16) |
-         (static_cast<uint32_t>(static_cast<uint8_t>(d)) << 24);
-}
 
 // One launch quantises up to three BTHD tensors (blockIdx.z picks the
 // tensor): per token with an optional smoothing mean (Q, K;
@@ -29,12 +23,7 @@ __device__ __forceinline__ uint32_t pack_i8x4(int8_t a, int8_t b, int8_t c, int8
 // or channel scales sit in registers for the whole workgroup and every lane
 // has kQuantR 16-byte row loads in flight before any arithmetic.
 //
-// Codes are trunc(fl(q + copysign(0.5, q))) of the IEEE quotient q = fl(x / s),
-// clamped to [-127, 127], exactly as the CPU oracle rounds. The kernel forms
-// q' = x * rcp(s) instead (v_rcp_f32, within 1 ulp of 1/s), within 2 ulp of q;
-// trunc(fl(. + 0.5)) can only differ between q and q' when fl(q' + 0.5) lies
-// within 4e-5 of an integer (|q| <= 127.5, so an ulp is at most 7.7e-6), and a
-// lane holding such a value recomputes its eight codes by IEEE division.
+// Codes and scales follow quant_common.hpp.
 constexpr int kQuantR = 8;                       // tokens per lane group
 constexpr int kQuantTok = kQuantR * kRowsPerWG;  // tokens per workgroup
 
@@ -52,36 +41,6 @@ struct QuantArgs {
   uint32_t T, H;
   int64_t TP;
 };
-
-// t = fl(q + copysign(0.5, q)) -> trunc(t) clamped to [-127, 127]
-// (v_cvt_i32_f32 truncates).
-__device__ __forceinline__ int code_of(float t) {
-  return static_cast<int>(__builtin_amdgcn_fmed3f(t, -127.f, 127.f));
-}
-
-__device__ __forceinline__ bool near_integer(float t) {
-  return fabsf(t - __builtin_rintf(t)) <= 4e-5f;
-}
-
-// fl(a / 127) for a >= 0 without a division: q0 = a * fl(1/127) corrected by
-// one fma residual step. Equal to the IEEE quotient for every non-negative
-// finite float (checked exhaustively on the CPU, tests/test_oracle.py).
-__device__ __forceinline__ float div127(float a) {
-  const float c = 1.0f / 127.0f;
-  const float q0 = a * c;
-  const float r = __builtin_fmaf(-q0, 127.0f, a);
-  return __builtin_fmaf(r, c, q0);
-}
-
-// Max over the 16 lanes of a lane group through DPP lane moves (no LDS):
-// swap neighbours, swap pairs, mirror within 8 lanes, mirror within 16.
-__device__ __forceinline__ float group16_max(float x) {
-  x = fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1, 0xf, 0xf, false)));
-  x = fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x4E, 0xf, 0xf, false)));
-  x = fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x141, 0xf, 0xf, false)));
-  x = fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x140, 0xf, 0xf, false)));
-  return x;
-}
 
 // PER_CHANNEL: V against vscale[d]; otherwise per token, smoothed by mean
 // when the tensor has one.
@@ -119,37 +78,14 @@ __device__ __forceinline__ void quant_rows_of(const QuantTensor& A, uint32_t T, 
       y[2 * e + 1] = hi_bf16(w[e]) - m[2 * e + 1];
     }
     float ss = 1.f;
+    uint2 o;
     if (!PER_CHANNEL) {
-      float amax = fmaxf(fmaxf(fabsf(y[0]), fabsf(y[1])), fmaxf(fabsf(y[2]), fabsf(y[3])));
-      amax = fmaxf(amax, fmaxf(fmaxf(fabsf(y[4]), fabsf(y[5])), fmaxf(fabsf(y[6]), fabsf(y[7]))));
-      const float sc = div127(group16_max(amax));
-      ss = sc > 1e-8f ? sc : 1e-8f;
-      const float rr = __builtin_amdgcn_rcpf(ss);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) rs[e] = rr;
-    }
-    int code[8];
-    bool near = false;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float q1 = y[e] * rs[e];
-      const float tq = q1 + copysignf(0.5f, q1);
-      near |= near_integer(tq);
-      code[e] = code_of(tq);
-    }
-    if (near) {
-      asm volatile("");  // keeps the divisions on this rare path
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float q = y[e] / (PER_CHANNEL ? sv[e] : ss);
-        code[e] = code_of(q + copysignf(0.5f, q));
-      }
+      ss = quant_token_row(y, o);
+    } else {
+      o = codes8(y, rs, sv);
     }
     if (t < T) {
       const int64_t row = (static_cast<int64_t>(b) * TP + t) * H + h;
-      uint2 o;
-      o.x = pack_i8x4(code[0], code[1], code[2], code[3]);
-      o.y = pack_i8x4(code[4], code[5], code[6], code[7]);
       *reinterpret_cast<uint2*>(A.xi + row * kQD + c8) = o;
       if (!PER_CHANNEL && (threadIdx.x & 15) == 0) A.xs[row] = ss;
     }
@@ -210,10 +146,12 @@ int quant_qkv(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h, const
               int64_t sv_t, int64_t sv_h, int64_t B, int64_t T, int64_t H, int64_t D,
               const float* k_mean, const float* vscale, int8_t* qi, float* qs, int8_t* ki,
               float* ks, int8_t* vi, int64_t TP, hipStream_t stream) {
-  const QuantTensor ts[3] = {{q, sq_b, sq_t, sq_h, nullptr, nullptr, qi, qs},
-                             {k, sk_b, sk_t, sk_h, k_mean, nullptr, ki, ks},
-                             {v, sv_b, sv_t, sv_h, nullptr, vscale, vi, nullptr}};
-  return launch_quant3(ts, vscale ? 3 : 2, B, T, H, D, TP, stream, "quant_qkv");
+  QuantTensor ts[3];
+  int n = 0;
+  if (q) ts[n++] = {q, sq_b, sq_t, sq_h, nullptr, nullptr, qi, qs};
+  ts[n++] = {k, sk_b, sk_t, sk_h, k_mean, nullptr, ki, ks};
+  if (vscale) ts[n++] = {v, sv_b, sv_t, sv_h, nullptr, vscale, vi, nullptr};
+  return launch_quant3(ts, n, B, T, H, D, TP, stream, "quant_qkv");
 }
 
 }  // namespace solattn

@@ -113,7 +113,11 @@ def test_full_size_int8(pkg, dev, video, int8_pv, block, tau):
     r, qi, qs, ki, ks, vi = fp.fused_preprocess_routing(q, k, v, tau=tau, scale=128 ** -0.5,
                                                         block=block)
     out = i8.forward_int8(q, v, r, qi, qs, ki, ks, vi, int8_pv=int8_pv)
+    # the one-call pipeline (Q codes from the pooling pass, K and V codes from
+    # the quantisation pass) feeds the same forward the same bits
+    one = i8.sol_attn_int8(q, k, v, tau=tau, block=block, int8_pv=int8_pv)
     torch.cuda.synchronize()
+    assert torch.equal(one.view(torch.int16), out.view(torch.int16))
     ref = oracle.prepare(qb, kb, vb, block=block, tau=tau, int8=True, int8_pv=int8_pv)
     _route_equal(r, ref)
     T = ref["T"]
@@ -175,7 +179,11 @@ def test_cfg1_image_dit_int8(pkg, dev, image, int8_pv):
     r, qi, qs, ki, ks, vi = fp.fused_preprocess_routing(q, k, v, tau=tau, scale=128 ** -0.5,
                                                         block=block)
     out = i8.forward_int8(q, v, r, qi, qs, ki, ks, vi, int8_pv=int8_pv)
+    # the one-call pipeline (Q codes from the pooling pass, K and V codes from
+    # the quantisation pass) feeds the same forward the same bits
+    one = i8.sol_attn_int8(q, k, v, tau=tau, block=block, int8_pv=int8_pv)
     torch.cuda.synchronize()
+    assert torch.equal(one.view(torch.int16), out.view(torch.int16))
     ref = oracle.prepare(qb, kb, vb, block=block, tau=tau, int8=True, int8_pv=int8_pv)
     _route_equal(r, ref)
     assert np.array_equal(qi.cpu().numpy(), ref["qi"]) and np.array_equal(ki.cpu().numpy(), ref["ki"])

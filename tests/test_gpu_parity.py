@@ -162,9 +162,17 @@ def test_fwd_int8_vs_port(pkg, dev, case, int8_pv):
     B, T, H, block, tau, skv, sq = case
     print(f"[fwd_int8] case={case} int8_pv={int8_pv}", flush=True)
     q, k, v = (randn_bf16((B, T, H, 128), s) for s in (40, 41, 42))
-    out = i8.sol_attn_int8(q.to(dev), k.to(dev), v.to(dev), tau=tau, block=block, int8_pv=int8_pv,
-                           sink_blocks=skv, sink_q=sq)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    out = i8.sol_attn_int8(qd, kd, vd, tau=tau, block=block, int8_pv=int8_pv, sink_blocks=skv,
+                           sink_q=sq)
+    # the one call (Q codes from the pooling pass, heads past H in its last
+    # 4-head wave idle) and the composed primitives give the same bits
+    r, qi, qs, ki, ks, vi = _mods(pkg)[3].fused_preprocess_routing(
+        qd, kd, vd, tau=tau, scale=128 ** -0.5, int8_pv=int8_pv, block=block, sink_blocks=skv,
+        sink_q=sq)
+    two = i8.forward_int8(qd, vd, r, qi, qs, ki, ks, vi, int8_pv=int8_pv)
     torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), two.view(torch.int16))
     ref = oracle.prepare(bits(q), bits(k), bits(v), block=block, tau=tau, int8=True, int8_pv=int8_pv,
                          sink_kv=skv, sink_q=sq)
     rows = _rows(B, H, ref["NT"], limit=16)
