@@ -330,40 +330,44 @@ route_kernel(const float* __restrict__ qbar, const uint16_t* __restrict__ kc, in
              uint32_t* __restrict__ mask) {
   const int i0 = blockIdx.x * kQB, h = blockIdx.y, b = blockIdx.z;
   const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
-  __shared__ __align__(16) float sq[kQB][kHeadDim];
-  __shared__ float smk[kHeadDim], svk[kHeadDim];
   __shared__ float sthr[kQB];
   // exact bits of the kQB query blocks, W words each, in dynamic LDS
   extern __shared__ __align__(16) uint32_t smask_lds[];
   const auto smask = [&](int i, int w) -> uint32_t& { return smask_lds[i * W + w]; };
   __shared__ __align__(16) uint16_t skc[kRouteThreads * kKcStride];
   const int64_t bh = static_cast<int64_t>(b) * H + h;
-  // The prologue's global loads are all issued before any of them is used:
-  // the query centroids (one float4 per thread) and the moments.
-  {
-    static_assert(kQB * kHeadDim == 4 * kRouteThreads, "one float4 of qbar per thread");
-    const int i = t / (kHeadDim / 4), d4 = t % (kHeadDim / 4);
-    float4 qv = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (i0 + i < NT) qv = *reinterpret_cast<const float4*>(qbar + (bh * NT + i0 + i) * kHeadDim + 4 * d4);
-    float mk = 0.f, vk = 0.f;
-    if (t < kHeadDim) {
-      mk = kc_mean[bh * kHeadDim + t];
-      vk = kc_var[bh * kHeadDim + t];
-    }
-    *reinterpret_cast<float4*>(&sq[i][4 * d4]) = qv;
-    if (t < kHeadDim) {
-      smk[t] = mk;
-      svk[t] = vk;
-    }
-  }
+  // Query rows past NT (a ragged last workgroup) read row NT-1; nothing of
+  // theirs is stored.
+  const float* qrow[kQB];
+#pragma unroll
+  for (int i = 0; i < kQB; ++i) qrow[i] = qbar + (bh * NT + min(i0 + i, NT - 1)) * kHeadDim;
   for (int e = t; e < kQB * W; e += kRouteThreads) smask_lds[e] = 0u;
-  __syncthreads();
-  if (t < kQB) {
+  if (wave == 0) {
+    // Lane i < kQB: the threshold of query block i0 + i, one fma chain per
+    // moment in ascending d. Its row comes in 16-float chunks ahead of the
+    // chain; the kc moments are the same for every lane (scalar loads).
+    const int i = min(lane, kQB - 1);
+    const float4* q4 = reinterpret_cast<const float4*>(qbar + (bh * NT + min(i0 + i, NT - 1)) * kHeadDim);
+    const float* mk = kc_mean + bh * kHeadDim;
+    const float* vk = kc_var + bh * kHeadDim;
     float mu = 0.f, var = 0.f;
-    for (int d = 0; d < kHeadDim; ++d) {
-      const float qd = sq[t][d];
-      if (mode == 0) mu = fmaf(qd, smk[d], mu);
-      var = fmaf(qd * qd, svk[d], var);
+    for (int d0 = 0; d0 < kHeadDim; d0 += 16) {
+      float qv[16];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float4 x = q4[d0 / 4 + u];
+        qv[4 * u] = x.x, qv[4 * u + 1] = x.y, qv[4 * u + 2] = x.z, qv[4 * u + 3] = x.w;
+      }
+      if (mode == 0) {
+#pragma unroll
+        for (int dd = 0; dd < 16; ++dd) {
+          mu = fmaf(qv[dd], mk[d0 + dd], mu);
+          var = fmaf(qv[dd] * qv[dd], vk[d0 + dd], var);
+        }
+      } else {
+#pragma unroll
+        for (int dd = 0; dd < 16; ++dd) var = fmaf(qv[dd] * qv[dd], vk[d0 + dd], var);
+      }
     }
     float th;
     if (mode == 0) {
@@ -375,10 +379,11 @@ route_kernel(const float* __restrict__ qbar, const uint16_t* __restrict__ kc, in
       var = var * c2;
       th = tau * sqrtf(var + 1e-6f);
     }
-    sthr[t] = th;
-    if (i0 + t < NT) thr_out[(static_cast<int64_t>(b) * NT + i0 + t) * H + h] = th;
+    if (lane < kQB) {
+      sthr[lane] = th;
+      if (i0 + lane < NT) thr_out[(static_cast<int64_t>(b) * NT + i0 + lane) * H + h] = th;
+    }
   }
-  __syncthreads();
 
   for (int j0 = 0; j0 < NT; j0 += kRouteThreads) {
     // Stage kc rows j0 .. j0+255 (coalesced 16-byte loads, all issued before
@@ -389,12 +394,13 @@ route_kernel(const float* __restrict__ qbar, const uint16_t* __restrict__ kc, in
       for (int u = 0; u < kKcLoads; ++u) {
         const int e = t + kRouteThreads * u;
         const int r = e >> 4, cc = e & 15;
-        const int j = j0 + r;
-        v[u] = make_uint4(0u, 0u, 0u, 0u);
-        if (j < NT)
-          v[u] = *reinterpret_cast<const uint4*>(
-              kc + ((static_cast<int64_t>(b) * npad + j) * H + h) * kHeadDim + cc * 8);
+        v[u] = *reinterpret_cast<const uint4*>(
+            kc + ((static_cast<int64_t>(b) * npad + min(j0 + r, NT - 1)) * H + h) * kHeadDim +
+            cc * 8);
       }
+#pragma unroll
+      for (int u = 0; u < kKcLoads; ++u)
+        if (j0 + ((t + kRouteThreads * u) >> 4) >= NT) v[u] = make_uint4(0u, 0u, 0u, 0u);
       __syncthreads();  // the previous chunk's rows have been read
 #pragma unroll
       for (int u = 0; u < kKcLoads; ++u) {
@@ -405,13 +411,15 @@ route_kernel(const float* __restrict__ qbar, const uint16_t* __restrict__ kc, in
         dst[1] = make_uint2(v[u].z, v[u].w);
       }
     }
-    __syncthreads();
+    __syncthreads();  // (the first one also publishes the thresholds)
     const int j = j0 + t;
     const bool active = j < NT;
     float acc[kQB];
 #pragma unroll
     for (int i = 0; i < kQB; ++i) acc[i] = 0.f;
     const uint16_t* krow = &skc[t * kKcStride];
+    // The query centroids are the same for every lane: scalar loads, so each
+    // fma takes its q operand from an SGPR.
 #pragma unroll 2
     for (int d4 = 0; d4 < kHeadDim / 4; ++d4) {
       const uint2 kw = *reinterpret_cast<const uint2*>(krow + 4 * d4);
@@ -419,7 +427,7 @@ route_kernel(const float* __restrict__ qbar, const uint16_t* __restrict__ kc, in
       const float k2 = lo_bf16(kw.y), k3 = hi_bf16(kw.y);
 #pragma unroll
       for (int i = 0; i < kQB; ++i) {
-        const float4 qv = *reinterpret_cast<const float4*>(&sq[i][4 * d4]);
+        const float4 qv = *reinterpret_cast<const float4*>(qrow[i] + 4 * d4);
         acc[i] = fmaf(qv.x, k0, acc[i]);
         acc[i] = fmaf(qv.y, k1, acc[i]);
         acc[i] = fmaf(qv.z, k2, acc[i]);
