@@ -114,26 +114,40 @@ __device__ int build_tile_list(TileList& tl, const int32_t* __restrict__ counts,
   const int cnt = min(max(counts[row], 0), NT);
   int16_t* blist = blist_lds();
   for (int e = threadIdx.x; e < cnt; e += blockDim.x) blist[e] = lists[row * NT + e];
-  if (threadIdx.x == 0) {
+  // Pooled chunks (64 key blocks each): wave 0 scans one chunk per lane, 64
+  // chunks a pass, so the mask words are loaded together; a ballot prefix
+  // keeps the chunks in ascending order.
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
     const uint32_t* mrow = mask + row * W;
     int np = 0;
-    for (int c = 0; c * 64 < NT; ++c) {
-      uint64_t ex = mrow[2 * c];
-      if (2 * c + 1 < W) ex |= static_cast<uint64_t>(mrow[2 * c + 1]) << 32;
-      const int nvalid = min(64, NT - 64 * c);
-      const uint64_t valid = nvalid >= 64 ? ~0ull : ((1ull << nvalid) - 1ull);
-      const uint64_t ap = ~ex & valid;
-      if (ap) {
-        tl.pmask[np] = ap;
-        tl.pchunk[np] = static_cast<int16_t>(c);
-        ++np;
+    for (int c0 = 0; c0 * 64 < NT; c0 += 64) {
+      const int c = c0 + lane;
+      uint64_t ap = 0;
+      if (c * 64 < NT) {
+        uint64_t ex = mrow[2 * c];
+        if (2 * c + 1 < W) ex |= static_cast<uint64_t>(mrow[2 * c + 1]) << 32;
+        const int nvalid = min(64, NT - 64 * c);
+        const uint64_t valid = nvalid >= 64 ? ~0ull : ((1ull << nvalid) - 1ull);
+        ap = ~ex & valid;
       }
+      const uint64_t has = __ballot(ap != 0ull);
+      if (ap) {
+        const int pos = np + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(has >> 32),
+                                                       __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(has), 0));
+        tl.pmask[pos] = ap;
+        tl.pchunk[pos] = static_cast<int16_t>(c);
+      }
+      np += __popcll(has);
     }
-    tl.npool = np;
+    if (lane == 0) tl.npool = np;
+  }
+  __syncthreads();  // blist and the pooled chunks are in LDS
+  if (threadIdx.x == 0) {
     constexpr int S = BLK / kKeys;
     int ne = cnt * S;
     const int tail = T - (NT - 1) * BLK;
-    if (S == 2 && cnt > 0 && lists[row * NT + cnt - 1] == NT - 1 && tail <= kKeys) ne -= 1;
+    if (S == 2 && cnt > 0 && blist[cnt - 1] == NT - 1 && tail <= kKeys) ne -= 1;
     tl.nexact = ne;
   }
   __syncthreads();
