@@ -33,22 +33,22 @@ namespace bf16fwd {
 // Pipelined step over full exact tile n (scores in sc): S(n+1) from the K tile
 // kn goes to sn, interleaved with the softmax of tile n; `mid` runs before
 // P(n) . V(n).
+// kl, vl: this lane's operand addresses (k_lane, v_lane) in K(n+1) and V(n).
 template <typename Mid>
 __device__ __forceinline__ void fast_step(SoftmaxState& st, f32x16 (&sc)[2], f32x16 (&sn)[2],
-                                          const uint16_t* kn, const uint16_t* vt,
-                                          const bf16x8 (&q)[8], float c, int lane, Mid&& mid) {
-  const int col = lane & 31, half = lane >> 5;
+                                          uint32_t kl, uint32_t vl, const bf16x8 (&q)[8],
+                                          float c, int lane, Mid&& mid) {
   const f32x16 zero = {};
   bf16x8 pb[4];
   bf16x8 ka[8][2];
   float mx = -INFINITY, alpha = 1.f, neg = 0.f, psum = 0.f;
-  ka[0][0] = k_op(kn, 0, 0, col, half);
-  ka[0][1] = k_op(kn, 1, 0, col, half);
+  ka[0][0] = k_op_x(kl, 0, 0);
+  ka[0][1] = k_op_x(kl, 1, 0);
 #pragma unroll
   for (int cc = 0; cc < 8; ++cc) {
     if (cc + 1 < 8) {
-      ka[cc + 1][0] = k_op(kn, 0, cc + 1, col, half);
-      ka[cc + 1][1] = k_op(kn, 1, cc + 1, col, half);
+      ka[cc + 1][0] = k_op_x(kl, 0, cc + 1);
+      ka[cc + 1][1] = k_op_x(kl, 1, cc + 1);
     }
     sn[0] = mfma_bf16(ka[cc][0], q[cc], cc == 0 ? zero : sn[0]);
     sn[1] = mfma_bf16(ka[cc][1], q[cc], cc == 0 ? zero : sn[1]);
@@ -74,7 +74,7 @@ __device__ __forceinline__ void fast_step(SoftmaxState& st, f32x16 (&sc)[2], f32
   st.l = fmaf(st.l, alpha, psum);
   rescale(st, alpha);
   mid();
-  pv_tile(vt, pb, lane, st.acc);
+  pv_tile(vl, pb, lane, st.acc);
 }
 
 // Three-stage step: S(n+1) = K(n+1) Q^T, O += P(n-1) V(n-1) and the softmax of
@@ -160,8 +160,8 @@ fwd_bf16_sbuf_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t,
                 const uint32_t* __restrict__ mask, int T, int H, int NT, int W, float c,
                 uint16_t* __restrict__ o, int64_t so_b, int64_t so_t, int64_t so_h) {
   constexpr int NTHREADS = BLK * 2;
-  __shared__ __align__(16) uint16_t kbuf[kTileElems];
-  __shared__ __align__(16) uint16_t vbuf[kTileElems];
+  __shared__ __align__(256) uint16_t kbuf[kTileElems];
+  __shared__ __align__(256) uint16_t vbuf[kTileElems];
   __shared__ TileList tl;
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -184,6 +184,7 @@ fwd_bf16_sbuf_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t,
   CopyOffsets<NTHREADS> off;
   off.init(sk_t, sv_t);
   const uint32_t kb = lds_addr(kbuf), vb = lds_addr(vbuf);  // LDS byte addresses
+  const uint32_t kl = k_lane(kb, col, half), vl = v_lane(vb, lane);  // this lane's operands
   const auto first_of = [&](int n) { return exact_first<BLK>(tl, n - nplain); };
   const auto issue_k_at = [&](int first) {
     issue_full<NTHREADS>(kb, src.k + static_cast<int64_t>(first) * src.sk, src.sk, off.k);
@@ -226,8 +227,8 @@ fwd_bf16_sbuf_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t,
     wait_tile_copies();
     __syncthreads();
     f32x16 s[2];
-    qk_tile(kbuf, qreg, col, half, s);
-    finish_tile<BLK>(st, s, vbuf, desc<BLK>(tl, n, nrag, T, NT), c, lane, NT, T);
+    qk_tile(kl, qreg, s);
+    finish_tile<BLK>(st, s, vl, desc<BLK>(tl, n, nrag, T, NT), c, lane, NT, T);
     __syncthreads();
     if (n + 1 < ntiles) issue_tile(n + 1);
   }
@@ -241,7 +242,7 @@ fwd_bf16_sbuf_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t,
     int n = F;
     wait_tile_copies();
     __syncthreads();
-    qk_tile(kbuf, qreg, col, half, sa);
+    qk_tile(kl, qreg, sa);
     __syncthreads();  // kbuf is free
     if (F + 1 < ntiles) issue_k(F + 1);
     wait_tile_copies();
@@ -252,7 +253,7 @@ fwd_bf16_sbuf_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t,
     // (kf, vf), so no copy waits on an LDS read.
     int kf = first_of(min(n + 2, ntiles - 1)), vf = first_of(n + 1);
     const auto step = [&](f32x16 (&sc)[2], f32x16 (&sn)[2]) {
-      fast_step(st, sc, sn, kbuf, vbuf, qreg, c, lane, [&] {
+      fast_step(st, sc, sn, kl, vl, qreg, c, lane, [&] {
         wait_tile_copies();  // V(n)
         __syncthreads();     // every wave is done with K(n+1)
         issue_k_at(kf);      // K(min(n + 2, ntiles - 1))
@@ -277,11 +278,11 @@ fwd_bf16_sbuf_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t,
       step(sa, sb);
       wait_tile_copies();
       __syncthreads();
-      finish_tile<BLK>(st, sb, vbuf, full, c, lane, NT, T);
+      finish_tile<BLK>(st, sb, vl, full, c, lane, NT, T);
     } else {
       wait_tile_copies();
       __syncthreads();
-      finish_tile<BLK>(st, sa, vbuf, full, c, lane, NT, T);
+      finish_tile<BLK>(st, sa, vl, full, c, lane, NT, T);
     }
   }
   wait_tile_copies();
@@ -319,8 +320,12 @@ fwd_bf16_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
   const int ntiles = build_tile_list<BLK>(tl, counts, lists, mask, row, NT, W, T);
   if (ntiles == 0) return;  // cannot happen for routed lists: the diagonal is exact
   const int nrag = ragged_tiles(tl, counts, row, NT, T);
-  const int nplain = tl.npool + nrag;
-  const int nfast = ntiles - nplain;  // full exact tiles: list tiles 0 .. nfast-1
+  // Full exact tiles (list tiles 0 .. nfast-1) run through the pipeline when
+  // there are at least two; a lone one runs as the first plain tile.
+  const int nfast = ntiles - tl.npool - nrag;
+  const int nlone = nfast == 1 ? 1 : 0;
+  const int npipe = nfast - nlone;
+  const int nplain = nlone + nrag + tl.npool;
 
   const KVSource src{k + b * sk_b + h * sk_h, sk_t, v + b * sv_b + h * sv_h, sv_t,
                      kc + (static_cast<int64_t>(b) * npad * H + h) * kD,
@@ -336,9 +341,12 @@ fwd_bf16_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
   };
   const auto issue_k = [&](int e, int buf) { issue_k_at(exact_first<BLK>(tl, e), buf); };
   const auto issue_v = [&](int e, int buf) { issue_v_at(exact_first<BLK>(tl, e), buf); };
-  // Plain tile p: the ragged exact tile (p < nrag), then the pooled tiles.
+  // Plain tile p: the lone full exact tile (p < nlone), the ragged exact tile
+  // (p < nlone + nrag), then the pooled tiles.
   const auto plain_desc = [&](int p) {
-    return p < nrag ? exact_desc<BLK>(tl, tl.nexact - 1, T, NT) : pooled_desc(tl, p - nrag, NT);
+    if (p < nlone) return exact_desc<BLK>(tl, 0, T, NT);
+    if (p < nlone + nrag) return exact_desc<BLK>(tl, tl.nexact - 1, T, NT);
+    return pooled_desc(tl, p - nlone - nrag, NT);
   };
   const auto issue_plain_k = [&](int p, int buf) {
     issue_generic<NTHREADS>(kb + buf * kTileBytes, 0, plain_desc(p), src);
@@ -346,10 +354,10 @@ fwd_bf16_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
   const auto issue_plain_v = [&](int p, int buf) {
     issue_generic<NTHREADS>(vb + buf * kTileBytes, 1, plain_desc(p), src);
   };
-  if (nfast > 0) {
+  if (npipe > 0) {
     issue_k(0, 0);
     issue_v(0, 0);
-    if (nfast > 1) issue_k(1, 1);
+    issue_k(1, 1);
   } else {
     issue_plain_k(0, 0);
     issue_plain_v(0, 0);
@@ -370,30 +378,23 @@ fwd_bf16_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
 
   SoftmaxState st;
   st.init();
-  const TileDesc full{0, 0, kKeys, ~0ull};
   int pbuf = 0;  // buffer of plain tile 0
+  // This lane's operand addresses in K / V buffer 0 (buffer 1 is kTileBytes on).
+  const uint32_t kl0 = k_lane(kb, col, half);
+  const uint32_t vl0 = v_lane(vb, lane);
 
-  // ---- full exact tiles. On entry to step n (0 < n < nfast): S(n) and
+  // ---- full exact tiles. On entry to step n (0 < n < npipe): S(n) and
   // P(n-1) in registers, K(n+1) and V(n-1) in LDS; the step copies K(n+2)
   // over K(n) and V(n) over V(n-2). K(n+2) past the last tile is clamped to
   // it: a redundant copy into a buffer nothing reads afterwards.
-  if (nfast > 0) {
+  if (npipe > 0) {
     f32x16 sa[2], sb[2];
     wait_tile_copies();
     __syncthreads();
-    qk_tile(kbuf[0], qreg, col, half, sa);
+    qk_tile(kl0, qreg, sa);
     __syncthreads();  // every wave is done with K(0)
-    if (nfast == 1) {
-      finish_tile<BLK>(st, sa, vbuf[0], full, c, lane, NT, T);
-      __syncthreads();
-      if (nplain > 0) {
-        issue_plain_k(0, 0);
-        issue_plain_v(0, 0);
-      }
-    } else {
-      const int E = nfast;
-      const uint32_t kl0 = k_lane(kb, col, half);
-      const uint32_t vl0 = v_lane(vb, lane);
+    {
+      const int E = npipe;
       bf16x8 pa[4], pb[4];
       issue_k(min(2, E - 1), 0);
       // First token rows of the tiles the next step copies, read from the LDS
@@ -433,7 +434,7 @@ fwd_bf16_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
           wait_tile_copies();
         __syncthreads();  // every wave is done with V(n-1)
         if (nplain > 0) issue_plain_v(0, pbuf);
-        pv_tile(vbuf[n & 1], pn, lane, st.acc);
+        pv_tile(vl0 + (n & 1) * kTileBytes, pn, lane, st.acc);
       };
       // Pairs of steps, so the S and P buffers swap roles without copies.
       while (n + 2 < E) {
@@ -462,8 +463,8 @@ fwd_bf16_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
     }
     __syncthreads();
     f32x16 s[2];
-    qk_tile(kbuf[cur], qreg, col, half, s);
-    finish_tile<BLK>(st, s, vbuf[cur], plain_desc(p), c, lane, NT, T);
+    qk_tile(kl0 + cur * kTileBytes, qreg, s);
+    finish_tile<BLK>(st, s, vl0 + cur * kTileBytes, plain_desc(p), c, lane, NT, T);
     __syncthreads();
   }
   wait_tile_copies();

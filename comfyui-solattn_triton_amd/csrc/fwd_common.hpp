@@ -383,17 +383,40 @@ __device__ __forceinline__ void qk_tile(const uint16_t* kt, const bf16x8 (&q)[8]
 
 // O^T += V^T . P^T over the tile's 16 (key step, channel tile) operands, each
 // read three operands ahead of its MFMA.
-__device__ __forceinline__ void pv_tile(const uint16_t* vt, const bf16x8 (&pb)[4], int lane,
-                                        f32x16 (&o)[4]) {
+// The same from the lane address kl = k_lane(tile, col, half) of a
+// 256-byte-aligned K tile: no per-chunk addresses to keep live.
+__device__ __forceinline__ void qk_tile(uint32_t kl, const bf16x8 (&q)[8], f32x16 (&s)[2]) {
+  const f32x16 zero = {};
+#pragma unroll
+  for (int cc = 0; cc < 8; ++cc) {
+    const bf16x8 a0 = k_op_x(kl, 0, cc);
+    const bf16x8 a1 = k_op_x(kl, 1, cc);
+    s[0] = mfma_bf16(a0, q[cc], cc == 0 ? zero : s[0]);
+    s[1] = mfma_bf16(a1, q[cc], cc == 0 ? zero : s[1]);
+  }
+}
+
+// O^T += V^T . P^T over one tile; vop(ks, dt) gives the V^T operand.
+template <typename VOp>
+__device__ __forceinline__ void pv_tile_with(VOp&& vop, const bf16x8 (&pb)[4], f32x16 (&o)[4]) {
   constexpr int L = 3;
   bf16x8 va[16];
 #pragma unroll
-  for (int i = 0; i < L; ++i) va[i] = v_op(vt, i >> 2, i & 3, lane);
+  for (int i = 0; i < L; ++i) va[i] = vop(i >> 2, i & 3);
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    if (i + L < 16) va[i + L] = v_op(vt, (i + L) >> 2, (i + L) & 3, lane);
+    if (i + L < 16) va[i + L] = vop((i + L) >> 2, (i + L) & 3);
     o[i & 3] = mfma_bf16(va[i], pb[i >> 2], o[i & 3]);
   }
+}
+__device__ __forceinline__ void pv_tile(const uint16_t* vt, const bf16x8 (&pb)[4], int lane,
+                                        f32x16 (&o)[4]) {
+  pv_tile_with([&](int ks, int dt) { return v_op(vt, ks, dt, lane); }, pb, o);
+}
+// From the lane address vl = v_lane(tile, lane) of a 256-byte-aligned V tile.
+__device__ __forceinline__ void pv_tile(uint32_t vl, const bf16x8 (&pb)[4], int /*lane*/,
+                                        f32x16 (&o)[4]) {
+  pv_tile_with([&](int ks, int dt) { return v_op_x(vl, ks, dt); }, pb, o);
 }
 
 // ------------------------------------------------------------ online softmax
@@ -461,8 +484,10 @@ __device__ __forceinline__ void rescale(SoftmaxState& st, float alpha) {
 // len_j in the row sum (/root/reference/_tri_fwd.py:302-307); P is rounded to
 // bf16 for the MFMA and, for exact tiles, summed as rounded (as on the
 // pipelined path).
-template <int BLK>
-__device__ __forceinline__ void finish_tile(SoftmaxState& st, f32x16 (&s)[2], const uint16_t* vt,
+// vt: the V tile, as a pointer or as the lane address v_lane(tile, lane) of a
+// 256-byte-aligned tile (see pv_tile).
+template <int BLK, typename VTile>
+__device__ __forceinline__ void finish_tile(SoftmaxState& st, f32x16 (&s)[2], VTile vt,
                                             const TileDesc& td, float c, int lane, int NT, int T) {
   const int half = lane >> 5;
   if (td.amask != ~0ull) {
