@@ -86,10 +86,17 @@ __device__ __forceinline__ void fast_step(SoftmaxState& st, f32x16 (&sc)[2], f32
 // while only the keys 0-31 half of S(n+1) accumulates; keys 32-63 start after
 // S(n) is dead. kl, vl: this lane's operand addresses (k_lane, v_lane) in
 // K(n+1) and V(n-1).
-template <bool QK, bool PV>
+// LAZY (every step after the first, whose running max is finite): the exps of
+// S(n) use the running max as it stands, and the tile's max is taken only when
+// a lane's row sum exceeds 255. No sum above 255 means every p <= 255, i.e.
+// every score is below the running max + log2(255.5) < kMaxSlack, so the
+// tile would not have moved the max: the running max, and so every bit of the
+// output, evolves as with the max taken every step.
+template <bool QK, bool PV, bool LAZY = false>
 __device__ __forceinline__ void step3(SoftmaxState& st, const f32x16 (&sc)[2], f32x16 (&sn)[2],
                                       const bf16x8 (&pp)[4], bf16x8 (&pn)[4], uint32_t kl,
                                       uint32_t vl, const bf16x8 (&q)[8], float c) {
+  static_assert(kMaxSlack >= 8.f, "the lazy test relies on 255 < 2^kMaxSlack");
   const f32x16 zero = {};
   constexpr int LK = 2, LV = 2;
   bf16x8 ka[16], va[16];
@@ -101,7 +108,7 @@ __device__ __forceinline__ void step3(SoftmaxState& st, const f32x16 (&sc)[2], f
 #pragma unroll
     for (int i = 0; i < LV; ++i) va[i] = v_op_x(vl, i >> 2, i & 3);
   }
-  float mx = -INFINITY, alpha = 1.f, neg = 0.f, psum = 0.f;
+  float mx = -INFINITY, alpha = 1.f, neg = LAZY ? -st.m : 0.f, psum = 0.f;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     if constexpr (QK) {
@@ -112,7 +119,9 @@ __device__ __forceinline__ void step3(SoftmaxState& st, const f32x16 (&sc)[2], f
       if (i + LV < 16) va[i + LV] = v_op_x(vl, (i + LV) >> 2, (i + LV) & 3);
       st.acc[i & 3] = mfma_bf16(va[i], pp[i >> 2], st.acc[i & 3]);
     }
-    if (i < 4) {
+    if (LAZY && i < 4) {
+      // nothing: the running max stands
+    } else if (i < 4) {
 #pragma unroll
       for (int r = 0; r < 8; ++r) mx = fmaxf(mx, sc[i >> 1][8 * (i & 1) + r]);
       if (i == 3) {
@@ -126,6 +135,20 @@ __device__ __forceinline__ void step3(SoftmaxState& st, const f32x16 (&sc)[2], f
       const int k = i - 4;
       psum = k & 1 ? exp8<8>(sc[k >> 1], c, neg, pn[k], psum) : exp8<0>(sc[k >> 1], c, neg, pn[k], psum);
       asm volatile("" : "+v"(pn[k]), "+v"(psum));
+      if (LAZY && k == 3 && __any(!(psum <= 255.f))) {  // (also catches inf / NaN)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaxf(sc[0][r], sc[1][r]));
+        const float m_new = new_max(st.m, xhalf_max(mx) * c, alpha);
+        if (__any(m_new != st.m)) {  // lanes whose max stays recompute the same P
+          st.m = m_new;
+          neg = -m_new;
+          psum = 0.f;
+          psum = exp8<0>(sc[0], c, neg, pn[0], psum);
+          psum = exp8<8>(sc[0], c, neg, pn[1], psum);
+          psum = exp8<0>(sc[1], c, neg, pn[2], psum);
+          psum = exp8<8>(sc[1], c, neg, pn[3], psum);
+        }
+      }
     }
     // Raised wave priority for the rest of the step: the issue arbiter then
     // prefers a wave inside its MFMA stream over one at its copies / barrier
@@ -409,8 +432,8 @@ fwd_bf16_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
                              bf16x8 (&pn)[4]) {
         issue_k_at(kf, n & 1);  // K(min(n + 2, E - 1))
         issue_v_at(vf, n & 1);  // V(n)
-        step3<true, true>(st, sc, sn, pp, pn, kl0 + ((n + 1) & 1) * kTileBytes,
-                          vl0 + ((n - 1) & 1) * kTileBytes, qreg, c);
+        step3<true, true, true>(st, sc, sn, pp, pn, kl0 + ((n + 1) & 1) * kTileBytes,
+                                vl0 + ((n - 1) & 1) * kTileBytes, qreg, c);
         // after the MFMA stream, so the read's latency overlaps the copy wait
         // and the barrier below rather than delaying this step's first MFMAs
         asm volatile("" ::: "memory");
@@ -427,7 +450,7 @@ fwd_bf16_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
         pbuf = (n - 1) & 1;
         issue_v_at(vf, n & 1);  // V(n)
         if (nplain > 0) issue_plain_k(0, pbuf);
-        step3<false, true>(st, sc, dummy, pp, pn, 0u, vl0 + pbuf * kTileBytes, qreg, c);
+        step3<false, true, true>(st, sc, dummy, pp, pn, 0u, vl0 + pbuf * kTileBytes, qreg, c);
         if (nplain > 0)
           wait_vmcnt<kCopiesPerTile / 2>();  // V(n) landed; plain K(0) may be in flight
         else
