@@ -41,7 +41,12 @@ __device__ __forceinline__ void fast_step(SoftmaxState& st, f32x16 (&sc)[2], f32
   const f32x16 zero = {};
   bf16x8 pb[4];
   bf16x8 ka[8][2];
-  float mx = -INFINITY, alpha = 1.f, neg = 0.f, psum = 0.f;
+  // Lazy tile max, as in step3: the exps use the running max as it stands
+  // and the tile max is taken only when a lane's row sum exceeds 255 (which
+  // also catches the first exact tile when no plain tile came before it:
+  // running max -inf, p = inf), so the running max evolves as if taken every
+  // tile.
+  float mx = -INFINITY, alpha = 1.f, neg = -st.m, psum = 0.f;
   ka[0][0] = k_op_x(kl, 0, 0);
   ka[0][1] = k_op_x(kl, 1, 0);
 #pragma unroll
@@ -53,15 +58,7 @@ __device__ __forceinline__ void fast_step(SoftmaxState& st, f32x16 (&sc)[2], f32
     sn[0] = mfma_bf16(ka[cc][0], q[cc], cc == 0 ? zero : sn[0]);
     sn[1] = mfma_bf16(ka[cc][1], q[cc], cc == 0 ? zero : sn[1]);
     // softmax of tile n, spread over the 8 MFMA pairs
-    if (cc == 0) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[0][r]);
-    } else if (cc == 1) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[1][r]);
-      st.m = new_max(st.m, xhalf_max(mx) * c, alpha);
-      neg = -st.m;
-    } else if (cc == 2) {
+    if (cc == 2) {
       psum = exp8<0>(sc[0], c, neg, pb[0], psum);
     } else if (cc == 3) {
       psum = exp8<8>(sc[0], c, neg, pb[1], psum);
@@ -69,6 +66,20 @@ __device__ __forceinline__ void fast_step(SoftmaxState& st, f32x16 (&sc)[2], f32
       psum = exp8<0>(sc[1], c, neg, pb[2], psum);
     } else if (cc == 5) {
       psum = exp8<8>(sc[1], c, neg, pb[3], psum);
+      if (__any(!(psum <= 255.f))) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaxf(sc[0][r], sc[1][r]));
+        const float m_new = new_max(st.m, xhalf_max(mx) * c, alpha);
+        if (__any(m_new != st.m)) {  // lanes whose max stays recompute the same P
+          st.m = m_new;
+          neg = -m_new;
+          psum = 0.f;
+          psum = exp8<0>(sc[0], c, neg, pb[0], psum);
+          psum = exp8<8>(sc[0], c, neg, pb[1], psum);
+          psum = exp8<0>(sc[1], c, neg, pb[2], psum);
+          psum = exp8<8>(sc[1], c, neg, pb[3], psum);
+        }
+      }
     }
   }
   st.l = fmaf(st.l, alpha, psum);
