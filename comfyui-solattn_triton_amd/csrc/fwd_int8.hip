@@ -194,7 +194,12 @@ __device__ __forceinline__ void fast_step(SoftmaxState& st, f32x16 (&sc)[2], f32
   const i32x16 zero = {};
   i32x16 si[2];
   i32x4 ka[4][2];
-  float mx = -INFINITY, alpha = 1.f, bmax = 0.f, neg = 0.f, psum = 0.f;
+  // bf16 P.V: lazy tile max, as in the BF16 forward's steps (the exps use the
+  // running max as it stands; the tile max is taken only when a lane's row
+  // sum exceeds 255, or is inf on a first tile with the running max -inf), so
+  // the running max evolves as if taken every tile. int8 P.V needs the block
+  // max itself: its P codes are relative to it.
+  float mx = -INFINITY, alpha = 1.f, bmax = 0.f, neg = INT8_PV ? 0.f : -st.m, psum = 0.f;
   uint32_t csum = 0u;
   bf16x8 pb[4];
   i32x4 pi[2];
@@ -208,7 +213,7 @@ __device__ __forceinline__ void fast_step(SoftmaxState& st, f32x16 (&sc)[2], f32
     }
     si[0] = mfma_i8(ka[cc][0], qi[cc], cc == 0 ? zero : si[0]);
     si[1] = mfma_i8(ka[cc][1], qi[cc], cc == 0 ? zero : si[1]);
-    if (cc == 0) {
+    if (cc == 0 && INT8_PV) {
 #pragma unroll
       for (int m = 0; m < 2; ++m)
 #pragma unroll
@@ -229,6 +234,20 @@ __device__ __forceinline__ void fast_step(SoftmaxState& st, f32x16 (&sc)[2], f32
       } else {
         psum = exp8<0>(sc[1], qsl, neg, pb[2], psum);
         psum = exp8<8>(sc[1], qsl, neg, pb[3], psum);
+        if (__any(!(psum <= 255.f))) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaxf(sc[0][r], sc[1][r]));
+          const float m_new = new_max(st.m, xhalf_max(mx) * qsl, alpha);
+          if (__any(m_new != st.m)) {  // lanes whose max stays recompute the same P
+            st.m = m_new;
+            neg = -m_new;
+            psum = 0.f;
+            psum = exp8<0>(sc[0], qsl, neg, pb[0], psum);
+            psum = exp8<8>(sc[0], qsl, neg, pb[1], psum);
+            psum = exp8<0>(sc[1], qsl, neg, pb[2], psum);
+            psum = exp8<8>(sc[1], qsl, neg, pb[3], psum);
+          }
+        }
       }
     }
   }
