@@ -334,13 +334,14 @@ __device__ __forceinline__ void issue_i8(uint32_t dst, const int8_t* rows, const
 }
 
 // K and V tiles double buffered. Block 128: 68 KB of LDS, two workgroups per
-// CU, two waves per SIMD. Block 64 with int8 P.V: packed int8 tiles (37 KB),
-// four workgroups per CU, two waves per SIMD. Block 64 with bf16 P.V: 68 KB,
-// two workgroups per CU, one wave per SIMD with 512 registers (its
-// single-buffered form spilled in the step loop and ran 1.5x slower).
+// CU, two waves per SIMD. Block 64: packed int8 K tiles; with int8 P.V packed
+// int8 V too (37 KB, four workgroups per CU), with bf16 P.V bf16 V tiles
+// (52 KB, three workgroups per CU: 3.66 -> 3.40 ms at cfg 2 against two
+// workgroups of 68 KB with one wave per SIMD; a single-buffered form spilled in
+// the step loop and ran 1.5x slower).
 template <int BLK, bool INT8_PV>
 __global__ void __launch_bounds__(BLK * 2)
-__attribute__((amdgpu_waves_per_eu(BLK == 64 && !INT8_PV ? 1 : 2)))
+__attribute__((amdgpu_waves_per_eu(2)))
 fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
                 const int8_t* __restrict__ qi, const float* __restrict__ qs,
                 const int8_t* __restrict__ ki, const float* __restrict__ ks,
@@ -351,14 +352,15 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
                 const uint32_t* __restrict__ mask, int T, int H, int NT, int W, float c,
                 uint16_t* __restrict__ o, int64_t so_b, int64_t so_t, int64_t so_h) {
   constexpr int NTHREADS = BLK * 2;
-  // LDS: exact-tile buffers K(i), V(i), i < 2. COMPACT (block 64, int8 P.V):
-  // the int8 tiles are packed (K + its ks: 8448 B, V: 8192 B), so two of each
-  // take 33 KB and four workgroups fit a CU; a bf16 pooled tile then spans
-  // K(0)-K(1) (or V(0)-V(1)) and the pooled tiles are single buffered.
+  // LDS: exact-tile buffers K(i), V(i), i < 2. COMPACT (block 64): the int8
+  // tiles are packed (K + its ks: 8448 B; int8 V: 8192 B), so with int8 P.V two
+  // of each take 33 KB and four workgroups fit a CU, with bf16 P.V (16 KB V
+  // tiles) 49 KB and three; a bf16 pooled tile then spans K(0)-K(1) (and, with
+  // int8 P.V, V(0)-V(1)) and the pooled tiles are single buffered.
   constexpr int NBUF = 2;
-  constexpr bool COMPACT = BLK == 64 && INT8_PV;
+  constexpr bool COMPACT = BLK == 64;
   constexpr int KSTRIDE = COMPACT ? kKsOffset + 256 : static_cast<int>(kTileBytes);
-  constexpr int VSTRIDE = COMPACT ? kKeys * kD : static_cast<int>(kTileBytes);
+  constexpr int VSTRIDE = COMPACT && INT8_PV ? kKeys * kD : static_cast<int>(kTileBytes);
   constexpr int VBASE = NBUF * KSTRIDE;
   constexpr int PNBUF = COMPACT ? 1 : NBUF;  // buffers for pooled tiles
   static_assert(!COMPACT || (2 * KSTRIDE >= static_cast<int>(kTileBytes) &&
@@ -373,8 +375,8 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int col = lane & 31, half = lane >> 5;
   int bh, qb;
-  // Block 64 with bf16 P.V (one wave per SIMD): the 64-dispatch window
-  // measured 1.5% faster there than the 8192-token (128-dispatch) one.
+  // Block 64 with bf16 P.V (three workgroups per CU): the 64-dispatch window
+  // measured 14% faster there than the 8192-token (128-dispatch) one.
   tile_coords_lpt<(BLK == 64 && !INT8_PV) ? 64 : kLptTokens / BLK>(counts, NT, bh, qb);
   const int b = bh / H, h = bh % H;
   const int64_t row = static_cast<int64_t>(bh) * NT + qb;
