@@ -112,6 +112,8 @@ FWD_CASES = [  # (B, T, H, block, tau, sink_kv, sink_q)
     (1, 3000, 2, 128, 1e30, (0, 0), (0, 0)),    # band only: pooled-heavy, 1-6 exact tiles per block
     (1, 2048, 2, 128, 0.8, (0, 0), (0, 0)),     # block 128, T a multiple of 128: no ragged block
     (1, 2112, 2, 128, 0.8, (0, 1), (0, 0)),     # block 128, last block of exactly 64 keys
+    (1, 1536, 2, 64, -1e30, (0, 0), (0, 0)),    # all exact, no ragged or pooled tile: the first
+                                                # pipelined tile starts from running max -inf
 ]
 
 
