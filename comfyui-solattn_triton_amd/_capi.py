@@ -32,6 +32,7 @@ SIGNATURES = {
     "solattn_route": ([_p, _p, _l, _p, _p, _l, _l, _l, _l, _l, _f, _f, _i, _l, _l, _l, _l,
                        _p, _p, _p, _p, _p], _i),
     "solattn_quant_rows": ([_p, _l, _l, _l, _l, _l, _l, _l, _p, _p, _p, _l, _p], _i),
+    "solattn_quant_rows_blocked": ([_p, _l, _l, _l, _l, _l, _l, _l, _p, _p, _p, _l, _p], _i),
     "solattn_quant_v": ([_p, _l, _l, _l, _l, _l, _l, _l, _p, _p, _l, _p], _i),
     "solattn_fwd_bf16": ([_p, _l, _l, _l] * 3 + [_p, _p, _l, _p, _p, _p] + [_l] * 5 +
                          [_f, _p, _l, _l, _l, _p], _i),
@@ -42,6 +43,8 @@ SIGNATURES = {
                                                            _p, _l, _l, _l, _p], _i),
     "solattn_sol_attn_int8": ([_p, _l, _l, _l] * 3 + [_l] * 5 + [_f, _f, _l, _l, _l, _l, _i, _p,
                                                                 _l, _p, _l, _l, _l, _p], _i),
+    "solattn_sol_attn_int8_qblock": ([_p, _l, _l, _l] * 3 + [_l] * 5 + [_f, _f, _l, _l, _l, _l, _i,
+                                                                       _p, _l, _p, _l, _l, _l, _p], _i),
     "solattn_sol_attn_noalloc": ([_p, _l, _l, _l] * 3 + [_l] * 5 + [_f, _f, _l, _l, _l, _l,
                                                                    _p, _l, _l, _l, _p], _i),
 }
@@ -49,6 +52,7 @@ SIGNATURES = {
 # Size of the per-device scratch array behind solattn_sol_attn_noalloc
 # (SOLATTN_NOALLOC_SCRATCH_BYTES).
 NOALLOC_SCRATCH_BYTES = 64 << 20
+QUANT_BLOCK = 128  # tokens per scale of the per-block INT8 variant (SOLATTN_QUANT_BLOCK)
 
 
 def _load() -> ctypes.CDLL:

@@ -9,22 +9,25 @@ from __future__ import annotations
 
 import torch
 
-from ._capi import call, ptr, stream
+from ._capi import QUANT_BLOCK, call, ptr, stream
 from ._preprocess import BLOCK_SIZE, HEAD_DIM, Routing, as_kernel_input, pad_heads, route
 
 __all__ = ["fused_preprocess", "fused_preprocess_routing"]
 
 
 def fused_preprocess_routing(q, k, v, *, tau, scale, int8_pv=True, block=BLOCK_SIZE,
-                             sink_blocks=(0, 0), sink_q=(0, 0)):
+                             sink_blocks=(0, 0), sink_q=(0, 0), quant_block=None):
     """(Routing, qi, qs, ki, ks, vi) -- the INT8 path's inputs to the forward.
     Head dims below 128 run zero-padded; codes come back for the first D
-    channels (the padded ones are 0)."""
+    channels (the padded ones are 0). ``quant_block=128``: Q and K scales per
+    128-token block (written for every token), as ``sol_attn_int8``."""
+    if quant_block not in (None, QUANT_BLOCK):
+        raise ValueError(f"quant_block must be None or {QUANT_BLOCK}, got {quant_block}")
     D0 = q.shape[-1]
     if D0 != HEAD_DIM:
         r, qi, qs, ki, ks, vi = fused_preprocess_routing(
             pad_heads(q), pad_heads(k), pad_heads(v), tau=tau, scale=scale, int8_pv=int8_pv,
-            block=block, sink_blocks=sink_blocks, sink_q=sink_q)
+            block=block, sink_blocks=sink_blocks, sink_q=sink_q, quant_block=quant_block)
         cut = lambda t: None if t is None else t[..., :D0]  # noqa: E731
         r = r._replace(kc=cut(r.kc), vc=cut(r.vc), qbar=cut(r.qbar), kc_mean=cut(r.kc_mean),
                        kc_var=cut(r.kc_var), vamax_part=cut(r.vamax_part), vscale=cut(r.vscale))
@@ -41,10 +44,11 @@ def fused_preprocess_routing(q, k, v, *, tau, scale, int8_pv=True, block=BLOCK_S
     vi = torch.empty_like(qi) if int8_pv else None
     with torch.cuda.device(dev):
         s = stream(dev)
-        call("solattn_quant_rows", ptr(q), q.stride(0), q.stride(1), q.stride(2), B, T, H, D,
-             None, ptr(qi), ptr(qs), T, s)
-        call("solattn_quant_rows", ptr(k), k.stride(0), k.stride(1), k.stride(2), B, T, H, D,
-             ptr(r.kc_mean), ptr(ki), ptr(ks), T, s)
+        rows = "solattn_quant_rows" if quant_block is None else "solattn_quant_rows_blocked"
+        call(rows, ptr(q), q.stride(0), q.stride(1), q.stride(2), B, T, H, D, None, ptr(qi),
+             ptr(qs), T, s)
+        call(rows, ptr(k), k.stride(0), k.stride(1), k.stride(2), B, T, H, D, ptr(r.kc_mean),
+             ptr(ki), ptr(ks), T, s)
         if int8_pv:
             call("solattn_quant_v", ptr(v), v.stride(0), v.stride(1), v.stride(2), B, T, H, D,
                  ptr(r.vscale), ptr(vi), T, s)

@@ -11,7 +11,7 @@ from __future__ import annotations
 
 import torch
 
-from ._capi import call, ptr, stream
+from ._capi import QUANT_BLOCK, call, ptr, stream
 from ._preprocess import BLOCK_SIZE, Routing, as_kernel_input, check_inputs
 from ._tri_fwd import _workspace
 
@@ -21,16 +21,22 @@ __all__ = ["sol_attn_int8", "forward_int8"]
 
 
 def sol_attn_int8(q, k, v, *, scale=None, tau=1.0, sink_blocks=(0, 0), sink_q=(0, 0),
-                  use_tma=False, int8_pv=True, block=BLOCK):
-    """Sol-Attn with an INT8 exact branch. Same contract as ``sol_attn``."""
+                  use_tma=False, int8_pv=True, block=BLOCK, quant_block=None):
+    """Sol-Attn with an INT8 exact branch. Same contract as ``sol_attn``.
+    ``quant_block=128`` quantises Q and smoothed K with one scale per 128-token
+    block instead of per token (an option of this build, BASELINE config 3's
+    wording; the default is the reference's per-token rule)."""
     check_inputs(q, k, v, block)
+    if quant_block not in (None, QUANT_BLOCK):
+        raise ValueError(f"quant_block must be None or {QUANT_BLOCK}, got {quant_block}")
     scale = q.shape[-1] ** -0.5 if scale is None else float(scale)
     q, k, v = as_kernel_input(q), as_kernel_input(k), as_kernel_input(v)
     B, T, H, D = q.shape
     out = torch.empty((B, T, H, D), device=q.device, dtype=torch.bfloat16)
     ws = _workspace(q, block, True)
     with torch.cuda.device(q.device):
-        call("solattn_sol_attn_int8", ptr(q), q.stride(0), q.stride(1), q.stride(2), ptr(k),
+        call("solattn_sol_attn_int8" if quant_block is None else "solattn_sol_attn_int8_qblock",
+             ptr(q), q.stride(0), q.stride(1), q.stride(2), ptr(k),
              k.stride(0), k.stride(1), k.stride(2), ptr(v), v.stride(0), v.stride(1), v.stride(2),
              B, T, H, D, block, float(scale), float(tau), int(sink_blocks[0]), int(sink_blocks[1]),
              int(sink_q[0]), int(sink_q[1]), 1 if int8_pv else 0, ptr(ws), ws.numel(), ptr(out),

@@ -212,17 +212,19 @@ int run_bf16_pipeline(const Layout& L, void* ws, const Call& call, solattn_strea
 
 // pool -> moments(centre) -> route(mode 1) -> quant(q, k smoothed, v) -> fwd_int8.
 int run_int8_pipeline(const Layout& L, void* ws, const Call& call, int int8_pv,
-                      solattn_stream_t stream) {
+                      solattn_stream_t stream, int qk_block = 0) {
   hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
   return with_kernel_head_dim(L, ws, call, hs, [&](const Call& c) {
     float* vamax = int8_pv ? at<float>(ws, L.vamax) : nullptr;
     float* vscale = int8_pv ? at<float>(ws, L.vscale) : nullptr;
-    // the pooling pass also quantises Q (the only tensor whose codes need no
-    // statistic over the whole head), so Q is read once
+    // Per token, the pooling pass also quantises Q (the only tensor whose codes
+    // need no statistic over the whole head), so Q is read once; per block the
+    // quantisation pass takes Q with K.
     int rc = pool_checked(c.q, c.sq_b, c.sq_t, c.sq_h, c.k, c.sk_b, c.sk_t, c.sk_h, c.v, c.sv_b,
                           c.sv_t, c.sv_h, c.B, c.T, c.H, c.D, c.block, at<uint16_t>(ws, L.kc),
                           at<uint16_t>(ws, L.vc), L.npad, at<float>(ws, L.qbar), vamax,
-                          at<int8_t>(ws, L.qi), at<float>(ws, L.qs), L.TP, hs);
+                          qk_block ? nullptr : at<int8_t>(ws, L.qi),
+                          qk_block ? nullptr : at<float>(ws, L.qs), L.TP, hs);
     if (rc) return rc;
     rc = solattn_moments(at<uint16_t>(ws, L.kc), L.npad, c.B, L.NT, c.H, c.D, 1,
                          at<float>(ws, L.kc_mean), at<float>(ws, L.kc_var), vamax, vscale, stream);
@@ -233,10 +235,11 @@ int run_int8_pipeline(const Layout& L, void* ws, const Call& call, int int8_pv,
                        at<int32_t>(ws, L.counts), at<int16_t>(ws, L.lists),
                        at<uint32_t>(ws, L.mask), stream);
     if (rc) return rc;
-    rc = quant_qkv(nullptr, c.sq_b, c.sq_t, c.sq_h, c.k, c.sk_b, c.sk_t, c.sk_h, c.v, c.sv_b, c.sv_t,
-                   c.sv_h, c.B, c.T, c.H, c.D, at<float>(ws, L.kc_mean), vscale,
-                   at<int8_t>(ws, L.qi), at<float>(ws, L.qs), at<int8_t>(ws, L.ki),
-                   at<float>(ws, L.ks), int8_pv ? at<int8_t>(ws, L.vi) : nullptr, L.TP, hs);
+    rc = quant_qkv(qk_block ? c.q : nullptr, c.sq_b, c.sq_t, c.sq_h, c.k, c.sk_b, c.sk_t, c.sk_h,
+                   c.v, c.sv_b, c.sv_t, c.sv_h, c.B, c.T, c.H, c.D, at<float>(ws, L.kc_mean),
+                   vscale, at<int8_t>(ws, L.qi), at<float>(ws, L.qs), at<int8_t>(ws, L.ki),
+                   at<float>(ws, L.ks), int8_pv ? at<int8_t>(ws, L.vi) : nullptr, L.TP, hs,
+                   qk_block);
     if (rc) return rc;
     return solattn_fwd_int8(c.q, c.sq_b, c.sq_t, c.sq_h, at<int8_t>(ws, L.qi), at<float>(ws, L.qs),
                             at<int8_t>(ws, L.ki), at<float>(ws, L.ks),
@@ -342,15 +345,17 @@ extern "C" int solattn_sol_attn_noalloc(const uint16_t* q, int64_t sq_b, int64_t
   return run_bf16_pipeline(L, ws, c, stream);
 }
 
-extern "C" int solattn_sol_attn_int8(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
-                                     const uint16_t* k, int64_t sk_b, int64_t sk_t, int64_t sk_h,
-                                     const uint16_t* v, int64_t sv_b, int64_t sv_t, int64_t sv_h,
-                                     int64_t B, int64_t T, int64_t H, int64_t D, int64_t block,
-                                     float scale, float tau, int64_t sink_kv_lo,
-                                     int64_t sink_kv_hi, int64_t sink_q_lo, int64_t sink_q_hi,
-                                     int int8_pv, void* workspace, int64_t workspace_bytes,
-                                     uint16_t* o, int64_t so_b, int64_t so_t, int64_t so_h,
-                                     solattn_stream_t stream) {
+#define SOLATTN_INT8_CALL_PARAMS                                                               \
+  const uint16_t *q, int64_t sq_b, int64_t sq_t, int64_t sq_h, const uint16_t *k, int64_t sk_b,   \
+      int64_t sk_t, int64_t sk_h, const uint16_t *v, int64_t sv_b, int64_t sv_t, int64_t sv_h,    \
+      int64_t B, int64_t T, int64_t H, int64_t D, int64_t block, float scale, float tau,          \
+      int64_t sink_kv_lo, int64_t sink_kv_hi, int64_t sink_q_lo, int64_t sink_q_hi, int int8_pv,  \
+      void *workspace, int64_t workspace_bytes, uint16_t *o, int64_t so_b, int64_t so_t,          \
+      int64_t so_h, solattn_stream_t stream
+
+namespace {
+
+int sol_attn_int8_call(SOLATTN_INT8_CALL_PARAMS, int qk_block) {
   clear_error();
   if (int rc = check_pipeline(B, T, H, D, block, "sol_attn_int8")) return rc;
   const Layout L(B, T, H, D, block, true);
@@ -361,5 +366,19 @@ extern "C" int solattn_sol_attn_int8(const uint16_t* q, int64_t sq_b, int64_t sq
                   "sol_attn_int8: workspace must be 256-byte aligned");
   const Call c{q, sq_b, sq_t, sq_h, k, sk_b, sk_t, sk_h, v, sv_b, sv_t, sv_h, o, so_b, so_t, so_h,
                B, T, H, D, block, scale, tau, sink_kv_lo, sink_kv_hi, sink_q_lo, sink_q_hi};
-  return run_int8_pipeline(L, workspace, c, int8_pv, stream);
+  return run_int8_pipeline(L, workspace, c, int8_pv, stream, qk_block);
+}
+
+}  // namespace
+
+extern "C" int solattn_sol_attn_int8(SOLATTN_INT8_CALL_PARAMS) {
+  return sol_attn_int8_call(q, sq_b, sq_t, sq_h, k, sk_b, sk_t, sk_h, v, sv_b, sv_t, sv_h, B, T, H,
+                            D, block, scale, tau, sink_kv_lo, sink_kv_hi, sink_q_lo, sink_q_hi,
+                            int8_pv, workspace, workspace_bytes, o, so_b, so_t, so_h, stream, 0);
+}
+
+extern "C" int solattn_sol_attn_int8_qblock(SOLATTN_INT8_CALL_PARAMS) {
+  return sol_attn_int8_call(q, sq_b, sq_t, sq_h, k, sk_b, sk_t, sk_h, v, sv_b, sv_t, sv_h, B, T, H,
+                            D, block, scale, tau, sink_kv_lo, sink_kv_hi, sink_q_lo, sink_q_hi,
+                            int8_pv, workspace, workspace_bytes, o, so_b, so_t, so_h, stream, 1);
 }

@@ -76,11 +76,12 @@ int pad_heads(const uint16_t* src, int64_t s_b, int64_t s_t, int64_t s_h, uint16
 
 // Per-token INT8 of q (skipped when q is null) and of k smoothed by k_mean,
 // and (vscale != null) per-channel INT8 of v, in one launch (quant.hip); same
-// codes and scales as solattn_quant_rows / solattn_quant_v.
+// codes and scales as solattn_quant_rows / solattn_quant_v (qk_block: q and k
+// as solattn_quant_rows_blocked).
 int quant_qkv(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h, const uint16_t* k,
               int64_t sk_b, int64_t sk_t, int64_t sk_h, const uint16_t* v, int64_t sv_b,
               int64_t sv_t, int64_t sv_h, int64_t B, int64_t T, int64_t H, int64_t D,
               const float* k_mean, const float* vscale, int8_t* qi, float* qs, int8_t* ki,
-              float* ks, int8_t* vi, int64_t TP, hipStream_t stream);
+              float* ks, int8_t* vi, int64_t TP, hipStream_t stream, int qk_block = 0);
 
 }  // namespace solattn

@@ -26,6 +26,7 @@ constexpr int kRowsPerWG = kQuantThreads / 16;
 // Codes and scales follow quant_common.hpp.
 constexpr int kQuantR = 8;                       // tokens per lane group
 constexpr int kQuantTok = kQuantR * kRowsPerWG;  // tokens per workgroup
+static_assert(kQuantTok == SOLATTN_QUANT_BLOCK, "a workgroup quantises one scale block");
 
 struct QuantTensor {
   const uint16_t* x;
@@ -34,6 +35,7 @@ struct QuantTensor {
   const float* vscale;    // [B, H, D] per-channel scale (V rule), or null
   int8_t* xi;             // [B, TP, H, D]
   float* xs;              // [B, TP, H] per-token scales (not written by the V rule)
+  int block_scale;        // per-token rule with one scale per kQuantTok-token block
 };
 
 struct QuantArgs {
@@ -42,8 +44,18 @@ struct QuantArgs {
   int64_t TP;
 };
 
-// PER_CHANNEL: V against vscale[d]; otherwise per token, smoothed by mean
-// when the tensor has one.
+// The eight bf16 of a 16-byte load minus the smoothing mean (0 without one).
+__device__ __forceinline__ void smoothed(const uint4& raw, const float (&m)[8], float (&y)[8]) {
+  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    y[2 * e] = lo_bf16(w[e]) - m[2 * e];
+    y[2 * e + 1] = hi_bf16(w[e]) - m[2 * e + 1];
+  }
+}
+
+// PER_CHANNEL: V against vscale[d]; otherwise per token (or per block with
+// block_scale), smoothed by mean when the tensor has one.
 template <bool PER_CHANNEL>
 __device__ __forceinline__ void quant_rows_of(const QuantTensor& A, uint32_t T, uint32_t H,
                                               int64_t TP) {
@@ -67,19 +79,44 @@ __device__ __forceinline__ void quant_rows_of(const QuantTensor& A, uint32_t T, 
     rs[e] = PER_CHANNEL ? __builtin_amdgcn_rcpf(sv[e]) : 1.f;
   }
 
+  // Per-block rule: the |max| of the workgroup's tokens (one kQuantTok-token
+  // block of one head; tokens past T repeat token T-1 of the same block), over
+  // the 16 lanes of a row by DPP and over the 16 rows through LDS.
+  float block_ss = 0.f;
+  float block_rr[8], block_sv[8];
+  if (!PER_CHANNEL && A.block_scale) {
+    __shared__ uint32_t srow_max[kRowsPerWG];
+    uint32_t mb = 0;
+#pragma unroll
+    for (int r = 0; r < kQuantR; ++r) {
+      float y[8];
+      smoothed(raw[r], m, y);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) mb = max(mb, __float_as_uint(y[e]) & 0x7fffffffu);
+    }
+    mb = group16_max_bits(mb);
+    if ((threadIdx.x & 15) == 0) srow_max[threadIdx.x >> 4] = mb;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kRowsPerWG; ++i) mb = max(mb, srow_max[i]);
+    const float sc = div127(__uint_as_float(mb));
+    block_ss = sc > 1e-8f ? sc : 1e-8f;
+    const float rr = __builtin_amdgcn_rcpf(block_ss);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) block_rr[e] = rr, block_sv[e] = block_ss;
+  }
+
 #pragma unroll
   for (int r = 0; r < kQuantR; ++r) {
     const uint32_t t = t0 + r * kRowsPerWG;
-    const uint32_t w[4] = {raw[r].x, raw[r].y, raw[r].z, raw[r].w};
     float y[8];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      y[2 * e] = lo_bf16(w[e]) - m[2 * e];
-      y[2 * e + 1] = hi_bf16(w[e]) - m[2 * e + 1];
-    }
+    smoothed(raw[r], m, y);
     float ss = 1.f;
     uint2 o;
-    if (!PER_CHANNEL) {
+    if (!PER_CHANNEL && block_ss > 0.f) {  // the block's scale
+      ss = block_ss;
+      o = codes8(y, block_rr, block_sv);
+    } else if (!PER_CHANNEL) {
       ss = quant_token_row(y, o);
     } else {
       o = codes8(y, rs, sv);
@@ -136,8 +173,9 @@ int launch_quant3(const QuantTensor* ts, int n, int64_t B, int64_t T, int64_t H,
 
 int launch_quant(const uint16_t* x, int64_t sx_b, int64_t sx_t, int64_t sx_h, int64_t B,
                  int64_t T, int64_t H, int64_t D, const float* mean, const float* vscale,
-                 int8_t* xi, float* xs, int64_t TP, hipStream_t stream, const char* what) {
-  const QuantTensor t{x, sx_b, sx_t, sx_h, mean, vscale, xi, xs};
+                 int8_t* xi, float* xs, int64_t TP, hipStream_t stream, const char* what,
+                 int block_scale = 0) {
+  const QuantTensor t{x, sx_b, sx_t, sx_h, mean, vscale, xi, xs, block_scale};
   return launch_quant3(&t, 1, B, T, H, D, TP, stream, what);
 }
 
@@ -145,12 +183,12 @@ int quant_qkv(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h, const
               int64_t sk_b, int64_t sk_t, int64_t sk_h, const uint16_t* v, int64_t sv_b,
               int64_t sv_t, int64_t sv_h, int64_t B, int64_t T, int64_t H, int64_t D,
               const float* k_mean, const float* vscale, int8_t* qi, float* qs, int8_t* ki,
-              float* ks, int8_t* vi, int64_t TP, hipStream_t stream) {
+              float* ks, int8_t* vi, int64_t TP, hipStream_t stream, int qk_block) {
   QuantTensor ts[3];
   int n = 0;
-  if (q) ts[n++] = {q, sq_b, sq_t, sq_h, nullptr, nullptr, qi, qs};
-  ts[n++] = {k, sk_b, sk_t, sk_h, k_mean, nullptr, ki, ks};
-  if (vscale) ts[n++] = {v, sv_b, sv_t, sv_h, nullptr, vscale, vi, nullptr};
+  if (q) ts[n++] = {q, sq_b, sq_t, sq_h, nullptr, nullptr, qi, qs, qk_block};
+  ts[n++] = {k, sk_b, sk_t, sk_h, k_mean, nullptr, ki, ks, qk_block};
+  if (vscale) ts[n++] = {v, sv_b, sv_t, sv_h, nullptr, vscale, vi, nullptr, 0};
   return launch_quant3(ts, n, B, T, H, D, TP, stream, "quant_qkv");
 }
 
@@ -164,6 +202,15 @@ extern "C" int solattn_quant_rows(const uint16_t* x, int64_t sx_b, int64_t sx_t,
   clear_error();
   return launch_quant(x, sx_b, sx_t, sx_h, B, T, H, D, mean, nullptr, xi, xs, TP,
                       reinterpret_cast<hipStream_t>(stream), "quant_rows");
+}
+
+extern "C" int solattn_quant_rows_blocked(const uint16_t* x, int64_t sx_b, int64_t sx_t,
+                                          int64_t sx_h, int64_t B, int64_t T, int64_t H,
+                                          int64_t D, const float* mean, int8_t* xi, float* xs,
+                                          int64_t TP, solattn_stream_t stream) {
+  clear_error();
+  return launch_quant(x, sx_b, sx_t, sx_h, B, T, H, D, mean, nullptr, xi, xs, TP,
+                      reinterpret_cast<hipStream_t>(stream), "quant_rows_blocked", 1);
 }
 
 extern "C" int solattn_quant_v(const uint16_t* v, int64_t sv_b, int64_t sv_t, int64_t sv_h,

@@ -147,6 +147,20 @@ int solattn_quant_rows(const uint16_t* x, int64_t sx_b, int64_t sx_t, int64_t sx
                        int64_t B, int64_t T, int64_t H, int64_t D, const float* mean,
                        int8_t* xi, float* xs, int64_t TP, solattn_stream_t stream);
 
+/* Tokens per scale of the per-block INT8 variant below. */
+#define SOLATTN_QUANT_BLOCK 128
+
+/* solattn_quant_rows with one scale per block of SOLATTN_QUANT_BLOCK tokens
+ * (per batch and head) instead of one per token: s = max(fl(amax / 127),
+ * 1e-8) with amax the |max| of y over the block's tokens and channels, the
+ * same code rule, and s written to xs for every token of the block. No
+ * counterpart in the reference, which quantises Q and K per token: this is
+ * BASELINE config 3's "Q/K quantised per 128-token block" wording, reported
+ * beside the per-token parity mode. */
+int solattn_quant_rows_blocked(const uint16_t* x, int64_t sx_b, int64_t sx_t, int64_t sx_h,
+                               int64_t B, int64_t T, int64_t H, int64_t D, const float* mean,
+                               int8_t* xi, float* xs, int64_t TP, solattn_stream_t stream);
+
 /* Per-channel INT8 of V with vscale fp32 [B, H, D]:
  *   code = clamp(round_half_away(v / vscale[d]), -127, 127); vi: int8 [B, TP, H, D].
  * Replaces: _quant_v_kernel / quantize_v_per_channel,
@@ -229,6 +243,20 @@ int solattn_sol_attn_int8(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t
                           void* workspace, int64_t workspace_bytes, uint16_t* o,
                           int64_t so_b, int64_t so_t, int64_t so_h,
                           solattn_stream_t stream);
+
+/* solattn_sol_attn_int8 with Q and smoothed K quantised per
+ * SOLATTN_QUANT_BLOCK-token block (solattn_quant_rows_blocked) instead of per
+ * token; V, routing and the forward as there. No counterpart in the
+ * reference: the config 3 variant above. */
+int solattn_sol_attn_int8_qblock(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
+                                 const uint16_t* k, int64_t sk_b, int64_t sk_t, int64_t sk_h,
+                                 const uint16_t* v, int64_t sv_b, int64_t sv_t, int64_t sv_h,
+                                 int64_t B, int64_t T, int64_t H, int64_t D, int64_t block,
+                                 float scale, float tau, int64_t sink_kv_lo, int64_t sink_kv_hi,
+                                 int64_t sink_q_lo, int64_t sink_q_hi, int int8_pv,
+                                 void* workspace, int64_t workspace_bytes, uint16_t* o,
+                                 int64_t so_b, int64_t so_t, int64_t so_h,
+                                 solattn_stream_t stream);
 
 /* ------------------------------------------------ allocation-free BF16 --
  * solattn_sol_attn without a workspace argument, for callers that cannot

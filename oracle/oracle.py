@@ -68,6 +68,9 @@ def lib() -> ctypes.CDLL:
         L.or_route.restype = None
         L.or_quant_rows.argtypes = [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _i64]
         L.or_quant_rows.restype = None
+        L.or_quant_rows_blocked.argtypes = [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp,
+                                            _vp, _vp, _i64, _i64]
+        L.or_quant_rows_blocked.restype = None
         L.or_quant_v.argtypes = [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _i64]
         L.or_quant_v.restype = None
         L.or_f2bf.argtypes = [ctypes.c_float]
@@ -190,12 +193,19 @@ def tie_count(scores, thr, exact_a, exact_b, ulps: int = 8):
     return int(diff.sum()), bool(np.all(band[diff]))
 
 
-def quant_rows(x, mean=None, TP: int | None = None):
+def quant_rows(x, mean=None, TP: int | None = None, block: int | None = None):
+    """Per-token codes and scales (the reference's), or with ``block`` one scale
+    per block of that many tokens (BASELINE config 3's variant), written for
+    every token of the block."""
     B, T, H, D = x.shape
     TP = T if TP is None else TP
     xi = np.zeros((B, TP, H, D), np.int8)
     xs = np.zeros((B, TP, H), np.float32)
-    lib().or_quant_rows(_p(x), *_estrides(x), B, T, H, D, _p(mean), _p(xi), _p(xs), TP)
+    if block is None:
+        lib().or_quant_rows(_p(x), *_estrides(x), B, T, H, D, _p(mean), _p(xi), _p(xs), TP)
+    else:
+        lib().or_quant_rows_blocked(_p(x), *_estrides(x), B, T, H, D, _p(mean), _p(xi), _p(xs),
+                                    TP, int(block))
     return xi, xs
 
 
@@ -209,7 +219,7 @@ def quant_v(v, vscale, TP: int | None = None):
 
 def prepare(q, k, v, *, block: int, scale: float | None = None, tau: float = 1.0,
             int8: bool = False, sink_kv=(0, 0), sink_q=(0, 0), int8_pv: bool = True,
-            want_scores: bool = False):
+            want_scores: bool = False, quant_block: int | None = None):
     """The whole pre-forward pipeline: BF16 ``prepare`` (/root/reference/_preprocess.py:268)
     or INT8 ``fused_preprocess`` (/root/reference/_fused_prep.py:62)."""
     B, T, H, D = q.shape
@@ -224,8 +234,8 @@ def prepare(q, k, v, *, block: int, scale: float | None = None, tau: float = 1.0
                kc_mean=mean, kc_var=var, thr=thr, counts=counts, lists=lists, mask=mask,
                scores=scores, vamax_part=amax, int8=int8)
     if int8:
-        qi, qs = quant_rows(q)
-        ki, ks = quant_rows(k, mean=mean)
+        qi, qs = quant_rows(q, block=quant_block)
+        ki, ks = quant_rows(k, mean=mean, block=quant_block)
         out.update(qi=qi, qs=qs, ki=ki, ks=ks)
         if int8_pv:
             out.update(vi=quant_v(v, vscale), vscale=vscale)

@@ -326,6 +326,43 @@ void or_quant_rows(const uint16_t* x, int64_t sx_b, int64_t sx_t, int64_t sx_h, 
       }
 }
 
+/* Per block of QB tokens (BASELINE config 3's "Q/K quantised per 128-token
+ * block ... fp32 scales (symmetric, absmax)"; the reference itself quantises
+ * per token): one scale per (b, block, h) from the |max| over the block's
+ * tokens and channels, the same code rule as per token, and the block's scale
+ * written for every token of the block. */
+void or_quant_rows_blocked(const uint16_t* x, int64_t sx_b, int64_t sx_t, int64_t sx_h,
+                           int64_t B, int64_t T, int64_t H, int64_t D, const float* mean,
+                           int8_t* xi, float* xs, int64_t TP, int64_t QB) {
+  if (QB <= 0) return;
+  const int64_t NB = (T + QB - 1) / QB;
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int64_t b = 0; b < B; ++b)
+    for (int64_t j = 0; j < NB; ++j)
+      for (int64_t h = 0; h < H; ++h) {
+        const int64_t t0 = j * QB, t1 = t0 + QB < T ? t0 + QB : T;
+        float amax = 0.f;
+        for (int64_t t = t0; t < t1; ++t)
+          for (int64_t d = 0; d < D; ++d) {
+            float val = bf2f(x[b * sx_b + t * sx_t + h * sx_h + d]);
+            if (mean) val = val - mean[(b * H + h) * D + d];
+            float a = fabsf(val);
+            if (a > amax) amax = a;
+          }
+        float s = amax / 127.0f;
+        float ss = s > 1e-8f ? s : 1e-8f;
+        for (int64_t t = t0; t < t1; ++t) {
+          int64_t o = ((b * TP + t) * H + h) * D;
+          for (int64_t d = 0; d < D; ++d) {
+            float val = bf2f(x[b * sx_b + t * sx_t + h * sx_h + d]);
+            if (mean) val = val - mean[(b * H + h) * D + d];
+            xi[o + d] = round_half_away_clamp(val / ss);
+          }
+          xs[(b * TP + t) * H + h] = ss;
+        }
+      }
+}
+
 /* Per channel V: /root/reference/_fused_quant.py:77-88. */
 void or_quant_v(const uint16_t* v, int64_t sv_b, int64_t sv_t, int64_t sv_h, int64_t B,
                 int64_t T, int64_t H, int64_t D, const float* vscale, int8_t* vi, int64_t TP) {

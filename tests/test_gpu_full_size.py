@@ -137,6 +137,34 @@ def test_full_size_int8(pkg, dev, video, int8_pv, block, tau):
                       out.float().cpu().numpy(), qb, vb, ref, rows, int8_pv, block)
 
 
+@pytest.mark.parametrize("int8_pv", [True, False])
+def test_full_size_int8_quant_block(pkg, dev, video, int8_pv):
+    """BASELINE config 3's wording, Q/K quantised per 128-token block, at full
+    size: codes and scales bit-exact, routing unchanged, forward per query block
+    against the oracle loops fed the same codes."""
+    fp = importlib.import_module(f"{pkg.__name__}._fused_prep")
+    i8 = importlib.import_module(f"{pkg.__name__}._int8_fwd")
+    cfg, (q, k, v), (qb, kb, vb) = video
+    block, tau = 128, cfg["tau"]
+    r, qi, qs, ki, ks, vi = fp.fused_preprocess_routing(q, k, v, tau=tau, scale=128 ** -0.5,
+                                                        block=block, quant_block=128)
+    out = i8.sol_attn_int8(q, k, v, tau=tau, block=block, int8_pv=int8_pv, quant_block=128)
+    torch.cuda.synchronize()
+    ref = oracle.prepare(qb, kb, vb, block=block, tau=tau, int8=True, int8_pv=int8_pv,
+                         quant_block=128)
+    _route_equal(r, ref)
+    T = ref["T"]
+    assert np.array_equal(qi[:, :T].cpu().numpy(), ref["qi"][:, :T])
+    assert np.array_equal(ki[:, :T].cpu().numpy(), ref["ki"][:, :T])
+    assert np.array_equal(qs[:, :T].cpu().numpy().view(np.uint32), ref["qs"][:, :T].view(np.uint32))
+    assert np.array_equal(ks[:, :T].cpu().numpy().view(np.uint32), ref["ks"][:, :T].view(np.uint32))
+    print(f"[full size int8 quant_block 128 pv={int8_pv}] routing and codes bit-exact", flush=True)
+    NT = ref["NT"]
+    rows = sorted(set(_sample_rows(cfg["H"], NT, 32, seed=7)) | {(0, 0, NT - 1)})
+    check_int8_blocks(f"full size int8 quant_block pv={int8_pv}", out.float().cpu().numpy(), qb,
+                      vb, ref, rows, int8_pv, block)
+
+
 @pytest.fixture(scope="module")
 def image(pkg, dev):
     cfg = dict(bench.CONFIGS[1])

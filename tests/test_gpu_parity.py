@@ -89,6 +89,39 @@ def test_quant_bit_exact(pkg, dev, mean, shape):
     assert np.array_equal(vi.cpu().numpy(), oracle.quant_v(bits(x), rsc))
 
 
+@pytest.mark.parametrize("shape,block", [((2, 333, 3), 64), ((1, 2048, 8), 128), ((1, 200, 2), 64)])
+def test_quant_blocked_bit_exact(pkg, dev, shape, block):
+    """Per-128-token-block Q and smoothed-K scales (the config 3 variant) through
+    the INT8 preparation: codes and scales bit-exact against the oracle,
+    including a ragged last scale block and a head whose block max is planted
+    in one row; the one call feeds the forward the same bits."""
+    fp, i8 = _mods(pkg)[3], _mods(pkg)[2]
+    B, T, H = shape
+    q, k, v = (randn_bf16((B, T, H, 128), s) for s in (50, 51, 52))  # unit scale, as the
+    q[0, 3, 0, 5] = 6.0  # other INT8 tests' bounds assume; one row holds its block's max
+    print(f"[quant_blocked] shape={shape} block={block}", flush=True)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    r, qi, qs, ki, ks, vi = fp.fused_preprocess_routing(qd, kd, vd, tau=0.9, scale=128 ** -0.5,
+                                                        block=block, quant_block=128)
+    ref = oracle.prepare(bits(q), bits(k), bits(v), block=block, tau=0.9, int8=True,
+                         quant_block=128)
+    assert np.array_equal(qi.cpu().numpy(), ref["qi"]) and np.array_equal(ki.cpu().numpy(), ref["ki"])
+    assert np.array_equal(qs.cpu().numpy().view(np.uint32), ref["qs"].view(np.uint32))
+    assert np.array_equal(ks.cpu().numpy().view(np.uint32), ref["ks"].view(np.uint32))
+    assert qs[0, 0, 0].item() == qs[0, min(T, 128) - 1, 0].item()  # one scale per block
+    for pv in (True, False):
+        two = i8.forward_int8(qd, vd, r, qi, qs, ki, ks, vi if pv else None, int8_pv=pv)
+        one = i8.sol_attn_int8(qd, kd, vd, tau=0.9, block=block, int8_pv=pv, quant_block=128)
+        torch.cuda.synchronize()
+        assert torch.equal(one.view(torch.int16), two.view(torch.int16))
+        if pv:
+            assert np.array_equal(vi.cpu().numpy(), ref["vi"])
+        refp = oracle.prepare(bits(q), bits(k), bits(v), block=block, tau=0.9, int8=True,
+                              int8_pv=pv, quant_block=128)
+        check_int8_blocks(f"quant_blocked {shape} pv={pv}", one.float().cpu().numpy(), bits(q),
+                          bits(v), refp, _rows(B, H, refp["NT"], limit=16), pv, block)
+
+
 def test_reorder_matches_index_select(pkg, dev):
     mort = _mods(pkg)[5]
     x = randn_bf16((2, 21 * 6 * 10, 3 * 128), 7).to(dev)

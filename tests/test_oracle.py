@@ -236,6 +236,50 @@ def test_quant_known_answers():
     assert xi.min() >= -127
 
 
+def test_quant_blocked_known_answers():
+    """Per-128-token-block scales (BASELINE config 3's variant): one scale per
+    (batch, block, head) from the block's |max|, the per-token code rule, the
+    scale written for every token of the block; a ragged last block has its
+    own scale."""
+    D, QB = 128, 128
+    x = np.zeros((1, 200, 2, D), np.float32)
+    x[0, 5, 0, 3] = 127.0                               # block 0, head 0: scale 1
+    x[0, 9, 0, :4] = [2.5, -2.5, 1.25, -0.5]           # ties away from zero at scale 1
+    x[0, 130, 0, 7] = -63.5                             # block 1 (72 tokens): scale 0.5
+    x[0, 131, 0, :2] = [1.25, -0.25]                    # -> 2.5 -> 3, -0.5 -> -1
+    x[0, :, 1, :] = 3.0                                 # head 1: constant -> all 127
+    xi, xs = oracle.quant_rows(oracle.f32_to_bf16(x), block=QB)
+    assert (xs[0, :128, 0] == np.float32(1.0)).all() and (xs[0, 128:, 0] == np.float32(0.5)).all()
+    assert list(xi[0, 9, 0, :4]) == [3, -3, 1, -1]
+    assert xi[0, 5, 0, 3] == 127 and xi[0, 130, 0, 7] == -127
+    assert list(xi[0, 131, 0, :2]) == [3, -1]
+    assert (xi[0, :, 1] == 127).all() and (xs[0, :, 1] == np.float32(3.0 / 127.0)).all()
+
+
+def test_quant_blocked_equals_per_token_on_equal_row_maxima():
+    """The blocked scale is the largest per-token scale of its block (fl(a/127)
+    is monotonic), smoothing included; and when every token row of a block
+    holds the block's |max| the per-block and per-token rules give the same
+    codes and scales."""
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((2, 300, 3, 128)).astype(np.float32)
+    mean = (rng.standard_normal((2, 3, 128)) * 0.1).astype(np.float32)
+    xb = oracle.f32_to_bf16(x)
+    ts = oracle.quant_rows(xb, mean)[1]
+    bs = oracle.quant_rows(xb, mean, block=128)[1]
+    for j in range(0, 300, 128):
+        blk = slice(j, min(j + 128, 300))
+        assert np.all(bs[:, blk] == ts[:, blk].max(1, keepdims=True))
+    xr = oracle.bf16_to_f32(xb)                          # plant each block's |max| in every row
+    for j in range(0, 300, 128):
+        blk = slice(j, min(j + 128, 300))
+        xr[:, blk, :, 0] = np.abs(xr[:, blk]).max(axis=(1, 3))[:, None, :]
+    xp = oracle.f32_to_bf16(xr)                          # bf16 values: exact
+    ti, ts = oracle.quant_rows(xp)
+    bi, bs = oracle.quant_rows(xp, block=128)
+    assert np.array_equal(bi, ti) and np.array_equal(bs, ts)
+
+
 def test_division_free_scale_matches_ieee():
     """The quantisers' per-token scale fl(amax / 127) computed without a
     division (one fma residual step on amax * fl(1/127)) equals the IEEE
