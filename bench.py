@@ -426,6 +426,11 @@ def main():
         for key, pv in (("int8_ms", False), ("int8_pv_ms", True)):
             line[key] = {str(t): round(time_cuda(lambda: i8(q, k, v, tau=t, block=block, int8_pv=pv),
                                                  args.steps, args.warmup), 4) for t in (0.8, 0.9, 0.95)}
+        # config 3's wording, Q/K scales per 128-token block (not the parity mode)
+        for key, pv in (("int8_qblock_ms", False), ("int8_pv_qblock_ms", True)):
+            line[key] = {str(t): round(time_cuda(lambda: i8(q, k, v, tau=t, block=block, int8_pv=pv,
+                                                            quant_block=128),
+                                                 args.steps, args.warmup), 4) for t in (0.8, 0.9, 0.95)}
         # the INT8 forward kernel alone at the config's tau, against the MFMA roofline
         fp = mods["_fused_prep"].fused_preprocess_routing(q, k, v, tau=tau, scale=D ** -0.5,
                                                           block=block)
