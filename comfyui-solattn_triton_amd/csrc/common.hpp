@@ -84,4 +84,16 @@ int quant_qkv(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h, const
               const float* k_mean, const float* vscale, int8_t* qi, float* qs, int8_t* ki,
               float* ks, int8_t* vi, int64_t TP, hipStream_t stream, int qk_block = 0);
 
+// solattn_fwd_int8 without clearing the error slot; uniform_ks: every 64-key
+// tile of K shares one scale (K quantised per 128-token block), so the
+// kernels multiply it once per tile instead of once per score.
+int fwd_int8(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h, const int8_t* qi,
+             const float* qs, const int8_t* ki, const float* ks, const int8_t* vi,
+             const float* vscale, const uint16_t* v, int64_t sv_b, int64_t sv_t, int64_t sv_h,
+             int64_t TP, const uint16_t* kc, const uint16_t* vc, int64_t npad,
+             const int32_t* counts, const int16_t* lists, const uint32_t* mask, int64_t B,
+             int64_t T, int64_t H, int64_t D, int64_t block, float scale, int int8_pv,
+             uint16_t* o, int64_t so_b, int64_t so_t, int64_t so_h, solattn_stream_t stream,
+             bool uniform_ks);
+
 }  // namespace solattn

@@ -57,6 +57,10 @@ __device__ __forceinline__ i32x4 ki_op(const char* kt, int m, int cc, int col, i
 // s[m][r] = int32 score * ks[key]: the reference's exact_scores without the
 // query factor qs*c, which multiplies later (it is positive, so it commutes
 // with the row max) (/root/reference/_int8_fwd.py:328-330).
+// UKS (uniform K scale: K quantised with one scale per 128-token block, so the
+// 64 keys of a tile share it): s = int32 score, and the tile's ks joins the
+// query factor instead (tile_qsl), one multiply per tile instead of per score.
+template <bool UKS>
 __device__ __forceinline__ void scale_scores(const char* kt, const i32x16 (&si)[2], int half,
                                              f32x16 (&s)[2]) {
   const float* ksl = reinterpret_cast<const float*>(kt + kKsOffset);
@@ -64,12 +68,26 @@ __device__ __forceinline__ void scale_scores(const char* kt, const i32x16 (&si)[
   for (int m = 0; m < 2; ++m)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float4 k4 = *reinterpret_cast<const float4*>(ksl + 32 * m + 8 * i + 4 * half);
-      s[m][4 * i + 0] = static_cast<float>(si[m][4 * i + 0]) * k4.x;
-      s[m][4 * i + 1] = static_cast<float>(si[m][4 * i + 1]) * k4.y;
-      s[m][4 * i + 2] = static_cast<float>(si[m][4 * i + 2]) * k4.z;
-      s[m][4 * i + 3] = static_cast<float>(si[m][4 * i + 3]) * k4.w;
+      if constexpr (UKS) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) s[m][4 * i + j] = static_cast<float>(si[m][4 * i + j]);
+      } else {
+        const float4 k4 = *reinterpret_cast<const float4*>(ksl + 32 * m + 8 * i + 4 * half);
+        s[m][4 * i + 0] = static_cast<float>(si[m][4 * i + 0]) * k4.x;
+        s[m][4 * i + 1] = static_cast<float>(si[m][4 * i + 1]) * k4.y;
+        s[m][4 * i + 2] = static_cast<float>(si[m][4 * i + 2]) * k4.z;
+        s[m][4 * i + 3] = static_cast<float>(si[m][4 * i + 3]) * k4.w;
+      }
     }
+}
+
+// The factor of a tile's scores from scale_scores<UKS>: qs*c, times the ks
+// its keys share when UKS (key 0's, in LDS behind the tile's int8 rows at
+// byte ks_offset).
+template <bool UKS>
+__device__ __forceinline__ float tile_qsl(const char* kt, int ks_offset, float qsl) {
+  if constexpr (UKS) return qsl * *reinterpret_cast<const float*>(kt + ks_offset);
+  return qsl;
 }
 
 __device__ __forceinline__ void qk_i8_tile(const char* kt, const i32x4 (&qi)[4], int col, int half,
@@ -183,10 +201,11 @@ __device__ __forceinline__ void exact_softmax_pv(SoftmaxState& st, f32x16 (&s)[2
   }
 }
 
-// Pipelined step over full exact tile n (scaled scores in sc): the i8 MFMAs
-// of S(n+1) from the K tile kn are interleaved with the softmax of tile n;
-// then P(n).V(n) and the conversion of S(n+1) into sn (ks of tile n+1 from kn).
-template <bool INT8_PV>
+// Pipelined step over full exact tile n (scaled scores in sc, factor qsl):
+// the i8 MFMAs of S(n+1) from the K tile kn are interleaved with the softmax
+// of tile n; then P(n).V(n) and the conversion of S(n+1) into sn (ks of tile
+// n+1 from kn).
+template <bool INT8_PV, bool UKS>
 __device__ __forceinline__ void fast_step(SoftmaxState& st, f32x16 (&sc)[2], f32x16 (&sn)[2],
                                           const char* kn, const void* vt, const i32x4 (&qi)[4],
                                           float qsl, int lane) {
@@ -260,11 +279,11 @@ __device__ __forceinline__ void fast_step(SoftmaxState& st, f32x16 (&sc)[2], f32
   }
   rescale(st, alpha);
   if constexpr (INT8_PV) {
-    scale_scores(kn, si, half, sn);  // frees the int32 scores before the P.V accumulators
+    scale_scores<UKS>(kn, si, half, sn);  // frees the int32 scores before the P.V accumulators
     pv_i8(static_cast<const char*>(vt), pi, beta * (1.f / 127.f), lane, st.acc);
   } else {
     pv_tile(static_cast<const uint16_t*>(vt), pb, lane, st.acc);
-    scale_scores(kn, si, half, sn);
+    scale_scores<UKS>(kn, si, half, sn);
   }
 }
 
@@ -339,7 +358,7 @@ __device__ __forceinline__ void issue_i8(uint32_t dst, const int8_t* rows, const
 // (52 KB, three workgroups per CU: 3.66 -> 3.40 ms at cfg 2 against two
 // workgroups of 68 KB with one wave per SIMD; a single-buffered form spilled in
 // the step loop and ran 1.5x slower).
-template <int BLK, bool INT8_PV>
+template <int BLK, bool INT8_PV, bool UKS>
 __global__ void __launch_bounds__(BLK * 2)
 __attribute__((amdgpu_waves_per_eu(2)))
 fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
@@ -467,7 +486,7 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
       f32x16 s[2];
       const char* kt = reinterpret_cast<const char*>(Kp(0));
       qk_i8_tile(kt, qireg, col, half, si);
-      scale_scores(kt, si, half, s);
+      scale_scores<UKS>(kt, si, half, s);
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
         const uint32_t bits = static_cast<uint32_t>(td.amask >> (32 * m + 4 * half));
@@ -475,47 +494,51 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
         for (int r = 0; r < 16; ++r)
           s[m][r] = ((bits >> (8 * (r >> 2) + (r & 3))) & 1u) ? s[m][r] : -INFINITY;
       }
-      exact_softmax_pv<INT8_PV>(st, s, Vp(0), qsl, lane);
+      exact_softmax_pv<INT8_PV>(st, s, Vp(0), tile_qsl<UKS>(kt, kKsOffset, qsl), lane);
       __syncthreads();
     }
-    // full exact tiles, pipelined (tile F = nrag was issued into buffers bi(F))
+    // full exact tiles, pipelined (tile F = nrag was issued into buffers bi(F));
+    // fa, fb: the score factors of sa, sb
     const int F = nrag;
     if (nfast > 0) {
       const int E = nexact;  // one past the last full exact tile
       f32x16 sa[2], sb[2];
+      float fa, fb;
       const auto qk_scaled = [&](const uint16_t* kb, f32x16 (&s)[2]) {
         i32x16 si[2];
         const char* kt = reinterpret_cast<const char*>(kb);
         qk_i8_tile(kt, qireg, col, half, si);
-        scale_scores(kt, si, half, s);
+        scale_scores<UKS>(kt, si, half, s);
+        return tile_qsl<UKS>(kt, kKsOffset, qsl);
       };
       wait_tile_copies();
       __syncthreads();
       if (F + 1 < E) issue_exact_full(F + 1, kbuf_at((F + 1) & 1), 0u, true, false);
-      qk_scaled(Kp(F & 1), sa);
+      fa = qk_scaled(Kp(F & 1), sa);
       wait_tile_copies();
       __syncthreads();  // K(F & 1) is refilled (K of tile F+2) by the first step
       int n = F;
       // Step n needs n + 1 < E. K(n+2) of the last step is clamped to the
       // last full tile: a redundant copy into a buffer nothing reads afterwards.
-      const auto step = [&](f32x16 (&sc)[2], f32x16 (&sn)[2]) {
+      const auto step = [&](f32x16 (&sc)[2], float qc, f32x16 (&sn)[2], float& qn) {
         issue_exact_full(min(n + 2, E - 1), kbuf_at(n & 1), 0u, true, false);
         issue_exact_full(n + 1, 0u, vbuf_at((n + 1) & 1), false, true);
-        fast_step<INT8_PV>(st, sc, sn, reinterpret_cast<const char*>(Kp((n + 1) & 1)), Vp(n & 1),
-                           qireg, qsl, lane);
+        const char* kn = reinterpret_cast<const char*>(Kp((n + 1) & 1));
+        fast_step<INT8_PV, UKS>(st, sc, sn, kn, Vp(n & 1), qireg, qc, lane);
+        qn = tile_qsl<UKS>(kn, kKsOffset, qsl);
         wait_tile_copies();
         __syncthreads();
         ++n;
       };
       while (n + 2 < E) {
-        step(sa, sb);
-        step(sb, sa);
+        step(sa, fa, sb, fb);
+        step(sb, fb, sa, fa);
       }
       if (n + 1 < E) {
-        step(sa, sb);
-        exact_softmax_pv<INT8_PV>(st, sb, Vp(bi(n)), qsl, lane);
+        step(sa, fa, sb, fb);
+        exact_softmax_pv<INT8_PV>(st, sb, Vp(bi(n)), fb, lane);
       } else {
-        exact_softmax_pv<INT8_PV>(st, sa, Vp(bi(n)), qsl, lane);
+        exact_softmax_pv<INT8_PV>(st, sa, Vp(bi(n)), fa, lane);
       }
       __syncthreads();
     }
@@ -590,34 +613,34 @@ __device__ __forceinline__ void issue_blk(uint32_t dst, const int8_t* rows, cons
   }
 }
 
-// s[m][r] = int32 score * ks[key] for the four 32-key chunks of a block.
-__device__ __forceinline__ void scale_block(const char* kt, const i32x16 (&si)[4], int half,
-                                            f32x16 (&s)[4]) {
-  const float* ksl = reinterpret_cast<const float*>(kt + kBlkKsOffset);
-#pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    if (m > 0) asm volatile("" ::: "memory");  // one chunk's ks loads at a time
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float4 k4 = *reinterpret_cast<const float4*>(ksl + 32 * m + 8 * i + 4 * half);
-      s[m][4 * i + 0] = static_cast<float>(si[m][4 * i + 0]) * k4.x;
-      s[m][4 * i + 1] = static_cast<float>(si[m][4 * i + 1]) * k4.y;
-      s[m][4 * i + 2] = static_cast<float>(si[m][4 * i + 2]) * k4.z;
-      s[m][4 * i + 3] = static_cast<float>(si[m][4 * i + 3]) * k4.w;
-    }
-  }
-}
-
-// s = int32 scores of 32-key chunk m * ks[key].
+// s = int32 scores of 32-key chunk m * ks[key] (UKS: the 128 keys of the
+// block share one ks, which tile_qsl folds into the block's factor).
+template <bool UKS>
 __device__ __forceinline__ void scale_chunk(const char* kt, const i32x16& si, int m, int half, f32x16& s) {
   const float* ksl = reinterpret_cast<const float*>(kt + kBlkKsOffset) + 32 * m + 4 * half;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const float4 k4 = *reinterpret_cast<const float4*>(ksl + 8 * i);
-    s[4 * i + 0] = static_cast<float>(si[4 * i + 0]) * k4.x;
-    s[4 * i + 1] = static_cast<float>(si[4 * i + 1]) * k4.y;
-    s[4 * i + 2] = static_cast<float>(si[4 * i + 2]) * k4.z;
-    s[4 * i + 3] = static_cast<float>(si[4 * i + 3]) * k4.w;
+    if constexpr (UKS) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) s[4 * i + j] = static_cast<float>(si[4 * i + j]);
+    } else {
+      const float4 k4 = *reinterpret_cast<const float4*>(ksl + 8 * i);
+      s[4 * i + 0] = static_cast<float>(si[4 * i + 0]) * k4.x;
+      s[4 * i + 1] = static_cast<float>(si[4 * i + 1]) * k4.y;
+      s[4 * i + 2] = static_cast<float>(si[4 * i + 2]) * k4.z;
+      s[4 * i + 3] = static_cast<float>(si[4 * i + 3]) * k4.w;
+    }
+  }
+}
+
+// scale_chunk over the four 32-key chunks of a block.
+template <bool UKS>
+__device__ __forceinline__ void scale_block(const char* kt, const i32x16 (&si)[4], int half,
+                                            f32x16 (&s)[4]) {
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    if (m > 0) asm volatile("" ::: "memory");  // one chunk's ks loads at a time
+    scale_chunk<UKS>(kt, si[m], m, half, s[m]);
   }
 }
 
@@ -666,8 +689,8 @@ __device__ __forceinline__ void pv_blk(const char* vt, const i32x4 (&pi)[4], flo
 // Block step: the i8 MFMAs of S(b+1) (chunk 0 beside the row max of block b,
 // chunks 1-2 beside its P codes), then P(b).V(b) and the conversion of
 // S(b+1) into scaled scores while block b+1's ks are in LDS. QK = false: the
-// last block (softmax and P.V only).
-template <bool QK>
+// last block (softmax and P.V only). qsl: the factor of sc's scores.
+template <bool QK, bool UKS>
 __device__ __forceinline__ void block_step(SoftmaxState& st, const f32x16 (&sc)[4], f32x16 (&sn)[4],
                                            const char* kn, const char* vt, const i32x4 (&qi)[4],
                                            float qsl, int lane) {
@@ -704,7 +727,7 @@ __device__ __forceinline__ void block_step(SoftmaxState& st, const f32x16 (&sc)[
   // P(b).V(b); chunk dt of S(b+1) is scaled beside channel tile dt's MFMAs
   pv_blk(vt, pi, beta * (1.f / 127.f), lane, st.acc, [&](int dt) {
     if constexpr (QK) {
-      scale_chunk(kn, si[dt], dt, half, sn[dt]);
+      scale_chunk<UKS>(kn, si[dt], dt, half, sn[dt]);
       asm volatile("" : "+v"(sn[dt]));
     }
   });
@@ -715,6 +738,7 @@ __device__ __forceinline__ void block_step(SoftmaxState& st, const f32x16 (&sc)[
 // tiles of a ragged last block (plain, per 64-key tile), the V channel scale,
 // then the pooled tiles in bf16. K and V blocks double buffered: 65 KB of
 // LDS, two workgroups per CU, two waves per SIMD.
+template <bool UKS>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 fwd_int8_b128_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
                      const int8_t* __restrict__ qi, const float* __restrict__ qs,
@@ -789,36 +813,39 @@ fwd_int8_b128_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t,
     }
     if (nfb > 0) {
       f32x16 sa[4], sb[4];
+      float fa, fb;  // the score factors of sa, sb
       wait_tile_copies();
       __syncthreads();
       {
         i32x16 si[4];
 #pragma unroll
         for (int m = 0; m < 4; ++m) si[m] = qk_chunk(Kp(0), qireg, m, col, half);
-        scale_block(Kp(0), si, half, sa);
+        scale_block<UKS>(Kp(0), si, half, sa);
+        fa = tile_qsl<UKS>(Kp(0), kBlkKsOffset, qsl);
       }
       __syncthreads();  // K(0) is refilled (K of block 2) by the first step
       int e = 0;
       // Step e needs e + 1 < nfb; K(e+2) past the last block is clamped to it
       // (a redundant copy into a buffer nothing reads afterwards).
-      const auto step = [&](const f32x16 (&sc)[4], f32x16 (&sn)[4]) {
+      const auto step = [&](const f32x16 (&sc)[4], float fc, f32x16 (&sn)[4], float& fn) {
         issue_k(min(e + 2, nfb - 1), e & 1);
         issue_v(e + 1, (e + 1) & 1);
-        block_step<true>(st, sc, sn, Kp((e + 1) & 1), Vp(e & 1), qireg, qsl, lane);
+        block_step<true, UKS>(st, sc, sn, Kp((e + 1) & 1), Vp(e & 1), qireg, fc, lane);
+        fn = tile_qsl<UKS>(Kp((e + 1) & 1), kBlkKsOffset, qsl);
         wait_tile_copies();
         __syncthreads();
         ++e;
       };
       while (e + 2 < nfb) {
-        step(sa, sb);
-        step(sb, sa);
+        step(sa, fa, sb, fb);
+        step(sb, fb, sa, fa);
       }
       f32x16 dummy[4];
       if (e + 1 < nfb) {
-        step(sa, sb);
-        block_step<false>(st, sb, dummy, nullptr, Vp(e & 1), qireg, qsl, lane);
+        step(sa, fa, sb, fb);
+        block_step<false, UKS>(st, sb, dummy, nullptr, Vp(e & 1), qireg, fb, lane);
       } else {
-        block_step<false>(st, sa, dummy, nullptr, Vp(e & 1), qireg, qsl, lane);
+        block_step<false, UKS>(st, sa, dummy, nullptr, Vp(e & 1), qireg, fa, lane);
       }
       __syncthreads();
     }
@@ -833,7 +860,7 @@ fwd_int8_b128_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t,
       f32x16 s[2];
       const char* kt = Kp(0);
       qk_i8_tile(kt, qireg, col, half, si);
-      scale_scores(kt, si, half, s);
+      scale_scores<UKS>(kt, si, half, s);
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
         const uint32_t bits = static_cast<uint32_t>(td.amask >> (32 * m + 4 * half));
@@ -841,7 +868,7 @@ fwd_int8_b128_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t,
         for (int r = 0; r < 16; ++r)
           s[m][r] = ((bits >> (8 * (r >> 2) + (r & 3))) & 1u) ? s[m][r] : -INFINITY;
       }
-      exact_softmax_pv<true>(st, s, Vp(0), qsl, lane);
+      exact_softmax_pv<true>(st, s, Vp(0), tile_qsl<UKS>(kt, kKsOffset, qsl), lane);
       __syncthreads();
     }
     // The per-channel V scale, common to every exact block; the empty asm
@@ -886,7 +913,7 @@ fwd_int8_b128_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t,
   store_rows(st, o + b * so_b + h * so_h, so_t, qrow, T, half);
 }
 
-template <int BLK, bool PV>
+template <int BLK, bool PV, bool UKS>
 void launch_i8(uint32_t grid, hipStream_t s, const uint16_t* q, int64_t sq_b, int64_t sq_t,
                int64_t sq_h, const int8_t* qi, const float* qs, const int8_t* ki, const float* ks,
                const int8_t* vi, const float* vscale, const uint16_t* v, int64_t sv_b,
@@ -894,26 +921,34 @@ void launch_i8(uint32_t grid, hipStream_t s, const uint16_t* q, int64_t sq_b, in
                int64_t npad, const int32_t* counts, const int16_t* lists, const uint32_t* mask,
                int T, int H, int NT, int W, float c, uint16_t* o, int64_t so_b, int64_t so_t,
                int64_t so_h) {
-  hipLaunchKernelGGL((fwd_int8_kernel<BLK, PV>), dim3(grid), dim3(BLK * 2), blist_lds_bytes(NT), s, q, sq_b, sq_t,
+  hipLaunchKernelGGL((fwd_int8_kernel<BLK, PV, UKS>), dim3(grid), dim3(BLK * 2), blist_lds_bytes(NT), s, q, sq_b, sq_t,
                      sq_h, qi, qs, ki, ks, vi, vscale, v, sv_b, sv_t, sv_h, TP, kc, vc, npad,
                      counts, lists, mask, T, H, NT, W, c, o, so_b, so_t, so_h);
 }
 
+template <int BLK, bool PV>
+void launch_i8_ks(bool uks, uint32_t grid, hipStream_t s, const uint16_t* q, int64_t sq_b,
+                  int64_t sq_t, int64_t sq_h, const int8_t* qi, const float* qs, const int8_t* ki,
+                  const float* ks, const int8_t* vi, const float* vscale, const uint16_t* v,
+                  int64_t sv_b, int64_t sv_t, int64_t sv_h, int64_t TP, const uint16_t* kc,
+                  const uint16_t* vc, int64_t npad, const int32_t* counts, const int16_t* lists,
+                  const uint32_t* mask, int T, int H, int NT, int W, float c, uint16_t* o,
+                  int64_t so_b, int64_t so_t, int64_t so_h) {
+  (uks ? launch_i8<BLK, PV, true> : launch_i8<BLK, PV, false>)(
+      grid, s, q, sq_b, sq_t, sq_h, qi, qs, ki, ks, vi, vscale, v, sv_b, sv_t, sv_h, TP, kc, vc,
+      npad, counts, lists, mask, T, H, NT, W, c, o, so_b, so_t, so_h);
+}
+
 }  // namespace int8fwd
-}  // namespace solattn
 
-using namespace solattn;
-
-extern "C" int solattn_fwd_int8(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
-                                const int8_t* qi, const float* qs, const int8_t* ki,
-                                const float* ks, const int8_t* vi, const float* vscale,
-                                const uint16_t* v, int64_t sv_b, int64_t sv_t, int64_t sv_h,
-                                int64_t TP, const uint16_t* kc, const uint16_t* vc, int64_t npad,
-                                const int32_t* counts, const int16_t* lists, const uint32_t* mask,
-                                int64_t B, int64_t T, int64_t H, int64_t D, int64_t block,
-                                float scale, int int8_pv, uint16_t* o, int64_t so_b, int64_t so_t,
-                                int64_t so_h, solattn_stream_t stream) {
-  clear_error();
+int fwd_int8(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h, const int8_t* qi,
+             const float* qs, const int8_t* ki, const float* ks, const int8_t* vi,
+             const float* vscale, const uint16_t* v, int64_t sv_b, int64_t sv_t, int64_t sv_h,
+             int64_t TP, const uint16_t* kc, const uint16_t* vc, int64_t npad,
+             const int32_t* counts, const int16_t* lists, const uint32_t* mask, int64_t B,
+             int64_t T, int64_t H, int64_t D, int64_t block, float scale, int int8_pv,
+             uint16_t* o, int64_t so_b, int64_t so_t, int64_t so_h, solattn_stream_t stream,
+             bool uniform_ks) {
   if (int rc = check_fwd_common(q, sq_b, sq_t, sq_h, kc, vc, npad, counts, lists, mask, B, T, H, D,
                                 block, o, so_b, so_t, so_h, "fwd_int8"))
     return rc;
@@ -943,15 +978,33 @@ extern "C" int solattn_fwd_int8(const uint16_t* q, int64_t sq_b, int64_t sq_t, i
       so_b, so_t, so_h
   if (block == 128) {
     if (int8_pv)
-      hipLaunchKernelGGL(int8fwd::fwd_int8_b128_kernel, dim3(grid), dim3(256), blist_lds_bytes(NT), s, q, sq_b, sq_t,
-                         sq_h, qi, qs, ki, ks, vi, vscale, TP, kc, vc, npad, counts, lists, mask,
+      hipLaunchKernelGGL(uniform_ks ? int8fwd::fwd_int8_b128_kernel<true> : int8fwd::fwd_int8_b128_kernel<false>,
+                         dim3(grid), dim3(256), blist_lds_bytes(NT), s, q, sq_b, sq_t, sq_h, qi, qs,
+                         ki, ks, vi, vscale, TP, kc, vc, npad, counts, lists, mask,
                          static_cast<int>(T), static_cast<int>(H), static_cast<int>(NT), W, c, o,
                          so_b, so_t, so_h);
-    else int8fwd::launch_i8<128, false>(SOLATTN_I8_ARGS);
+    else int8fwd::launch_i8_ks<128, false>(uniform_ks, SOLATTN_I8_ARGS);
   } else {
-    if (int8_pv) int8fwd::launch_i8<64, true>(SOLATTN_I8_ARGS);
-    else int8fwd::launch_i8<64, false>(SOLATTN_I8_ARGS);
+    if (int8_pv) int8fwd::launch_i8_ks<64, true>(uniform_ks, SOLATTN_I8_ARGS);
+    else int8fwd::launch_i8_ks<64, false>(uniform_ks, SOLATTN_I8_ARGS);
   }
 #undef SOLATTN_I8_ARGS
   return check_launch("fwd_int8");
+}
+
+}  // namespace solattn
+
+extern "C" int solattn_fwd_int8(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
+                                const int8_t* qi, const float* qs, const int8_t* ki,
+                                const float* ks, const int8_t* vi, const float* vscale,
+                                const uint16_t* v, int64_t sv_b, int64_t sv_t, int64_t sv_h,
+                                int64_t TP, const uint16_t* kc, const uint16_t* vc, int64_t npad,
+                                const int32_t* counts, const int16_t* lists, const uint32_t* mask,
+                                int64_t B, int64_t T, int64_t H, int64_t D, int64_t block,
+                                float scale, int int8_pv, uint16_t* o, int64_t so_b, int64_t so_t,
+                                int64_t so_h, solattn_stream_t stream) {
+  solattn::clear_error();
+  return solattn::fwd_int8(q, sq_b, sq_t, sq_h, qi, qs, ki, ks, vi, vscale, v, sv_b, sv_t, sv_h,
+                           TP, kc, vc, npad, counts, lists, mask, B, T, H, D, block, scale,
+                           int8_pv, o, so_b, so_t, so_h, stream, false);
 }

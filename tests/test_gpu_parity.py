@@ -94,7 +94,10 @@ def test_quant_blocked_bit_exact(pkg, dev, shape, block):
     """Per-128-token-block Q and smoothed-K scales (the config 3 variant) through
     the INT8 preparation: codes and scales bit-exact against the oracle,
     including a ragged last scale block and a head whose block max is planted
-    in one row; the one call feeds the forward the same bits."""
+    in one row. The one call folds each tile's shared K scale into the tile's
+    score factor (one multiply per tile); the composed call through
+    forward_int8 multiplies every score by its key's scale: the two agree up
+    to fp32 rounding, and both against the oracle."""
     fp, i8 = _mods(pkg)[3], _mods(pkg)[2]
     B, T, H = shape
     q, k, v = (randn_bf16((B, T, H, 128), s) for s in (50, 51, 52))  # unit scale, as the
@@ -113,7 +116,10 @@ def test_quant_blocked_bit_exact(pkg, dev, shape, block):
         two = i8.forward_int8(qd, vd, r, qi, qs, ki, ks, vi if pv else None, int8_pv=pv)
         one = i8.sol_attn_int8(qd, kd, vd, tau=0.9, block=block, int8_pv=pv, quant_block=128)
         torch.cuda.synchronize()
-        assert torch.equal(one.view(torch.int16), two.view(torch.int16))
+        diff = (one.float() - two.float()).abs()
+        print(f"  pv={pv}: one call vs composed max|d| {diff.max().item():.3g}, "
+              f"{(diff > 0).float().mean().item():.3%} of outputs differ", flush=True)
+        assert diff.max().item() <= 1e-2
         if pv:
             assert np.array_equal(vi.cpu().numpy(), ref["vi"])
         refp = oracle.prepare(bits(q), bits(k), bits(v), block=block, tau=0.9, int8=True,
