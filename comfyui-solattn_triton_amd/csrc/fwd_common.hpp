@@ -539,14 +539,27 @@ __device__ __forceinline__ void store_rows(const SoftmaxState& st, uint16_t* __r
   const float inv = 1.f / xhalf_sum(st.l);
   if (qrow >= T) return;
   uint16_t* orow = obase + static_cast<int64_t>(qrow) * so_t;
+  // the two lanes of a row swap halves so each writes 16 contiguous bytes
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      uint2 w;
-      w.x = pack_bf16x2(st.acc[dt][4 * i] * inv, st.acc[dt][4 * i + 1] * inv);
-      w.y = pack_bf16x2(st.acc[dt][4 * i + 2] * inv, st.acc[dt][4 * i + 3] * inv);
-      *reinterpret_cast<uint2*>(orow + 32 * dt + 8 * i + 4 * half) = w;
+    for (int ip = 0; ip < 2; ++ip) {
+      uint32_t w[2][2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int i = 2 * ip + u;
+        w[u][0] = pack_bf16x2(st.acc[dt][4 * i] * inv, st.acc[dt][4 * i + 1] * inv);
+        w[u][1] = pack_bf16x2(st.acc[dt][4 * i + 2] * inv, st.acc[dt][4 * i + 3] * inv);
+      }
+      uint32_t y[2];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const uint32_t x = half ? w[0][e] : w[1][e];
+        const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+        y[e] = half ? r[0] : r[1];
+      }
+      const uint4 v = half ? make_uint4(y[0], y[1], w[1][0], w[1][1]) : make_uint4(w[0][0], w[0][1], y[0], y[1]);
+      *reinterpret_cast<uint4*>(orow + 32 * dt + 16 * ip + 8 * half) = v;
     }
 }
 
