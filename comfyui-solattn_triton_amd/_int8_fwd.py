@@ -26,9 +26,9 @@ def sol_attn_int8(q, k, v, *, scale=None, tau=1.0, sink_blocks=(0, 0), sink_q=(0
     ``quant_block=128`` quantises Q and smoothed K with one scale per 128-token
     block instead of per token (an option of this build, BASELINE config 3's
     wording; the default is the reference's per-token rule)."""
-    check_inputs(q, k, v, block)
     if quant_block not in (None, QUANT_BLOCK):
         raise ValueError(f"quant_block must be None or {QUANT_BLOCK}, got {quant_block}")
+    check_inputs(q, k, v, block)
     scale = q.shape[-1] ** -0.5 if scale is None else float(scale)
     q, k, v = as_kernel_input(q), as_kernel_input(k), as_kernel_input(v)
     B, T, H, D = q.shape

@@ -66,6 +66,31 @@ def test_errors_are_reported(capi):
     assert rc == -4 and b"workspace" in L.solattn_last_error()
 
 
+def test_quant_block_variant_rejects_bad_arguments(capi, pkg):
+    """The per-128-token-block INT8 variant: the C entry points refuse a short
+    workspace and a head dim they do not take before any device work, and the
+    Python options accept only quant_block None or 128."""
+    import importlib
+    import torch
+    L = capi.LIB
+    null = None
+    ws = L.solattn_sol_attn_workspace_bytes(1, 1000, 2, 128, 128, 1)
+    rc = L.solattn_sol_attn_int8_qblock(*([null, 0, 0, 0] * 3), 1, 1000, 2, 128, 128, 0.1, 1.0,
+                                        0, 0, 0, 0, 1, null, ws - 1, null, 0, 0, 0, null)
+    assert rc == -4 and b"workspace" in L.solattn_last_error()
+    rc = L.solattn_quant_rows_blocked(null, 0, 0, 0, 1, 100, 1, 64, null, null, null, 100, null)
+    assert rc == -2 and b"head_dim" in L.solattn_last_error()
+    assert capi.QUANT_BLOCK == 128
+    x = torch.zeros(1, 256, 2, 128, dtype=torch.bfloat16)
+    i8 = importlib.import_module(f"{pkg.__name__}._int8_fwd")
+    fp = importlib.import_module(f"{pkg.__name__}._fused_prep")
+    for bad in (64, 256, 0):
+        with pytest.raises(ValueError, match="quant_block"):
+            i8.sol_attn_int8(x, x, x, tau=0.9, quant_block=bad)
+        with pytest.raises(ValueError, match="quant_block"):
+            fp.fused_preprocess_routing(x, x, x, tau=0.9, scale=0.1, quant_block=bad)
+
+
 def test_noalloc_rejects_oversize_before_device_work(capi):
     """The allocation-free pipeline refuses shapes whose intermediates exceed
     its fixed scratch, with SOLATTN_ESIZE, before it touches a device."""
