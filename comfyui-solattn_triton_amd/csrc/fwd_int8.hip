@@ -205,10 +205,12 @@ __device__ __forceinline__ void exact_softmax_pv(SoftmaxState& st, f32x16 (&s)[2
 // the i8 MFMAs of S(n+1) from the K tile kn are interleaved with the softmax
 // of tile n; then P(n).V(n) and the conversion of S(n+1) into sn (ks of tile
 // n+1 from kn).
-template <bool INT8_PV, bool UKS>
+// mid(): called before P(n).V(n) reads the V tile (a single-buffered V tile
+// is waited for there).
+template <bool INT8_PV, bool UKS, typename Mid>
 __device__ __forceinline__ void fast_step(SoftmaxState& st, f32x16 (&sc)[2], f32x16 (&sn)[2],
                                           const char* kn, const void* vt, const i32x4 (&qi)[4],
-                                          float qsl, int lane) {
+                                          float qsl, int lane, Mid&& mid) {
   const int col = lane & 31, half = lane >> 5;
   const i32x16 zero = {};
   i32x16 si[2];
@@ -280,8 +282,10 @@ __device__ __forceinline__ void fast_step(SoftmaxState& st, f32x16 (&sc)[2], f32
   rescale(st, alpha);
   if constexpr (INT8_PV) {
     scale_scores<UKS>(kn, si, half, sn);  // frees the int32 scores before the P.V accumulators
+    mid();
     pv_i8(static_cast<const char*>(vt), pi, beta * (1.f / 127.f), lane, st.acc);
   } else {
+    mid();
     pv_tile(static_cast<const uint16_t*>(vt), pb, lane, st.acc);
     scale_scores<UKS>(kn, si, half, sn);
   }
@@ -353,11 +357,11 @@ __device__ __forceinline__ void issue_i8(uint32_t dst, const int8_t* rows, const
 }
 
 // K and V tiles double buffered. Block 128: 68 KB of LDS, two workgroups per
-// CU, two waves per SIMD. Block 64: packed int8 K tiles; with int8 P.V packed
-// int8 V too (37 KB, four workgroups per CU), with bf16 P.V bf16 V tiles
-// (52 KB, three workgroups per CU: 3.66 -> 3.40 ms at cfg 2 against two
-// workgroups of 68 KB with one wave per SIMD; a single-buffered form spilled in
-// the step loop and ran 1.5x slower).
+// CU, two waves per SIMD. Block 64: packed int8 K tiles, double buffered; with
+// int8 P.V packed int8 V too, double buffered (37 KB, four workgroups per CU),
+// with bf16 P.V one bf16 V tile (VSINGLE: 37 KB, four workgroups per CU, two
+// waves on every SIMD), copied after the step's P.V and waited for before the
+// next one's.
 template <int BLK, bool INT8_PV, bool UKS>
 __global__ void __launch_bounds__(BLK * 2)
 __attribute__((amdgpu_waves_per_eu(2)))
@@ -378,25 +382,30 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
   // int8 P.V, V(0)-V(1)) and the pooled tiles are single buffered.
   constexpr int NBUF = 2;
   constexpr bool COMPACT = BLK == 64;
+  constexpr bool VSINGLE = COMPACT && !INT8_PV;  // one bf16 V tile buffer
+  constexpr int NVBUF = VSINGLE ? 1 : NBUF;
   constexpr int KSTRIDE = COMPACT ? kKsOffset + 256 : static_cast<int>(kTileBytes);
   constexpr int VSTRIDE = COMPACT && INT8_PV ? kKeys * kD : static_cast<int>(kTileBytes);
   constexpr int VBASE = NBUF * KSTRIDE;
   constexpr int PNBUF = COMPACT ? 1 : NBUF;  // buffers for pooled tiles
   static_assert(!COMPACT || (2 * KSTRIDE >= static_cast<int>(kTileBytes) &&
-                             2 * VSTRIDE >= static_cast<int>(kTileBytes)), "pooled tile must fit");
-  __shared__ __align__(256) char arena[VBASE + NBUF * VSTRIDE];
+                             NVBUF * VSTRIDE >= static_cast<int>(kTileBytes)), "pooled tile must fit");
+  // copies per wave of one K tile (rows and ks): VSINGLE waits for the V tile
+  // issued before them with these still in flight
+  constexpr int kKCopies = I8Offsets<NTHREADS>::U + 1;
+  __shared__ __align__(256) char arena[VBASE + NVBUF * VSTRIDE];
   __shared__ TileList tl;
   const auto Kp = [&](int i) { return reinterpret_cast<uint16_t*>(arena + i * KSTRIDE); };
-  const auto Vp = [&](int i) { return reinterpret_cast<uint16_t*>(arena + VBASE + i * VSTRIDE); };
+  const auto Vp = [&](int i) {
+    return reinterpret_cast<uint16_t*>(arena + VBASE + (VSINGLE ? 0 : i) * VSTRIDE);
+  };
   const auto bi = [](int n) { return n & 1; };                      // buffer of exact tile n
   const auto bp = [](int n) { return PNBUF == 2 ? (n & 1) : 0; };   // buffer of pooled tile n
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int col = lane & 31, half = lane >> 5;
   int bh, qb;
-  // Block 64 with bf16 P.V (three workgroups per CU): the 64-dispatch window
-  // measured 14% faster there than the 8192-token (128-dispatch) one.
-  tile_coords_lpt<(BLK == 64 && !INT8_PV) ? 64 : kLptTokens / BLK>(counts, NT, bh, qb);
+  tile_coords_lpt<kLptTokens / BLK>(counts, NT, bh, qb);
   const int b = bh / H, h = bh % H;
   const int64_t row = static_cast<int64_t>(bh) * NT + qb;
 
@@ -425,7 +434,7 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
   };
   const uint32_t kb = lds_addr(arena), vb = kb + VBASE;  // LDS byte addresses
   const auto kbuf_at = [&](int buf) { return kb + buf * KSTRIDE; };
-  const auto vbuf_at = [&](int buf) { return vb + buf * VSTRIDE; };
+  const auto vbuf_at = [&](int buf) { return vb + (VSINGLE ? 0 : buf) * VSTRIDE; };
   const auto issue_exact_full = [&](int n, uint32_t kd, uint32_t vd, bool with_k, bool with_v) {
     const int first = exact_first<BLK>(tl, n - nrag);
     if (with_k) issue_i8<NTHREADS, true, true>(kd, is.ki, is, first, kKeys, ioff.k, ioff.ks, false);
@@ -479,8 +488,14 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
     if (nrag) {
       wait_tile_copies();
       __syncthreads();
-      // a pooled tile 1 does not fit buffer 1 when COMPACT: the pooled phase issues it
-      if (1 < ntiles && (!COMPACT || 1 < nexact)) issue_tile(1, 1);
+      // a pooled tile 1 does not fit buffer 1 when COMPACT: the pooled phase
+      // issues it; VSINGLE: tile 1's V follows the ragged tile's P.V
+      if (1 < ntiles && (!COMPACT || 1 < nexact)) {
+        if constexpr (VSINGLE)
+          issue_exact_full(1, kbuf_at(1), 0u, true, false);
+        else
+          issue_tile(1, 1);
+      }
       const TileDesc td = exact_tile(0);
       i32x16 si[2];
       f32x16 s[2];
@@ -496,6 +511,9 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
       }
       exact_softmax_pv<INT8_PV>(st, s, Vp(0), tile_qsl<UKS>(kt, kKsOffset, qsl), lane);
       __syncthreads();
+      if constexpr (VSINGLE) {
+        if (1 < nexact) issue_exact_full(1, 0u, vbuf_at(0), false, true);
+      }
     }
     // full exact tiles, pipelined (tile F = nrag was issued into buffers bi(F));
     // fa, fb: the score factors of sa, sb
@@ -520,21 +538,39 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
       int n = F;
       // Step n needs n + 1 < E. K(n+2) of the last step is clamped to the
       // last full tile: a redundant copy into a buffer nothing reads afterwards.
+      // VSINGLE: V(n) was copied at the end of step n-1, before this step's
+      // K(n+2); it is waited for before P(n).V(n), and V(n+1) is copied once
+      // every wave is past P(n).V(n).
       const auto step = [&](f32x16 (&sc)[2], float qc, f32x16 (&sn)[2], float& qn) {
         issue_exact_full(min(n + 2, E - 1), kbuf_at(n & 1), 0u, true, false);
-        issue_exact_full(n + 1, 0u, vbuf_at((n + 1) & 1), false, true);
+        if constexpr (!VSINGLE) issue_exact_full(n + 1, 0u, vbuf_at((n + 1) & 1), false, true);
         const char* kn = reinterpret_cast<const char*>(Kp((n + 1) & 1));
-        fast_step<INT8_PV, UKS>(st, sc, sn, kn, Vp(n & 1), qireg, qc, lane);
+        fast_step<INT8_PV, UKS>(st, sc, sn, kn, Vp(n & 1), qireg, qc, lane, [&] {
+          if constexpr (VSINGLE) {
+            wait_vmcnt<kKCopies>();
+            __syncthreads();
+          }
+        });
         qn = tile_qsl<UKS>(kn, kKsOffset, qsl);
         wait_tile_copies();
         __syncthreads();
+        if constexpr (VSINGLE) issue_exact_full(n + 1, 0u, vbuf_at(0), false, true);
         ++n;
       };
       while (n + 2 < E) {
         step(sa, fa, sb, fb);
         step(sb, fb, sa, fa);
       }
-      if (n + 1 < E) {
+      if constexpr (VSINGLE) {
+        const bool odd = n + 1 < E;  // one more step, the last tile's scores in sb
+        if (odd) step(sa, fa, sb, fb);
+        wait_tile_copies();  // V of the last tile
+        __syncthreads();
+        if (odd)
+          exact_softmax_pv<INT8_PV>(st, sb, Vp(bi(n)), fb, lane);
+        else
+          exact_softmax_pv<INT8_PV>(st, sa, Vp(bi(n)), fa, lane);
+      } else if (n + 1 < E) {
         step(sa, fa, sb, fb);
         exact_softmax_pv<INT8_PV>(st, sb, Vp(bi(n)), fb, lane);
       } else {
