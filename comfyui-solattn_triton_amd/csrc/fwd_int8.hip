@@ -359,7 +359,7 @@ __device__ __forceinline__ void issue_i8(uint32_t dst, const int8_t* rows, const
 // K and V tiles double buffered. Block 128: 68 KB of LDS, two workgroups per
 // CU, two waves per SIMD. Block 64: packed int8 K tiles, double buffered; with
 // int8 P.V packed int8 V too, double buffered (37 KB, four workgroups per CU),
-// with bf16 P.V one bf16 V tile (VSINGLE: 37 KB, four workgroups per CU, two
+// with bf16 P.V one bf16 V tile (VSINGLE: 36 KB, four workgroups per CU, two
 // waves on every SIMD), copied after the step's P.V and waited for before the
 // next one's.
 template <int BLK, bool INT8_PV, bool UKS>
