@@ -319,8 +319,13 @@ constexpr int kQB = 8;
 constexpr int kRouteThreads = 256;
 constexpr int kMaxWords = 512;  // NT <= 16384 (the forwards' limit)
 constexpr int kKcStride = kHeadDim + 4;  // bf16 per staged kc row (264 B): conflict-free 8-byte reads
-constexpr int kKcLoads = kHeadDim / 8;   // 16-byte loads per thread to stage 256 kc rows
+// TPR threads score each staged kc row, each against kQB / TPR query blocks:
+// kRouteThreads / TPR rows per chunk (TPR 2: 33 KB of LDS, four workgroups per
+// CU; TPR 4: 17 KB). Against one row per thread (67 KB, two workgroups per
+// CU): 34.8 -> 24.1 us (TPR 2) / 25.6 us (TPR 4) at NT 256 and 83 -> 61 / 58 us
+// at NT 512, same bits; the launch takes TPR 2 up to NT 256, else 4.
 
+template <int TPR>
 __global__ void __launch_bounds__(kRouteThreads)
 route_kernel(const float* __restrict__ qbar, const uint16_t* __restrict__ kc, int64_t npad,
              const float* __restrict__ kc_mean, const float* __restrict__ kc_var, int H, int NT,
@@ -328,19 +333,27 @@ route_kernel(const float* __restrict__ qbar, const uint16_t* __restrict__ kc, in
              int64_t sq_lo, int64_t sq_hi, float* __restrict__ thr_out,
              int32_t* __restrict__ counts, int16_t* __restrict__ lists,
              uint32_t* __restrict__ mask) {
+  constexpr int kRouteRows = kRouteThreads / TPR;  // kc rows staged per chunk
+  constexpr int kQH = kQB / TPR;                   // query blocks per thread
+  constexpr int kKcLoads = kRouteRows * (kHeadDim / 8) / kRouteThreads;  // 16-byte loads per thread
+  static_assert(kRouteRows % 64 == 0 && kQB % TPR == 0, "route tiling");
   const int i0 = blockIdx.x * kQB, h = blockIdx.y, b = blockIdx.z;
   const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
   __shared__ float sthr[kQB];
   // exact bits of the kQB query blocks, W words each, in dynamic LDS
   extern __shared__ __align__(16) uint32_t smask_lds[];
   const auto smask = [&](int i, int w) -> uint32_t& { return smask_lds[i * W + w]; };
-  __shared__ __align__(16) uint16_t skc[kRouteThreads * kKcStride];
+  __shared__ __align__(16) uint16_t skc[kRouteRows * kKcStride];
   const int64_t bh = static_cast<int64_t>(b) * H + h;
   // Query rows past NT (a ragged last workgroup) read row NT-1; nothing of
   // theirs is stored.
-  const float* qrow[kQB];
+  // Threads t, t + kRouteRows, ... score the same kc row, against query blocks
+  // qh*kQH .. +kQH-1 (qh is the same for the whole wave).
+  const int qh = __builtin_amdgcn_readfirstlane(t / kRouteRows);
+  const float* qrow[kQH];
 #pragma unroll
-  for (int i = 0; i < kQB; ++i) qrow[i] = qbar + (bh * NT + min(i0 + i, NT - 1)) * kHeadDim;
+  for (int i = 0; i < kQH; ++i)
+    qrow[i] = qbar + (bh * NT + min(i0 + qh * kQH + i, NT - 1)) * kHeadDim;
   for (int e = t; e < kQB * W; e += kRouteThreads) smask_lds[e] = 0u;
   if (wave == 0) {
     // Lane i < kQB: the threshold of query block i0 + i, one fma chain per
@@ -385,9 +398,10 @@ route_kernel(const float* __restrict__ qbar, const uint16_t* __restrict__ kc, in
     }
   }
 
-  for (int j0 = 0; j0 < NT; j0 += kRouteThreads) {
-    // Stage kc rows j0 .. j0+255 (coalesced 16-byte loads, all issued before
-    // the LDS stores; rows past NT are 0), then thread t scores row t.
+  for (int j0 = 0; j0 < NT; j0 += kRouteRows) {
+    // Stage kc rows j0 .. j0+kRouteRows-1 (coalesced 16-byte loads, all issued
+    // before the LDS stores; rows past NT are 0), then the TPR threads
+    // t = r (mod kRouteRows) score row r.
     {
       uint4 v[kKcLoads];
 #pragma unroll
@@ -412,12 +426,13 @@ route_kernel(const float* __restrict__ qbar, const uint16_t* __restrict__ kc, in
       }
     }
     __syncthreads();  // (the first one also publishes the thresholds)
-    const int j = j0 + t;
+    const int rr = t % kRouteRows;
+    const int j = j0 + rr;
     const bool active = j < NT;
-    float acc[kQB];
+    float acc[kQH];
 #pragma unroll
-    for (int i = 0; i < kQB; ++i) acc[i] = 0.f;
-    const uint16_t* krow = &skc[t * kKcStride];
+    for (int i = 0; i < kQH; ++i) acc[i] = 0.f;
+    const uint16_t* krow = &skc[rr * kKcStride];
     // The query centroids are the same for every lane: scalar loads, so each
     // fma takes its q operand from an SGPR.
 #pragma unroll 2
@@ -426,7 +441,7 @@ route_kernel(const float* __restrict__ qbar, const uint16_t* __restrict__ kc, in
       const float k0 = lo_bf16(kw.x), k1 = hi_bf16(kw.x);
       const float k2 = lo_bf16(kw.y), k3 = hi_bf16(kw.y);
 #pragma unroll
-      for (int i = 0; i < kQB; ++i) {
+      for (int i = 0; i < kQH; ++i) {
         const float4 qv = *reinterpret_cast<const float4*>(qrow[i] + 4 * d4);
         acc[i] = fmaf(qv.x, k0, acc[i]);
         acc[i] = fmaf(qv.y, k1, acc[i]);
@@ -435,19 +450,20 @@ route_kernel(const float* __restrict__ qbar, const uint16_t* __restrict__ kc, in
       }
     }
     const bool in_skv = j >= skv_lo && j < skv_hi;
+    const int w0 = (j0 + (rr & ~63)) >> 5;  // this wave's 64 rows
 #pragma unroll
-    for (int i = 0; i < kQB; ++i) {
-      const int qi = i0 + i;
+    for (int i = 0; i < kQH; ++i) {
+      const int il = qh * kQH + i;
+      const int qi = i0 + il;
       const float r = acc[i] * c;
       const int dij = qi > j ? qi - j : j - qi;
       const bool q_in_sink = qi >= sq_lo && qi < sq_hi;
-      const bool routed = (r > sthr[i]) || dij <= 1 || in_skv;
+      const bool routed = (r > sthr[il]) || dij <= 1 || in_skv;
       const bool exact = active && qi < NT && (q_in_sink || routed);
       const uint64_t bal = __ballot(exact);
-      const int w0 = (j0 + wave * 64) >> 5;
       if (lane == 0 && w0 < W) {
-        smask(i, w0) = static_cast<uint32_t>(bal);
-        if (w0 + 1 < W) smask(i, w0 + 1) = static_cast<uint32_t>(bal >> 32);
+        smask(il, w0) = static_cast<uint32_t>(bal);
+        if (w0 + 1 < W) smask(il, w0 + 1) = static_cast<uint32_t>(bal >> 32);
       }
     }
   }
@@ -608,7 +624,7 @@ extern "C" int solattn_route(const float* qbar, const uint16_t* kc, int64_t npad
   const float c2 = c * c;
   dim3 grid(static_cast<uint32_t>(cdiv(NT, kQB)), static_cast<uint32_t>(H),
             static_cast<uint32_t>(B));
-  hipLaunchKernelGGL(route_kernel, grid, dim3(kRouteThreads),
+  hipLaunchKernelGGL(NT <= 256 ? route_kernel<2> : route_kernel<4>, grid, dim3(kRouteThreads),
                      static_cast<size_t>(kQB * W * sizeof(uint32_t)),
                      reinterpret_cast<hipStream_t>(stream), qbar, kc, npad,
                      mode == 0 ? kc_mean : kc_var, kc_var, static_cast<int>(H),
