@@ -239,17 +239,18 @@ int run_int8_pipeline(const Layout& L, void* ws, const Call& call, int int8_pv,
                    c.v, c.sv_b, c.sv_t, c.sv_h, c.B, c.T, c.H, c.D, at<float>(ws, L.kc_mean),
                    vscale, at<int8_t>(ws, L.qi), at<float>(ws, L.qs), at<int8_t>(ws, L.ki),
                    at<float>(ws, L.ks), int8_pv ? at<int8_t>(ws, L.vi) : nullptr, L.TP, hs,
-                   qk_block);
+                   qk_block, /*ks_head_major=*/1);
     if (rc) return rc;
     // per block, every 64-key tile of K shares one scale: the forward folds it
-    // into the tile's score factor
+    // into the tile's score factor. K's scales are kept head-major here, so a
+    // tile's 64 scales are one contiguous 256-byte read.
     return fwd_int8(c.q, c.sq_b, c.sq_t, c.sq_h, at<int8_t>(ws, L.qi), at<float>(ws, L.qs),
                     at<int8_t>(ws, L.ki), at<float>(ws, L.ks),
                     int8_pv ? at<int8_t>(ws, L.vi) : nullptr, vscale, c.v, c.sv_b, c.sv_t, c.sv_h,
                     L.TP, at<uint16_t>(ws, L.kc), at<uint16_t>(ws, L.vc), L.npad,
                     at<int32_t>(ws, L.counts), at<int16_t>(ws, L.lists), at<uint32_t>(ws, L.mask),
                     c.B, c.T, c.H, c.D, c.block, c.scale, int8_pv, c.o, c.so_b, c.so_t, c.so_h,
-                    stream, qk_block != 0);
+                    stream, qk_block != 0, /*ks_head_major=*/true);
   });
 }
 

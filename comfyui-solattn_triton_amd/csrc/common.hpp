@@ -77,16 +77,19 @@ int pad_heads(const uint16_t* src, int64_t s_b, int64_t s_t, int64_t s_h, uint16
 // Per-token INT8 of q (skipped when q is null) and of k smoothed by k_mean,
 // and (vscale != null) per-channel INT8 of v, in one launch (quant.hip); same
 // codes and scales as solattn_quant_rows / solattn_quant_v (qk_block: q and k
-// as solattn_quant_rows_blocked).
+// as solattn_quant_rows_blocked); ks_head_major: k's scales laid out [B, H, TP]
+// instead of [B, TP, H].
 int quant_qkv(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h, const uint16_t* k,
               int64_t sk_b, int64_t sk_t, int64_t sk_h, const uint16_t* v, int64_t sv_b,
               int64_t sv_t, int64_t sv_h, int64_t B, int64_t T, int64_t H, int64_t D,
               const float* k_mean, const float* vscale, int8_t* qi, float* qs, int8_t* ki,
-              float* ks, int8_t* vi, int64_t TP, hipStream_t stream, int qk_block = 0);
+              float* ks, int8_t* vi, int64_t TP, hipStream_t stream, int qk_block = 0,
+              int ks_head_major = 0);
 
 // solattn_fwd_int8 without clearing the error slot; uniform_ks: every 64-key
 // tile of K shares one scale (K quantised per 128-token block), so the
-// kernels multiply it once per tile instead of once per score.
+// kernels multiply it once per tile instead of once per score; ks_head_major:
+// ks laid out [B, H, TP] (a tile's 64 scales contiguous) instead of [B, TP, H].
 int fwd_int8(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h, const int8_t* qi,
              const float* qs, const int8_t* ki, const float* ks, const int8_t* vi,
              const float* vscale, const uint16_t* v, int64_t sv_b, int64_t sv_t, int64_t sv_h,
@@ -94,6 +97,6 @@ int fwd_int8(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h, const 
              const int32_t* counts, const int16_t* lists, const uint32_t* mask, int64_t B,
              int64_t T, int64_t H, int64_t D, int64_t block, float scale, int int8_pv,
              uint16_t* o, int64_t so_b, int64_t so_t, int64_t so_h, solattn_stream_t stream,
-             bool uniform_ks);
+             bool uniform_ks, bool ks_head_major = false);
 
 }  // namespace solattn

@@ -294,10 +294,10 @@ __device__ __forceinline__ void fast_step(SoftmaxState& st, f32x16 (&sc)[2], f32
 // ------------------------------------------------------------------ copies
 struct I8Source {
   const int8_t* ki;  // rows of this batch/head, stride srow bytes
-  const float* ks;   // stride H floats
+  const float* ks;   // this head's scales, kst floats from token to token
   const int8_t* vi;
   int64_t srow;
-  int H;
+  int kst;
 };
 
 // Per-lane byte offsets of this lane's 16-byte chunk of an int8 tile (copy u
@@ -306,13 +306,13 @@ template <int NTHREADS>
 struct I8Offsets {
   static constexpr int U = kKeys * 8 / NTHREADS;  // copies per lane per int8 tile
   static constexpr int kKsPerWave = kKeys / (NTHREADS / 64);
-  uint32_t k, v, ks;  // ks: this lane's key of the tile (waves copy kKsPerWave each) x H x 4
-  __device__ __forceinline__ void init(int64_t srow, int H) {
+  uint32_t k, v, ks;  // ks: this lane's key of the tile (waves copy kKsPerWave each) x kst x 4
+  __device__ __forceinline__ void init(int64_t srow, int kst) {
     const int row = threadIdx.x >> 3, pc = threadIdx.x & 7;
     k = static_cast<uint32_t>(row * srow + swz_ki(row, pc) * 16);
     v = static_cast<uint32_t>(row * srow + swz_vi(row, pc) * 16);
     const int key = kKsPerWave * (threadIdx.x >> 6) + (threadIdx.x & 63);
-    ks = static_cast<uint32_t>(key * H * 4);
+    ks = static_cast<uint32_t>(key * kst * 4);
   }
 };
 
@@ -346,11 +346,11 @@ __device__ __forceinline__ void issue_i8(uint32_t dst, const int8_t* rows, const
     if (lane < kpw) {
       const uint32_t d = l0 + kKsOffset + 4 * kpw * wave;
       if constexpr (FULL) {
-        g2l4_s(is.ks + static_cast<int64_t>(first) * is.H, ks_off, d);
+        g2l4_s(is.ks + static_cast<int64_t>(first) * is.kst, ks_off, d);
       } else {
         const int key = kpw * wave + lane;
         const int r = key < nvalid ? key : 0;
-        g2l4(is.ks + static_cast<int64_t>(first + r) * is.H, d);
+        g2l4(is.ks + static_cast<int64_t>(first + r) * is.kst, d);
       }
     }
   }
@@ -373,7 +373,8 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
                 int64_t TP, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
                 int64_t npad, const int32_t* __restrict__ counts, const int16_t* __restrict__ lists,
                 const uint32_t* __restrict__ mask, int T, int H, int NT, int W, float c,
-                uint16_t* __restrict__ o, int64_t so_b, int64_t so_t, int64_t so_h) {
+                uint16_t* __restrict__ o, int64_t so_b, int64_t so_t, int64_t so_h, int kst,
+                int64_t ksh) {
   constexpr int NTHREADS = BLK * 2;
   // LDS: exact-tile buffers K(i), V(i), i < 2. COMPACT (block 64): the int8
   // tiles are packed (K + its ks: 8448 B; int8 V: 8192 B), so with int8 P.V two
@@ -419,11 +420,11 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
   const KVSource src{nullptr, 0, v + b * sv_b + h * sv_h, sv_t, kc + bhD,
                      static_cast<int64_t>(H) * kD, vc + bhD};
   const I8Source is{ki + (static_cast<int64_t>(b) * TP * H + h) * kD,
-                    ks + static_cast<int64_t>(b) * TP * H + h,
+                    ks + static_cast<int64_t>(b) * TP * H + h * ksh,
                     vi + (static_cast<int64_t>(b) * TP * H + h) * kD,
-                    static_cast<int64_t>(H) * kD, H};
+                    static_cast<int64_t>(H) * kD, kst};
   I8Offsets<NTHREADS> ioff;
-  ioff.init(is.srow, H);
+  ioff.init(is.srow, kst);
   CopyOffsets<NTHREADS> boff;
   boff.init(0, sv_t);
 
@@ -645,7 +646,7 @@ __device__ __forceinline__ void issue_blk(uint32_t dst, const int8_t* rows, cons
   }
   if constexpr (KS) {
     if ((threadIdx.x & 63) < 32)
-      g2l4_s(is.ks + static_cast<int64_t>(first) * is.H, ks_off, dst + kBlkKsOffset + 128 * wave);
+      g2l4_s(is.ks + static_cast<int64_t>(first) * is.kst, ks_off, dst + kBlkKsOffset + 128 * wave);
   }
 }
 
@@ -784,7 +785,7 @@ fwd_int8_b128_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t,
                      int64_t npad, const int32_t* __restrict__ counts,
                      const int16_t* __restrict__ lists, const uint32_t* __restrict__ mask, int T,
                      int H, int NT, int W, float c, uint16_t* __restrict__ o, int64_t so_b,
-                     int64_t so_t, int64_t so_h) {
+                     int64_t so_t, int64_t so_h, int kst, int64_t ksh) {
   constexpr int BLK = 128, NTHREADS = 256;
   __shared__ __align__(256) char arena[2 * kBlkKStride + 2 * kBlkVStride];
   __shared__ TileList tl;
@@ -809,12 +810,12 @@ fwd_int8_b128_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t,
   const int64_t bhD = (static_cast<int64_t>(b) * npad * H + h) * kD;
   const KVSource src{nullptr, 0, nullptr, 0, kc + bhD, static_cast<int64_t>(H) * kD, vc + bhD};
   const I8Source is{ki + (static_cast<int64_t>(b) * TP * H + h) * kD,
-                    ks + static_cast<int64_t>(b) * TP * H + h,
+                    ks + static_cast<int64_t>(b) * TP * H + h * ksh,
                     vi + (static_cast<int64_t>(b) * TP * H + h) * kD,
-                    static_cast<int64_t>(H) * kD, H};
+                    static_cast<int64_t>(H) * kD, kst};
   I8Offsets<NTHREADS> ioff;
-  ioff.init(is.srow, H);
-  const uint32_t ks_blk = static_cast<uint32_t>((32 * wave + lane) * H * 4);
+  ioff.init(is.srow, kst);
+  const uint32_t ks_blk = static_cast<uint32_t>((32 * wave + lane) * kst * 4);
   const uint32_t kb = lds_addr(arena);
   const auto kbuf_at = [&](int i) { return kb + i * kBlkKStride; };
   const auto vbuf_at = [&](int i) { return kb + 2 * kBlkKStride + i * kBlkVStride; };
@@ -956,10 +957,10 @@ void launch_i8(uint32_t grid, hipStream_t s, const uint16_t* q, int64_t sq_b, in
                int64_t sv_t, int64_t sv_h, int64_t TP, const uint16_t* kc, const uint16_t* vc,
                int64_t npad, const int32_t* counts, const int16_t* lists, const uint32_t* mask,
                int T, int H, int NT, int W, float c, uint16_t* o, int64_t so_b, int64_t so_t,
-               int64_t so_h) {
+               int64_t so_h, int kst, int64_t ksh) {
   hipLaunchKernelGGL((fwd_int8_kernel<BLK, PV, UKS>), dim3(grid), dim3(BLK * 2), blist_lds_bytes(NT), s, q, sq_b, sq_t,
                      sq_h, qi, qs, ki, ks, vi, vscale, v, sv_b, sv_t, sv_h, TP, kc, vc, npad,
-                     counts, lists, mask, T, H, NT, W, c, o, so_b, so_t, so_h);
+                     counts, lists, mask, T, H, NT, W, c, o, so_b, so_t, so_h, kst, ksh);
 }
 
 template <int BLK, bool PV>
@@ -969,10 +970,10 @@ void launch_i8_ks(bool uks, uint32_t grid, hipStream_t s, const uint16_t* q, int
                   int64_t sv_b, int64_t sv_t, int64_t sv_h, int64_t TP, const uint16_t* kc,
                   const uint16_t* vc, int64_t npad, const int32_t* counts, const int16_t* lists,
                   const uint32_t* mask, int T, int H, int NT, int W, float c, uint16_t* o,
-                  int64_t so_b, int64_t so_t, int64_t so_h) {
+                  int64_t so_b, int64_t so_t, int64_t so_h, int kst, int64_t ksh) {
   (uks ? launch_i8<BLK, PV, true> : launch_i8<BLK, PV, false>)(
       grid, s, q, sq_b, sq_t, sq_h, qi, qs, ki, ks, vi, vscale, v, sv_b, sv_t, sv_h, TP, kc, vc,
-      npad, counts, lists, mask, T, H, NT, W, c, o, so_b, so_t, so_h);
+      npad, counts, lists, mask, T, H, NT, W, c, o, so_b, so_t, so_h, kst, ksh);
 }
 
 }  // namespace int8fwd
@@ -984,7 +985,7 @@ int fwd_int8(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h, const 
              const int32_t* counts, const int16_t* lists, const uint32_t* mask, int64_t B,
              int64_t T, int64_t H, int64_t D, int64_t block, float scale, int int8_pv,
              uint16_t* o, int64_t so_b, int64_t so_t, int64_t so_h, solattn_stream_t stream,
-             bool uniform_ks) {
+             bool uniform_ks, bool ks_head_major) {
   if (int rc = check_fwd_common(q, sq_b, sq_t, sq_h, kc, vc, npad, counts, lists, mask, B, T, H, D,
                                 block, o, so_b, so_t, so_h, "fwd_int8"))
     return rc;
@@ -1008,17 +1009,20 @@ int fwd_int8(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h, const 
   const float c = scale * kLog2e;
   const uint32_t grid = static_cast<uint32_t>(B * H * NT);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  // ks: token-major [B, TP, H] (the reference's) or head-major [B, H, TP]
+  const int kst = ks_head_major ? 1 : static_cast<int>(H);
+  const int64_t ksh = ks_head_major ? TP : 1;
 #define SOLATTN_I8_ARGS                                                                          \
   grid, s, q, sq_b, sq_t, sq_h, qi, qs, ki, ks, vi, vscale, v, sv_b, sv_t, sv_h, TP, kc, vc, npad, \
       counts, lists, mask, static_cast<int>(T), static_cast<int>(H), static_cast<int>(NT), W, c, o, \
-      so_b, so_t, so_h
+      so_b, so_t, so_h, kst, ksh
   if (block == 128) {
     if (int8_pv)
       hipLaunchKernelGGL(uniform_ks ? int8fwd::fwd_int8_b128_kernel<true> : int8fwd::fwd_int8_b128_kernel<false>,
                          dim3(grid), dim3(256), blist_lds_bytes(NT), s, q, sq_b, sq_t, sq_h, qi, qs,
                          ki, ks, vi, vscale, TP, kc, vc, npad, counts, lists, mask,
                          static_cast<int>(T), static_cast<int>(H), static_cast<int>(NT), W, c, o,
-                         so_b, so_t, so_h);
+                         so_b, so_t, so_h, kst, ksh);
     else int8fwd::launch_i8_ks<128, false>(uniform_ks, SOLATTN_I8_ARGS);
   } else {
     if (int8_pv) int8fwd::launch_i8_ks<64, true>(uniform_ks, SOLATTN_I8_ARGS);

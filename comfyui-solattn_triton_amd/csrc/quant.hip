@@ -34,8 +34,12 @@ struct QuantTensor {
   const float* mean;      // [B, H, D] smoothing mean, or null
   const float* vscale;    // [B, H, D] per-channel scale (V rule), or null
   int8_t* xi;             // [B, TP, H, D]
-  float* xs;              // [B, TP, H] per-token scales (not written by the V rule)
+  float* xs;              // per-token scales (not written by the V rule)
   int block_scale;        // per-token rule with one scale per kQuantTok-token block
+  // element strides of xs within a batch's TP*H scales: token-major [B, TP, H]
+  // (xs_st = H, xs_sh = 1, as the reference's) or head-major [B, H, TP]
+  // (xs_st = 1, xs_sh = TP, the INT8 call's own K scales)
+  int64_t xs_st, xs_sh;
 };
 
 struct QuantArgs {
@@ -124,7 +128,8 @@ __device__ __forceinline__ void quant_rows_of(const QuantTensor& A, uint32_t T, 
     if (t < T) {
       const int64_t row = (static_cast<int64_t>(b) * TP + t) * H + h;
       *reinterpret_cast<uint2*>(A.xi + row * kQD + c8) = o;
-      if (!PER_CHANNEL && (threadIdx.x & 15) == 0) A.xs[row] = ss;
+      if (!PER_CHANNEL && (threadIdx.x & 15) == 0)
+        A.xs[static_cast<int64_t>(b) * TP * H + t * A.xs_st + h * A.xs_sh] = ss;
     }
   }
 }
@@ -175,7 +180,7 @@ int launch_quant(const uint16_t* x, int64_t sx_b, int64_t sx_t, int64_t sx_h, in
                  int64_t T, int64_t H, int64_t D, const float* mean, const float* vscale,
                  int8_t* xi, float* xs, int64_t TP, hipStream_t stream, const char* what,
                  int block_scale = 0) {
-  const QuantTensor t{x, sx_b, sx_t, sx_h, mean, vscale, xi, xs, block_scale};
+  const QuantTensor t{x, sx_b, sx_t, sx_h, mean, vscale, xi, xs, block_scale, H, 1};
   return launch_quant3(&t, 1, B, T, H, D, TP, stream, what);
 }
 
@@ -183,12 +188,14 @@ int quant_qkv(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h, const
               int64_t sk_b, int64_t sk_t, int64_t sk_h, const uint16_t* v, int64_t sv_b,
               int64_t sv_t, int64_t sv_h, int64_t B, int64_t T, int64_t H, int64_t D,
               const float* k_mean, const float* vscale, int8_t* qi, float* qs, int8_t* ki,
-              float* ks, int8_t* vi, int64_t TP, hipStream_t stream, int qk_block) {
+              float* ks, int8_t* vi, int64_t TP, hipStream_t stream, int qk_block,
+              int ks_head_major) {
   QuantTensor ts[3];
   int n = 0;
-  if (q) ts[n++] = {q, sq_b, sq_t, sq_h, nullptr, nullptr, qi, qs, qk_block};
-  ts[n++] = {k, sk_b, sk_t, sk_h, k_mean, nullptr, ki, ks, qk_block};
-  if (vscale) ts[n++] = {v, sv_b, sv_t, sv_h, nullptr, vscale, vi, nullptr, 0};
+  if (q) ts[n++] = {q, sq_b, sq_t, sq_h, nullptr, nullptr, qi, qs, qk_block, H, 1};
+  ts[n++] = {k, sk_b, sk_t, sk_h, k_mean, nullptr, ki, ks, qk_block, ks_head_major ? 1 : H,
+             ks_head_major ? TP : 1};
+  if (vscale) ts[n++] = {v, sv_b, sv_t, sv_h, nullptr, vscale, vi, nullptr, 0, H, 1};
   return launch_quant3(ts, n, B, T, H, D, TP, stream, "quant_qkv");
 }
 
