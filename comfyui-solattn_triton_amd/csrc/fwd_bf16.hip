@@ -258,15 +258,27 @@ fwd_bf16_sbuf_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t,
   SoftmaxState st;
   st.init();
 
-  // ---- plain tiles (pooled, ragged)
+  // ---- plain tiles (pooled, ragged). The next tile's K is copied once
+  // every wave has its scores (it lands during the softmax and P.V), its V
+  // once every wave is done with P.V (it lands during the next QK).
+  const auto issue_tile_kv = [&](int n, int kv) {
+    if (n >= nplain) {
+      if (kv == 0) issue_k(n); else issue_v(n);
+    } else {
+      issue_generic<NTHREADS>(kv == 0 ? kb : vb, kv, desc<BLK>(tl, n, nrag, T, NT), src);
+    }
+  };
   for (int n = 0; n < nplain; ++n) {
-    wait_tile_copies();
+    wait_vmcnt<CopyOffsets<NTHREADS>::U>();  // K(n); V(n) may be in flight
     __syncthreads();
     f32x16 s[2];
     qk_tile(kl, qreg, s);
+    wait_tile_copies();  // V(n)
+    __syncthreads();     // every wave is done with K(n)
+    if (n + 1 < ntiles) issue_tile_kv(n + 1, 0);
     finish_tile<BLK>(st, s, vl, desc<BLK>(tl, n, nrag, T, NT), c, lane, NT, T);
-    __syncthreads();
-    if (n + 1 < ntiles) issue_tile(n + 1);
+    __syncthreads();     // every wave is done with V(n)
+    if (n + 1 < ntiles) issue_tile_kv(n + 1, 1);
   }
 
   // ---- full exact tiles, pipelined; tile F was issued. K(n+2) past the last
