@@ -94,83 +94,99 @@ __device__ __forceinline__ void fast_step(SoftmaxState& st, f32x16 (&sc)[2], f32
 // the P(n-1) V(n-1) products; P(n) V(n) is left to the next step. QK = false
 // drops the score product (last tile), PV = false the value product (first).
 // The two key halves of S(n+1) accumulate alternately (MFMA i adds channel
-// chunk i/2 to half i%2), so consecutive score MFMAs are independent: with the
-// halves one after the other (each a chain of 8) the loop ran 1.3-2% slower,
-// same bits. The softmax turns S(n) into P(n) during the first half of the
-// step. kl, vl: this lane's operand addresses (k_lane, v_lane) in K(n+1) and
-// V(n-1).
-// LAZY (every step after the first, whose running max is finite): the exps of
-// S(n) use the running max as it stands, and the tile's max is taken only when
-// a lane's row sum exceeds 255. No sum above 255 means every p <= 255, i.e.
-// every score is below the running max + log2(255.5) < kMaxSlack, so the
-// tile would not have moved the max: the running max, and so every bit of the
-// output, evolves as with the max taken every step.
-template <bool QK, bool PV, bool LAZY = false>
+// chunk i/2 to half i%2), so consecutive score MFMAs are independent (with the
+// halves one after the other, each a chain of 8, the loop ran 1.3-2% slower).
+// kl, vl: this lane's operand addresses (k_lane, v_lane) in K(n+1) and V(n-1).
+// The step is one hand-ordered stream (fwd_common.hpp: mfma_v*, exp_pair):
+// slot i (16 per step) issues the MFMA of score chunk i, the exps of P(n)
+// word i (two scores of S(n)), then the MFMA of P.V operand i; the K and V
+// operands of slot i + 2 are read at the top of slot i (the empty asm with a
+// memory clobber keeps the reads there, so each has two slots to land).
+// Measured on a stand-alone copy of the loop: 1346 against 1250 TFLOP/s, the
+// compiler's order having issued the MFMAs four at a time with the softmax
+// between the groups.
+// Lazy tile max: the exps use the running max as it stands, and the tile's max
+// is taken only when a lane's row sum exceeds 255. No sum above 255 means every
+// p <= 255, i.e. every score is below the running max + log2(255.5) <
+// kMaxSlack, so the tile would not have moved the max: the running max evolves
+// as with the max taken every step. The first exact tile of a workgroup
+// (running max -inf, p = inf) always takes that path.
+template <bool QK, bool PV>
 __device__ __forceinline__ void step3(SoftmaxState& st, const f32x16 (&sc)[2], f32x16 (&sn)[2],
                                       const bf16x8 (&pp)[4], bf16x8 (&pn)[4], uint32_t kl,
                                       uint32_t vl, const bf16x8 (&q)[8], float c) {
   static_assert(kMaxSlack >= 8.f, "the lazy test relies on 255 < 2^kMaxSlack");
-  const f32x16 zero = {};
-  constexpr int LK = 2, LV = 2;
-  bf16x8 ka[16], va[16];
+  bf16x8 ka[3], va[3];
+  uint32_t pw[4][4];
+  float psum = 0.f;
+  const float neg = -st.m;
   if constexpr (QK) {
-#pragma unroll
-    for (int i = 0; i < LK; ++i) ka[i] = k_op_x(kl, i & 1, i >> 1);
+    ka[0] = k_op_x(kl, 0, 0);
+    ka[1] = k_op_x(kl, 1, 0);
   }
   if constexpr (PV) {
-#pragma unroll
-    for (int i = 0; i < LV; ++i) va[i] = v_op_x(vl, i >> 2, i & 3);
+    va[0] = v_op_x(vl, 0, 0);
+    va[1] = v_op_x(vl, 0, 1);
   }
-  float mx = -INFINITY, alpha = 1.f, neg = LAZY ? -st.m : 0.f, psum = 0.f;
+  asm volatile("" ::: "memory");
+  const auto unit = [&](int i) {
+    const int ks = i >> 2, w = i & 3;
+    const int r = 8 * (ks & 1) + 2 * w;
+    pw[ks][w] = exp_pair(sc[ks >> 1][r], sc[ks >> 1][r + 1], c, neg, psum);
+  };
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
+    if (i + 2 < 16) {
+      if constexpr (QK) ka[(i + 2) % 3] = k_op_x(kl, (i + 2) & 1, (i + 2) >> 1);
+      if constexpr (PV) va[(i + 2) % 3] = v_op_x(vl, (i + 2) >> 2, (i + 2) & 3);
+      asm volatile("" ::: "memory");
+    }
     if constexpr (QK) {
-      if (i + LK < 16) ka[i + LK] = k_op_x(kl, (i + LK) & 1, (i + LK) >> 1);
-      sn[i & 1] = mfma_bf16(ka[i], q[i >> 1], i < 2 ? zero : sn[i & 1]);
+      // the two key halves of S(n+1) alternate (consecutive MFMAs independent)
+      if (i < 2)
+        mfma_v0(sn[i & 1], ka[i % 3], q[i >> 1]);
+      else
+        mfma_v(sn[i & 1], ka[i % 3], q[i >> 1]);
+      unit(i);
     }
     if constexpr (PV) {
-      if (i + LV < 16) va[i + LV] = v_op_x(vl, (i + LV) >> 2, (i + LV) & 3);
-      st.acc[i & 3] = mfma_bf16(va[i], pp[i >> 2], st.acc[i & 3]);
+      if (i == 0)
+        mfma_v_first(st.acc[0], va[0], pp[0]);
+      else if (QK && i == 15)
+        mfma_v_tie(st.acc[3], va[0], pp[3], sn);  // va[15 % 3]
+      else
+        mfma_v(st.acc[i & 3], va[i % 3], pp[i >> 2]);
     }
-    if (LAZY && i < 4) {
-      // nothing: the running max stands
-    } else if (i < 4) {
-#pragma unroll
-      for (int r = 0; r < 8; ++r) mx = fmaxf(mx, sc[i >> 1][8 * (i & 1) + r]);
-      if (i == 3) {
-        st.m = new_max(st.m, xhalf_max(mx) * c, alpha);
-        neg = -st.m;
-      }
-    } else if (i < 8) {
-      // P(n) chunk i - 4; the empty asm keeps the exps in this slot (left
-      // alone, the compiler sinks them to P(n)'s first use in the next step
-      // and S(n) stays live through this one).
-      const int k = i - 4;
-      psum = k & 1 ? exp8<8>(sc[k >> 1], c, neg, pn[k], psum) : exp8<0>(sc[k >> 1], c, neg, pn[k], psum);
-      asm volatile("" : "+v"(pn[k]), "+v"(psum));
-      if (LAZY && k == 3 && __any(!(psum <= 255.f))) {  // (also catches inf / NaN)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaxf(sc[0][r], sc[1][r]));
-        const float m_new = new_max(st.m, xhalf_max(mx) * c, alpha);
-        if (__any(m_new != st.m)) {  // lanes whose max stays recompute the same P
-          st.m = m_new;
-          neg = -m_new;
-          psum = 0.f;
-          psum = exp8<0>(sc[0], c, neg, pn[0], psum);
-          psum = exp8<8>(sc[0], c, neg, pn[1], psum);
-          psum = exp8<0>(sc[1], c, neg, pn[2], psum);
-          psum = exp8<8>(sc[1], c, neg, pn[3], psum);
-        }
-      }
-    }
+    if constexpr (!QK) unit(i);
     // Raised wave priority for the rest of the step: the issue arbiter then
     // prefers a wave inside its MFMA stream over one at its copies / barrier
     // (about 1-2% at cfg 2).
     if (i == 0) __builtin_amdgcn_s_setprio(1);
   }
   __builtin_amdgcn_s_setprio(0);
+  if constexpr (QK && !PV) mfma_fence(sn);
+  if constexpr (!QK) mfma_fence(st.acc);  // the plain path's builtin MFMAs follow
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+    pn[ks] = __builtin_bit_cast(bf16x8, make_uint4(pw[ks][0], pw[ks][1], pw[ks][2], pw[ks][3]));
+  float alpha = 1.f;
+  if (__any(!(psum <= 255.f))) {  // (also catches inf / NaN)
+    float mx = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaxf(sc[0][r], sc[1][r]));
+    const float m_new = new_max(st.m, xhalf_max(mx) * c, alpha);
+    if (__any(m_new != st.m)) {  // lanes whose max stays recompute the same P
+      st.m = m_new;
+      psum = 0.f;
+      psum = exp8_f32sum<0>(sc[0], c, -m_new, pn[0], psum);
+      psum = exp8_f32sum<8>(sc[0], c, -m_new, pn[1], psum);
+      psum = exp8_f32sum<0>(sc[1], c, -m_new, pn[2], psum);
+      psum = exp8_f32sum<8>(sc[1], c, -m_new, pn[3], psum);
+      if constexpr (PV) mfma_fence(st.acc);  // the rescale reads O
+      rescale(st, alpha);
+    }
+  }
   st.l = fmaf(st.l, alpha, psum);
-  rescale(st, alpha);
 }
 
 // Tile n of this kernel's order: pooled tiles, the ragged exact tile (if
@@ -440,6 +456,7 @@ fwd_bf16_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
     wait_tile_copies();
     __syncthreads();
     qk_tile(kl0, qreg, sa);
+    mfma_fence(sa);   // the step's softmax reads S(0) through asm
     __syncthreads();  // every wave is done with K(0)
     {
       const int E = npipe;
@@ -457,7 +474,7 @@ fwd_bf16_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
                              bf16x8 (&pn)[4]) {
         issue_k_at(kf, n & 1);  // K(min(n + 2, E - 1))
         issue_v_at(vf, n & 1);  // V(n)
-        step3<true, true, true>(st, sc, sn, pp, pn, kl0 + ((n + 1) & 1) * kTileBytes,
+        step3<true, true>(st, sc, sn, pp, pn, kl0 + ((n + 1) & 1) * kTileBytes,
                                 vl0 + ((n - 1) & 1) * kTileBytes, qreg, c);
         // after the MFMA stream, so the read's latency overlaps the copy wait
         // and the barrier below rather than delaying this step's first MFMAs
@@ -475,7 +492,7 @@ fwd_bf16_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
         pbuf = (n - 1) & 1;
         issue_v_at(vf, n & 1);  // V(n)
         if (nplain > 0) issue_plain_k(0, pbuf);
-        step3<false, true, true>(st, sc, dummy, pp, pn, 0u, vl0 + pbuf * kTileBytes, qreg, c);
+        step3<false, true>(st, sc, dummy, pp, pn, 0u, vl0 + pbuf * kTileBytes, qreg, c);
         if (nplain > 0)
           wait_vmcnt<kCopiesPerTile / 2>();  // V(n) landed; plain K(0) may be in flight
         else

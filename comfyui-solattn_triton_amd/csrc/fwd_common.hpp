@@ -419,6 +419,83 @@ __device__ __forceinline__ void pv_tile(uint32_t vl, const bf16x8 (&pb)[4], int 
   pv_tile_with([&](int ks, int dt) { return v_op_x(vl, ks, dt); }, pb, o);
 }
 
+// ------------------------------------------- hand-ordered MFMA / softmax stream
+// The pipelined step issues its MFMAs and its softmax as inline asm so that
+// the instruction order is the one written: one MFMA, one pair of exps, the
+// next MFMA. (Left to the compiler, the MFMAs go out four at a time with ~30
+// VALU instructions behind them, and the MFMA pipe idles during the softmax.)
+// The compiler does not know that these asm statements are MFMAs, so the
+// hazards it would cover with wait states are covered here:
+//   VALU write -> MFMA read of that VGPR: 2 wait states, the s_nop 2 in front
+//     of the first P.V MFMA of a step (P and the rescaled O are written by
+//     VALU code before it);
+//   MFMA write -> VALU read of the result: at most NumPasses + 4 = 12 wait
+//     states for these 8-pass MFMAs; scores reach the softmax only through
+//     mfma_fence (16 wait states) or the in-out operands of the last MFMA
+//     of a step, which follows the last score MFMA by a pair of exps and
+//     another MFMA.
+// Every statement is volatile, so they keep their program order.
+__device__ __forceinline__ void mfma_v0(f32x16& d, const bf16x8& a, const bf16x8& b) {
+  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(d) : "v"(a), "v"(b));
+}
+__device__ __forceinline__ void mfma_v(f32x16& d, const bf16x8& a, const bf16x8& b) {
+  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(d) : "v"(a), "v"(b));
+}
+__device__ __forceinline__ void mfma_v_first(f32x16& d, const bf16x8& a, const bf16x8& b) {
+  asm volatile("s_nop 2\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(d) : "v"(a), "v"(b));
+}
+// An MFMA that also passes s through: readers of s come after it.
+__device__ __forceinline__ void mfma_v_tie(f32x16& d, const bf16x8& a, const bf16x8& b,
+                                           f32x16 (&s)[2]) {
+  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %3, %4, %0\n\ts_nop 3"
+               : "+v"(d), "+v"(s[0]), "+v"(s[1])
+               : "v"(a), "v"(b));
+}
+// 16 wait states after the MFMAs that wrote x; readers of x come after it.
+template <int N>
+__device__ __forceinline__ void mfma_fence(f32x16 (&x)[N]) {
+  static_assert(N == 2 || N == 4, "fence sizes");
+  if constexpr (N == 2)
+    asm volatile("s_nop 7\n\ts_nop 7" : "+v"(x[0]), "+v"(x[1]));
+  else
+    asm volatile("s_nop 7\n\ts_nop 7" : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]));
+}
+// p = exp2(s*c + neg) for two scores, packed to bf16 (round to nearest even),
+// both added to the row sum in fp32 (the reference sums the fp32 p,
+// /root/reference/_tri_fwd.py:330). The s_nop covers the one wait state a
+// transcendental result needs before a VALU reads it.
+__device__ __forceinline__ uint32_t exp_pair(float s0, float s1, float c, float neg, float& sum) {
+  uint32_t p;
+  float t0, t1;
+  asm volatile(
+      "v_fma_f32 %2, %4, %6, %7\n\t"
+      "v_fma_f32 %3, %5, %6, %7\n\t"
+      "v_exp_f32 %2, %2\n\t"
+      "v_exp_f32 %3, %3\n\t"
+      "s_nop 0\n\t"
+      "v_cvt_pk_bf16_f32 %0, %2, %3\n\t"
+      "v_add_f32 %1, %1, %2\n\t"
+      "v_add_f32 %1, %1, %3"
+      : "=v"(p), "+v"(sum), "=&v"(t0), "=&v"(t1)
+      : "v"(s0), "v"(s1), "v"(c), "v"(neg));
+  return p;
+}
+// The same arithmetic in plain code (the rare paths): P words of S elements
+// [R0, R0 + 8) into pk, fp32 row sum.
+template <int R0>
+__device__ __forceinline__ float exp8_f32sum(const f32x16& s, float c, float neg, bf16x8& pk,
+                                             float sum) {
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) {
+    const float p0 = __builtin_amdgcn_exp2f(fmaf(s[R0 + e], c, neg));
+    const float p1 = __builtin_amdgcn_exp2f(fmaf(s[R0 + e + 1], c, neg));
+    pk[e] = static_cast<__bf16>(p0);
+    pk[e + 1] = static_cast<__bf16>(p1);
+    sum = (sum + p0) + p1;
+  }
+  return sum;
+}
+
 // ------------------------------------------------------------ online softmax
 struct SoftmaxState {
   float m;          // running max, in the exp2 domain (score * c)
