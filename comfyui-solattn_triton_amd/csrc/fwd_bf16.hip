@@ -34,58 +34,73 @@ namespace bf16fwd {
 // kn goes to sn, interleaved with the softmax of tile n; `mid` runs before
 // P(n) . V(n).
 // kl, vl: this lane's operand addresses (k_lane, v_lane) in K(n+1) and V(n).
+// Hand-ordered as step3 below: each score MFMA is followed by the exps of
+// one P word, the operands are read two MFMAs ahead, and the lazy tile max
+// works the same way (also catching the first exact tile when no plain tile
+// came before it: running max -inf, p = inf).
 template <typename Mid>
 __device__ __forceinline__ void fast_step(SoftmaxState& st, f32x16 (&sc)[2], f32x16 (&sn)[2],
                                           uint32_t kl, uint32_t vl, const bf16x8 (&q)[8],
                                           float c, int lane, Mid&& mid) {
-  const f32x16 zero = {};
-  bf16x8 pb[4];
-  bf16x8 ka[8][2];
-  // Lazy tile max, as in step3: the exps use the running max as it stands
-  // and the tile max is taken only when a lane's row sum exceeds 255 (which
-  // also catches the first exact tile when no plain tile came before it:
-  // running max -inf, p = inf), so the running max evolves as if taken every
-  // tile.
-  float mx = -INFINITY, alpha = 1.f, neg = -st.m, psum = 0.f;
-  ka[0][0] = k_op_x(kl, 0, 0);
-  ka[0][1] = k_op_x(kl, 1, 0);
+  bf16x8 ka[3], va[3], pb[4];
+  uint32_t pw[4][4];
+  float psum = 0.f;
+  const float neg = -st.m;
+  ka[0] = k_op_x(kl, 0, 0);
+  ka[1] = k_op_x(kl, 1, 0);
+  asm volatile("" ::: "memory");
 #pragma unroll
-  for (int cc = 0; cc < 8; ++cc) {
-    if (cc + 1 < 8) {
-      ka[cc + 1][0] = k_op_x(kl, 0, cc + 1);
-      ka[cc + 1][1] = k_op_x(kl, 1, cc + 1);
+  for (int i = 0; i < 16; ++i) {
+    if (i + 2 < 16) {
+      ka[(i + 2) % 3] = k_op_x(kl, (i + 2) & 1, (i + 2) >> 1);
+      asm volatile("" ::: "memory");
     }
-    sn[0] = mfma_bf16(ka[cc][0], q[cc], cc == 0 ? zero : sn[0]);
-    sn[1] = mfma_bf16(ka[cc][1], q[cc], cc == 0 ? zero : sn[1]);
-    // softmax of tile n, spread over the 8 MFMA pairs
-    if (cc == 2) {
-      psum = exp8<0>(sc[0], c, neg, pb[0], psum);
-    } else if (cc == 3) {
-      psum = exp8<8>(sc[0], c, neg, pb[1], psum);
-    } else if (cc == 4) {
-      psum = exp8<0>(sc[1], c, neg, pb[2], psum);
-    } else if (cc == 5) {
-      psum = exp8<8>(sc[1], c, neg, pb[3], psum);
-      if (__any(!(psum <= 255.f))) {
+    if (i < 2)
+      mfma_v0(sn[i & 1], ka[i % 3], q[i >> 1]);
+    else
+      mfma_v(sn[i & 1], ka[i % 3], q[i >> 1]);
+    const int ks = i >> 2, w = i & 3;
+    const int r = 8 * (ks & 1) + 2 * w;
+    pw[ks][w] = exp_pair(sc[ks >> 1][r], sc[ks >> 1][r + 1], c, neg, psum);
+  }
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaxf(sc[0][r], sc[1][r]));
-        const float m_new = new_max(st.m, xhalf_max(mx) * c, alpha);
-        if (__any(m_new != st.m)) {  // lanes whose max stays recompute the same P
-          st.m = m_new;
-          neg = -m_new;
-          psum = 0.f;
-          psum = exp8<0>(sc[0], c, neg, pb[0], psum);
-          psum = exp8<8>(sc[0], c, neg, pb[1], psum);
-          psum = exp8<0>(sc[1], c, neg, pb[2], psum);
-          psum = exp8<8>(sc[1], c, neg, pb[3], psum);
-        }
-      }
+  for (int ks = 0; ks < 4; ++ks)
+    pb[ks] = __builtin_bit_cast(bf16x8, make_uint4(pw[ks][0], pw[ks][1], pw[ks][2], pw[ks][3]));
+  float alpha = 1.f;
+  if (__any(!(psum <= 255.f))) {  // (also catches inf / NaN)
+    float mx = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaxf(sc[0][r], sc[1][r]));
+    const float m_new = new_max(st.m, xhalf_max(mx) * c, alpha);
+    if (__any(m_new != st.m)) {  // lanes whose max stays recompute the same P
+      st.m = m_new;
+      psum = 0.f;
+      psum = exp8_f32sum<0>(sc[0], c, -m_new, pb[0], psum);
+      psum = exp8_f32sum<8>(sc[0], c, -m_new, pb[1], psum);
+      psum = exp8_f32sum<0>(sc[1], c, -m_new, pb[2], psum);
+      psum = exp8_f32sum<8>(sc[1], c, -m_new, pb[3], psum);
+      mfma_fence(st.acc);  // the rescale reads O
+      rescale(st, alpha);
     }
   }
   st.l = fmaf(st.l, alpha, psum);
-  rescale(st, alpha);
   mid();
-  pv_tile(vl, pb, lane, st.acc);
+  va[0] = v_op_x(vl, 0, 0);
+  va[1] = v_op_x(vl, 0, 1);
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    if (i + 2 < 16) {
+      va[(i + 2) % 3] = v_op_x(vl, (i + 2) >> 2, (i + 2) & 3);
+      asm volatile("" ::: "memory");
+    }
+    if (i == 0)
+      mfma_v_first(st.acc[0], va[0], pb[0]);
+    else if (i == 15)
+      mfma_v_tie(st.acc[3], va[0], pb[3], sn);  // va[15 % 3]
+    else
+      mfma_v(st.acc[i & 3], va[i % 3], pb[i >> 2]);
+  }
 }
 
 // Three-stage step: S(n+1) = K(n+1) Q^T, O += P(n-1) V(n-1) and the softmax of
@@ -307,6 +322,7 @@ fwd_bf16_sbuf_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t,
     wait_tile_copies();
     __syncthreads();
     qk_tile(kl, qreg, sa);
+    mfma_fence(sa);   // the step's softmax reads S(F) through asm
     __syncthreads();  // kbuf is free
     if (F + 1 < ntiles) issue_k(F + 1);
     wait_tile_copies();
@@ -342,10 +358,12 @@ fwd_bf16_sbuf_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t,
       step(sa, sb);
       wait_tile_copies();
       __syncthreads();
+      mfma_fence(st.acc);  // O from the asm MFMAs, read by the plain path
       finish_tile<BLK>(st, sb, vl, full, c, lane, NT, T);
     } else {
       wait_tile_copies();
       __syncthreads();
+      mfma_fence(st.acc);
       finish_tile<BLK>(st, sa, vl, full, c, lane, NT, T);
     }
   }
