@@ -208,10 +208,131 @@ __device__ __forceinline__ void exact_softmax_pv(SoftmaxState& st, f32x16 (&s)[2
 // n+1 from kn).
 // mid(): called before P(n).V(n) reads the V tile (a single-buffered V tile
 // is waited for there).
+// asm i8 MFMAs of the hand-ordered step (hazards as for the bf16 ones in
+// fwd_common.hpp).
+__device__ __forceinline__ void mfma_i8_v0(i32x16& d, const i32x4& a, const i32x4& b) {
+  asm volatile("v_mfma_i32_32x32x32_i8 %0, %1, %2, 0" : "=&v"(d) : "v"(a), "v"(b));
+}
+__device__ __forceinline__ void mfma_i8_v(i32x16& d, const i32x4& a, const i32x4& b) {
+  asm volatile("v_mfma_i32_32x32x32_i8 %0, %1, %2, %0" : "+v"(d) : "v"(a), "v"(b));
+}
+
+// bf16 P.V form of the pipelined step, hand-ordered like the BF16 forward's
+// steps: each of the 8 i8 score MFMAs of S(n+1) is followed by the exps of two
+// P(n) words; after mid(), each of the 16 P.V MFMAs by the conversion of two
+// int32 scores of S(n+1) to fp32 (times their ks). The K and V operands are
+// read two MFMAs ahead, the ks one group (four scores) ahead; the lazy tile
+// max is the BF16 forward's. (Spreading the exps over both phases, with the
+// tile max taken every step so that the P.V MFMAs could start on the first P
+// words, measured 7% slower.)
+template <bool UKS, typename Mid>
+__device__ __forceinline__ void fast_step_bf16pv(SoftmaxState& st, const f32x16 (&sc)[2],
+                                                 f32x16 (&sn)[2], const char* kn, const void* vt,
+                                                 const i32x4 (&qi)[4], float qsl, int lane,
+                                                 Mid&& mid) {
+  const int col = lane & 31, half = lane >> 5;
+  i32x16 si[2];
+  i32x4 ka[3];
+  bf16x8 va[3], pb[4];
+  uint32_t pw[4][4];
+  float psum = 0.f;
+  const float neg = -st.m;
+  const uint16_t* vtile = static_cast<const uint16_t*>(vt);
+  ka[0] = ki_op(kn, 0, 0, col, half);
+  ka[1] = ki_op(kn, 1, 0, col, half);
+  asm volatile("" ::: "memory");
+  const auto unit = [&](int u) {
+    const int ks = u >> 2, w = u & 3;
+    const int r = 8 * (ks & 1) + 2 * w;
+    pw[ks][w] = exp_pair(sc[ks >> 1][r], sc[ks >> 1][r + 1], qsl, neg, psum);
+  };
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    if (i + 2 < 8) {
+      ka[(i + 2) % 3] = ki_op(kn, (i + 2) & 1, (i + 2) >> 1, col, half);
+      asm volatile("" ::: "memory");
+    }
+    if (i < 2)
+      mfma_i8_v0(si[i & 1], ka[i % 3], qi[i >> 1]);
+    else
+      mfma_i8_v(si[i & 1], ka[i % 3], qi[i >> 1]);
+    unit(2 * i);
+    unit(2 * i + 1);
+  }
+  // the int32 scores are read after this point: 16 VALU instructions (the
+  // last two exp pairs) follow the last score MFMA
+  asm volatile("" : "+v"(si[0]), "+v"(si[1]));
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+    pb[ks] = __builtin_bit_cast(bf16x8, make_uint4(pw[ks][0], pw[ks][1], pw[ks][2], pw[ks][3]));
+  float alpha = 1.f;
+  if (__any(!(psum <= 255.f))) {  // (also catches inf / NaN)
+    float mx = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaxf(sc[0][r], sc[1][r]));
+    const float m_new = new_max(st.m, xhalf_max(mx) * qsl, alpha);
+    if (__any(m_new != st.m)) {  // lanes whose max stays recompute the same P
+      st.m = m_new;
+      psum = 0.f;
+      psum = exp8_f32sum<0>(sc[0], qsl, -m_new, pb[0], psum);
+      psum = exp8_f32sum<8>(sc[0], qsl, -m_new, pb[1], psum);
+      psum = exp8_f32sum<0>(sc[1], qsl, -m_new, pb[2], psum);
+      psum = exp8_f32sum<8>(sc[1], qsl, -m_new, pb[3], psum);
+      mfma_fence(st.acc);  // the rescale reads O
+      rescale(st, alpha);
+    }
+  }
+  st.l = fmaf(st.l, alpha, psum);
+  mid();
+  // ks of score group g (elements 4(g%4) .. +3 of tile g/4): read one group
+  // ahead of its two slots
+  const float* ksl = reinterpret_cast<const float*>(kn + kKsOffset);
+  const auto ks_group = [&](int g) {
+    return *reinterpret_cast<const float4*>(ksl + 32 * (g >> 2) + 8 * (g & 3) + 4 * half);
+  };
+  float4 kq[2];
+  if constexpr (!UKS) kq[0] = ks_group(0);
+  const uint32_t vl = v_lane(lds_addr(vtile), lane);
+  va[0] = v_op_x(vl, 0, 0);
+  va[1] = v_op_x(vl, 0, 1);
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    if (i + 2 < 16) {
+      va[(i + 2) % 3] = v_op_x(vl, (i + 2) >> 2, (i + 2) & 3);
+      if (!UKS && (i & 1) == 0 && (i >> 1) + 1 < 8) kq[((i >> 1) + 1) & 1] = ks_group((i >> 1) + 1);
+      asm volatile("" ::: "memory");
+    }
+    if (i == 0)
+      mfma_v_first(st.acc[0], va[0], pb[0]);
+    else
+      mfma_v(st.acc[i & 3], va[i % 3], pb[i >> 2]);
+    // scores 2i, 2i + 1 of S(n+1): element e of tile m (group i/2)
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int e2 = 2 * i + t, m = e2 >> 4, e = e2 & 15;
+      const float f = static_cast<float>(si[m][e]);
+      if constexpr (UKS) {
+        sn[m][e] = f;
+      } else {
+        const float4 kk = kq[(i >> 1) & 1];
+        const float kv = (e & 3) == 0 ? kk.x : (e & 3) == 1 ? kk.y : (e & 3) == 2 ? kk.z : kk.w;
+        sn[m][e] = f * kv;
+      }
+    }
+    asm volatile("" : "+v"(sn[i >> 3]));
+  }
+  mfma_fence(st.acc);  // O is read by plain code after the pipeline
+}
+
 template <bool INT8_PV, bool UKS, typename Mid>
 __device__ __forceinline__ void fast_step(SoftmaxState& st, f32x16 (&sc)[2], f32x16 (&sn)[2],
                                           const char* kn, const void* vt, const i32x4 (&qi)[4],
                                           float qsl, int lane, Mid&& mid) {
+  if constexpr (!INT8_PV) {
+    fast_step_bf16pv<UKS>(st, sc, sn, kn, vt, qi, qsl, lane, mid);
+    return;
+  }
   const int col = lane & 31, half = lane >> 5;
   const i32x16 zero = {};
   i32x16 si[2];
