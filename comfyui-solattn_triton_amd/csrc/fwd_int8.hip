@@ -325,6 +325,114 @@ __device__ __forceinline__ void fast_step_bf16pv(SoftmaxState& st, const f32x16 
   mfma_fence(st.acc);  // O is read by plain code after the pipeline
 }
 
+// Three-stage bf16 P.V step (block 128): S(n+1) = Ki(n+1) Qi^T (8 i8 MFMAs),
+// O += P(n-1) V(n-1) (16 bf16 MFMAs) and the softmax of S(n) in one
+// hand-ordered stream: slot i (16) issues score MFMA i (i < 8), the exps of P
+// word i, then P.V MFMA i; slots 8-15 also convert four int32 scores of S(n+1)
+// to fp32 times their ks (read two slots ahead, while tile n+1's ks are in
+// LDS). The last score MFMA is followed by two exp pairs and a P.V MFMA before
+// the int32 scores are read. QK = false: the last tile (no scores to make);
+// PV = false: the first. Lazy tile max, hazards and the final O rescale as
+// in the BF16 forward's step3. qc: the factor of sc's scores.
+template <bool QK, bool PV, bool UKS>
+__device__ __forceinline__ void step3_i8(SoftmaxState& st, const f32x16 (&sc)[2], float qc,
+                                         f32x16 (&sn)[2], const bf16x8 (&pp)[4], bf16x8 (&pn)[4],
+                                         const char* kn, uint32_t vl, const i32x4 (&qi)[4],
+                                         int lane) {
+  const int col = lane & 31, half = lane >> 5;
+  i32x16 si[2];
+  i32x4 ka[3];
+  bf16x8 va[3];
+  float4 kq[3];
+  uint32_t pw[4][4];
+  float psum = 0.f;
+  const float neg = -st.m;
+  const float* ksl = QK ? reinterpret_cast<const float*>(kn + kKsOffset) : nullptr;
+  const auto ks_group = [&](int g) {
+    return *reinterpret_cast<const float4*>(ksl + 32 * (g >> 2) + 8 * (g & 3) + 4 * half);
+  };
+  if constexpr (QK) {
+    ka[0] = ki_op(kn, 0, 0, col, half);
+    ka[1] = ki_op(kn, 1, 0, col, half);
+  }
+  if constexpr (PV) {
+    va[0] = v_op_x(vl, 0, 0);
+    va[1] = v_op_x(vl, 0, 1);
+  }
+  asm volatile("" ::: "memory");
+  const auto unit = [&](int u) {
+    const int ks = u >> 2, w = u & 3;
+    const int r = 8 * (ks & 1) + 2 * w;
+    pw[ks][w] = exp_pair(sc[ks >> 1][r], sc[ks >> 1][r + 1], qc, neg, psum);
+  };
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    if constexpr (QK) {
+      if (i + 2 < 8) ka[(i + 2) % 3] = ki_op(kn, (i + 2) & 1, (i + 2) >> 1, col, half);
+      if (!UKS && i >= 6 && i <= 13) kq[(i - 6) % 3] = ks_group(i - 6);
+    }
+    if constexpr (PV) {
+      if (i + 2 < 16) va[(i + 2) % 3] = v_op_x(vl, (i + 2) >> 2, (i + 2) & 3);
+    }
+    asm volatile("" ::: "memory");
+    if constexpr (QK) {
+      if (i < 2)
+        mfma_i8_v0(si[i & 1], ka[i % 3], qi[i >> 1]);
+      else if (i < 8)
+        mfma_i8_v(si[i & 1], ka[i % 3], qi[i >> 1]);
+    }
+    unit(i);
+    if constexpr (PV) {
+      if (i == 0)
+        mfma_v_first(st.acc[0], va[0], pp[0]);
+      else
+        mfma_v(st.acc[i & 3], va[i % 3], pp[i >> 2]);
+    }
+    if constexpr (QK) {
+      if (i == 8) asm volatile("" : "+v"(si[0]), "+v"(si[1]));  // the int32 scores are read after this
+      if (i >= 8) {
+        const int g = i - 8, m = g >> 2, e0 = 4 * (g & 3);
+        const float4 kk = kq[g % 3];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const float f = static_cast<float>(si[m][e0 + t]);
+          if constexpr (UKS) {
+            sn[m][e0 + t] = f;
+          } else {
+            const float kv = t == 0 ? kk.x : t == 1 ? kk.y : t == 2 ? kk.z : kk.w;
+            sn[m][e0 + t] = f * kv;
+          }
+        }
+        asm volatile("" : "+v"(sn[m]));
+      }
+    }
+    if (i == 0) __builtin_amdgcn_s_setprio(1);
+  }
+  __builtin_amdgcn_s_setprio(0);
+  if constexpr (!QK) mfma_fence(st.acc);  // the plain path's builtin MFMAs follow
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+    pn[ks] = __builtin_bit_cast(bf16x8, make_uint4(pw[ks][0], pw[ks][1], pw[ks][2], pw[ks][3]));
+  float alpha = 1.f;
+  if (__any(!(psum <= 255.f))) {  // (also catches inf / NaN)
+    float mx = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaxf(sc[0][r], sc[1][r]));
+    const float m_new = new_max(st.m, xhalf_max(mx) * qc, alpha);
+    if (__any(m_new != st.m)) {  // lanes whose max stays recompute the same P
+      st.m = m_new;
+      psum = 0.f;
+      psum = exp8_f32sum<0>(sc[0], qc, -m_new, pn[0], psum);
+      psum = exp8_f32sum<8>(sc[0], qc, -m_new, pn[1], psum);
+      psum = exp8_f32sum<0>(sc[1], qc, -m_new, pn[2], psum);
+      psum = exp8_f32sum<8>(sc[1], qc, -m_new, pn[3], psum);
+      if constexpr (PV) mfma_fence(st.acc);  // the rescale reads O
+      rescale(st, alpha);
+    }
+  }
+  st.l = fmaf(st.l, alpha, psum);
+}
+
 template <bool INT8_PV, bool UKS, typename Mid>
 __device__ __forceinline__ void fast_step(SoftmaxState& st, f32x16 (&sc)[2], f32x16 (&sn)[2],
                                           const char* kn, const void* vt, const i32x4 (&qi)[4],
@@ -659,6 +767,58 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
       wait_tile_copies();
       __syncthreads();  // K(F & 1) is refilled (K of tile F+2) by the first step
       int n = F;
+      if constexpr (!INT8_PV && !VSINGLE) {
+        // Three-stage pipeline (step3_i8). On entry to step n (F < n < E-1):
+        // S(n) and P(n-1) in registers, K(n+1) and V(n-1) in LDS; the step
+        // copies K(n+2) over K(n) and V(n) over V(n-2) (V(F) came with tile F).
+        const uint32_t vl0 = v_lane(vbuf_at(0), lane);
+        if (F + 1 < E) {
+          bf16x8 pa[4], pb[4];
+          issue_exact_full(min(F + 2, E - 1), kbuf_at(F & 1), 0u, true, false);
+          {
+            const char* kn = reinterpret_cast<const char*>(Kp((F + 1) & 1));
+            step3_i8<true, false, UKS>(st, sa, fa, sb, pb, pa, kn, 0u, qireg, lane);
+            fb = tile_qsl<UKS>(kn, kKsOffset, qsl);
+          }
+          wait_tile_copies();
+          __syncthreads();
+          n = F + 1;  // S(n) in sb (factor fb), P(n-1) in pa
+          const auto gstep = [&](const f32x16 (&sc)[2], float fc, f32x16 (&sn)[2], float& fnext,
+                                 const bf16x8 (&pp)[4], bf16x8 (&pn)[4]) {
+            issue_exact_full(min(n + 2, E - 1), kbuf_at(n & 1), 0u, true, false);
+            issue_exact_full(n, 0u, vbuf_at(n & 1), false, true);
+            const char* kn = reinterpret_cast<const char*>(Kp((n + 1) & 1));
+            step3_i8<true, true, UKS>(st, sc, fc, sn, pp, pn, kn, vl0 + ((n - 1) & 1) * VSTRIDE,
+                                      qireg, lane);
+            fnext = tile_qsl<UKS>(kn, kKsOffset, qsl);
+            wait_tile_copies();
+            __syncthreads();
+            ++n;
+          };
+          const auto last = [&](const f32x16 (&sc)[2], float fc, f32x16 (&dummy)[2],
+                                const bf16x8 (&pp)[4], bf16x8 (&pn)[4]) {
+            issue_exact_full(n, 0u, vbuf_at(n & 1), false, true);  // V(E-1)
+            step3_i8<false, true, UKS>(st, sc, fc, dummy, pp, pn, nullptr,
+                                       vl0 + ((n - 1) & 1) * VSTRIDE, qireg, lane);
+            wait_tile_copies();
+            __syncthreads();
+            pv_tile(reinterpret_cast<const uint16_t*>(Vp(n & 1)), pn, lane, st.acc);
+          };
+          while (n + 2 < E) {
+            gstep(sb, fb, sa, fa, pa, pb);
+            gstep(sa, fa, sb, fb, pb, pa);
+          }
+          if (n + 1 < E) {
+            gstep(sb, fb, sa, fa, pa, pb);
+            last(sa, fa, sb, pb, pa);
+          } else {
+            last(sb, fb, sa, pa, pb);
+          }
+        } else {
+          exact_softmax_pv<INT8_PV>(st, sa, Vp(bi(n)), fa, lane);
+        }
+        __syncthreads();
+      } else {
       // Step n needs n + 1 < E. K(n+2) of the last step is clamped to the
       // last full tile: a redundant copy into a buffer nothing reads afterwards.
       // VSINGLE: V(n) was copied at the end of step n-1, before this step's
@@ -700,6 +860,7 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
         exact_softmax_pv<INT8_PV>(st, sa, Vp(bi(n)), fa, lane);
       }
       __syncthreads();
+      }
     }
     if constexpr (INT8_PV) {
       // The per-channel V scale, common to every exact tile. The empty asm
