@@ -58,7 +58,8 @@ def per_block(got: np.ndarray, ref: dict, block: int):
     return stats
 
 
-def check_int8_blocks(label, got, qb, vb, prep, rows, int8_pv, block):
+def check_int8_blocks(label, got, qb, vb, prep, rows, int8_pv, block,
+                      kernel_maxabs=INT8_KERNEL_MAXABS):
     """Per-query-block INT8 checks against the oracle's two arithmetics, with
     the worst block of each printed."""
     import oracle
@@ -75,5 +76,5 @@ def check_int8_blocks(label, got, qb, vb, prep, rows, int8_pv, block):
           f"arithmetic: worst max|err| {w_abs[1]:.3e} at {w_abs[0]}, worst cos {w_cos[2]:.6f} "
           f"at {w_cos[0]}", flush=True)
     assert w_ref[2] >= INT8_COS, w_ref
-    assert w_abs[1] <= INT8_KERNEL_MAXABS, w_abs
+    assert w_abs[1] <= kernel_maxabs, w_abs
     assert w_cos[2] >= INT8_KERNEL_COS, w_cos

@@ -224,6 +224,45 @@ def test_fwd_int8_vs_port(pkg, dev, case, int8_pv):
 
 
 @pytest.mark.parametrize("block", [64, 128])
+@pytest.mark.parametrize("mode", ["bf16", "int8_pv", "int8_bf16pv"])
+def test_fwd_running_max_moves(pkg, dev, block, mode):
+    """Keys scaled up along the sequence (x1 at the start, x8 at the end): a row's
+    scores grow with the key index, so its running max moves by more than the
+    kernels' slack (8, log2 units) several times inside the pipelined exact
+    tiles, and the steps' rare path runs (P recomputed against the new max, O
+    rescaled after the step's MFMAs)."""
+    B, T, H, tau = 1, 4096, 2, 0.9
+    print(f"[fwd max moves] block={block} mode={mode}", flush=True)
+    q, k, v = (randn_bf16((B, T, H, 128), s) for s in (50, 51, 52))
+    ramp = (1.0 + 7.0 * torch.arange(T, dtype=torch.float32) / T).view(1, T, 1, 1)
+    k = (k.float() * ramp).to(torch.bfloat16)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    if mode == "bf16":
+        out = _mods(pkg)[1].sol_attn(qd, kd, vd, tau=tau, block=block)
+        torch.cuda.synchronize()
+        ref = oracle.prepare(bits(q), bits(k), bits(v), block=block, tau=tau)
+        rows = _rows(B, H, ref["NT"], limit=24)
+        port = oracle.forward_port(bits(q), bits(k), bits(v), ref, rows)
+        err, cos = compare_rows(out.float().cpu().numpy(), port, block)
+        print(f"[fwd max moves] max|err|={err:.3e} cos={cos:.6f}", flush=True)
+        assert err < BF16_MAXABS and cos >= BF16_COS
+    else:
+        int8_pv = mode == "int8_pv"
+        out = _mods(pkg)[2].sol_attn_int8(qd, kd, vd, tau=tau, block=block, int8_pv=int8_pv)
+        torch.cuda.synchronize()
+        ref = oracle.prepare(bits(q), bits(k), bits(v), block=block, tau=tau, int8=True,
+                             int8_pv=int8_pv)
+        rows = _rows(B, H, ref["NT"], limit=16)
+        # Rows here are sharply peaked (few large P codes), so one code of
+        # difference where exp2 lands on a rounding boundary moves an output by
+        # ~|v| / (sum of codes): the kernel-arithmetic max-abs bound is 3e-2
+        # (1.4e-2 measured) instead of the 1e-2 of ordinary inputs; the
+        # cosines keep their bounds.
+        check_int8_blocks(f"fwd max moves {mode} block={block}", out.float().cpu().numpy(),
+                          bits(q), bits(v), ref, rows, int8_pv, block, kernel_maxabs=3e-2)
+
+
+@pytest.mark.parametrize("block", [64, 128])
 def test_fwd_vs_dense_block_mask_diagnostic(pkg, dev, block):
     """Dense SDPA restricted to the same block mask (the pooled term dropped).
     A diagnostic, not the reference's output: the skipped blocks carry real
