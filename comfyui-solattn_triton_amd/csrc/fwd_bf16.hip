@@ -17,6 +17,9 @@
 //   block 64 (fwd_bf16_sbuf_kernel): K and V single buffered, four workgroups
 //     per CU; plain tiles first, two-stage step n = S(n+1) with the softmax of
 //     tile n interleaved, then O += P(n) V(n).
+// Both pipelined steps are hand-ordered: inline-asm MFMAs and softmax exp
+// pairs in a fixed interleave (fwd_common.hpp), which the compiler's own
+// schedule did not give.
 //
 // MFMA dataflow (v_mfma_f32_32x32x16_bf16): S^T = K . Q^T puts one query row
 // per lane column, so row max / sum need one cross-lane step (lanes 32 apart,
