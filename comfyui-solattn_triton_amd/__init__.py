@@ -159,7 +159,8 @@ if _COMFY_ERROR is None:
                     io.Float.Input("end_percent", default=0.9, min=0.0, max=1.0, step=0.01),
                     io.Int.Input("min_tokens", default=MIN_TOKENS, min=0, max=1 << 20, step=512,
                                  tooltip="Sequences shorter than this stay dense. On MI355X "
-                                         "the sparse path beats dense SDPA from 2048 tokens."),
+                                         "the sparse path already beats dense SDPA from 2048 "
+                                         "tokens; lower this to trade exactness for speed."),
                     io.Boolean.Input("int8_qk", default=True,
                                      tooltip="INT8 QK in the exact branch (smoothed K, per-token "
                                              "scales) on the int8 matrix cores."),

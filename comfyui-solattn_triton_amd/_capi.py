@@ -30,14 +30,14 @@ SIGNATURES = {
     "solattn_pool": ([_p, _l, _l, _l] * 3 + [_l] * 5 + [_p, _p, _l, _p, _p, _p], _i),
     "solattn_moments": ([_p, _l, _l, _l, _l, _l, _i, _p, _p, _p, _p, _p], _i),
     "solattn_route": ([_p, _p, _l, _p, _p, _l, _l, _l, _l, _l, _f, _f, _i, _l, _l, _l, _l,
-                       _p, _p, _p, _p, _p], _i),
+                       _p, _p, _p, _p], _i),
     "solattn_quant_rows": ([_p, _l, _l, _l, _l, _l, _l, _l, _p, _p, _p, _l, _p], _i),
     "solattn_quant_rows_blocked": ([_p, _l, _l, _l, _l, _l, _l, _l, _p, _p, _p, _l, _p], _i),
     "solattn_quant_v": ([_p, _l, _l, _l, _l, _l, _l, _l, _p, _p, _l, _p], _i),
-    "solattn_fwd_bf16": ([_p, _l, _l, _l] * 3 + [_p, _p, _l, _p, _p, _p] + [_l] * 5 +
+    "solattn_fwd_bf16": ([_p, _l, _l, _l] * 3 + [_p, _p, _l, _p, _p] + [_l] * 5 +
                          [_f, _p, _l, _l, _l, _p], _i),
     "solattn_fwd_int8": ([_p, _l, _l, _l, _p, _p, _p, _p, _p, _p, _p, _l, _l, _l, _l, _p, _p, _l,
-                          _p, _p, _p] + [_l] * 5 + [_f, _i, _p, _l, _l, _l, _p], _i),
+                          _p, _p] + [_l] * 5 + [_f, _i, _p, _l, _l, _l, _p], _i),
     "solattn_sol_attn_workspace_bytes": ([_l, _l, _l, _l, _l, _i], _l),
     "solattn_sol_attn": ([_p, _l, _l, _l] * 3 + [_l] * 5 + [_f, _f, _l, _l, _l, _l, _p, _l,
                                                            _p, _l, _l, _l, _p], _i),

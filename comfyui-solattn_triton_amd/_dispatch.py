@@ -44,11 +44,12 @@ except Exception as exc:
     _INT8_IMPORT_ERROR = exc
 
 HEAD_DIM = 128
-# Shortest sequence the sparse path takes by default: on MI355X every sparse
-# call (BF16 and both INT8 modes, prep included) beats the dense PyTorch SDPA
-# from 2048 tokens on; the INT8 calls lose to it at 1024 (the reference's
-# default, tuned for its own kernels, is 4096).
-MIN_TOKENS = 2048
+# Shortest sequence the sparse path takes by default: the reference's 4096
+# (/root/reference/__init__.py:256, 442, 657), so calls of 2048-4095 tokens stay
+# exact (dense) as there. On MI355X every sparse call (BF16 and both INT8
+# modes, prep included) already beats dense PyTorch SDPA from 2048 tokens, so
+# a node may lower its min_tokens to 2048 to trade that exactness for speed.
+MIN_TOKENS = 4096
 BLOCK_SIZE = 64  # default routing block (the reference's); 128 is also supported
 # Query/key blocks per head the forward kernels take; longer sequences stay dense.
 MAX_BLOCKS = 16384

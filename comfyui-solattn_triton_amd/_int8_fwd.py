@@ -61,7 +61,7 @@ def forward_int8(q, v, routing: Routing, qi, qs, ki, ks, vi=None, *, scale=None,
              ptr(ki), ptr(ks), ptr(vi if int8_pv else None),
              ptr(routing.vscale if int8_pv else None), ptr(v), v.stride(0), v.stride(1),
              v.stride(2), TP, ptr(routing.kc), ptr(routing.vc), npad, ptr(routing.counts),
-             ptr(routing.lists), ptr(routing.mask), B, T, H, D, routing.block, float(scale),
+             ptr(routing.mask), B, T, H, D, routing.block, float(scale),
              1 if int8_pv else 0, ptr(out), out.stride(0), out.stride(1), out.stride(2),
              stream(q.device))
     return out

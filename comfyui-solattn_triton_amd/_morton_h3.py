@@ -48,7 +48,11 @@ def _log_once(message):
 
 
 def _gather(x: torch.Tensor, index: torch.Tensor, dim: int) -> torch.Tensor:
-    """The hooks' row permutation: the gfx950 gather kernel."""
+    """The hooks' row permutation: the gfx950 gather kernel for GPU tensors;
+    a pass whose tensors live on the host (no kernel can touch them) is
+    permuted with ``index_select``, as the reference does on any device."""
+    if x.device.type != "cuda":
+        return x.index_select(dim, index.to(x.device))
     return reorder_tokens(x, index, dim=dim)
 
 

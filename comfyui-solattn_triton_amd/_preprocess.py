@@ -1,4 +1,4 @@
-"""Block summaries, routing thresholds and exact-block lists (host side).
+"""Block summaries, routing thresholds and exact-block masks (host side).
 
 Mirrors /root/reference/_preprocess.py (``prepare``, ``_reduce_kv``,
 ``_compute_diag_threshold``) over the gfx950 kernels ``solattn_pool``,
@@ -93,8 +93,7 @@ class Routing(NamedTuple):
     qbar: torch.Tensor      # fp32 [B, H, NT, D]
     kc_mean: torch.Tensor   # fp32 [B, H, D]
     kc_var: torch.Tensor    # fp32 [B, H, D]
-    counts: torch.Tensor    # int32 [B, H, NT]
-    lists: torch.Tensor     # int16 [B, H, NT, NT]
+    counts: torch.Tensor    # int32 [B, H, NT] exact blocks per query block
     mask: torch.Tensor      # int32 view of uint32 [B, H, NT, ceil(NT/32)]
     vamax_part: torch.Tensor | None
     vscale: torch.Tensor | None  # fp32 [B, H, D]
@@ -108,7 +107,7 @@ def _sv(t):
 
 def route(q, k, v, *, scale: float, tau: float, block: int = BLOCK_SIZE, int8: bool = False,
           v_absmax: bool = False, sink_blocks=(0, 0), sink_q=(0, 0)) -> Routing:
-    """pool -> moments -> thresholds + routing lists, all on the device.
+    """pool -> moments -> thresholds + routing masks, all on the device.
 
     ``int8`` selects the INT8 path's centred pooled keys and tau*sigma
     threshold (/root/reference/_fused_prep.py:77-81, 50-59); ``v_absmax``
@@ -139,7 +138,6 @@ def route(q, k, v, *, scale: float, tau: float, block: int = BLOCK_SIZE, int8: b
     vscale = torch.empty((B, H, D), **f32) if v_absmax else None
     thr = torch.empty((B, NT, H), **f32)
     counts = torch.empty((B, H, NT), device=dev, dtype=torch.int32)
-    lists = torch.empty((B, H, NT, NT), device=dev, dtype=torch.int16)
     mask = torch.empty((B, H, NT, W), device=dev, dtype=torch.int32)
     with torch.cuda.device(dev):
         s = stream(dev)
@@ -150,8 +148,8 @@ def route(q, k, v, *, scale: float, tau: float, block: int = BLOCK_SIZE, int8: b
         call("solattn_route", ptr(qbar), ptr(kc), npad, ptr(kc_mean), ptr(kc_var), B, T, H, D,
              block, float(scale), float(tau), 1 if int8 else 0, int(sink_blocks[0]),
              int(sink_blocks[1]), int(sink_q[0]), int(sink_q[1]), ptr(thr), ptr(counts),
-             ptr(lists), ptr(mask), s)
-    return Routing(kc, vc, thr, qbar, kc_mean, kc_var, counts, lists, mask, vamax, vscale, block, T)
+             ptr(mask), s)
+    return Routing(kc, vc, thr, qbar, kc_mean, kc_var, counts, mask, vamax, vscale, block, T)
 
 
 def prepare(q, k, v, *, tau: float, scale: float, tokens: int | None = None,

@@ -71,7 +71,7 @@ def forward_bf16(q, k, v, routing: Routing, *, scale: float | None = None,
     with torch.cuda.device(q.device):
         call("solattn_fwd_bf16", ptr(q), q.stride(0), q.stride(1), q.stride(2), ptr(k), k.stride(0),
              k.stride(1), k.stride(2), ptr(v), v.stride(0), v.stride(1), v.stride(2),
-             ptr(routing.kc), ptr(routing.vc), npad, ptr(routing.counts), ptr(routing.lists),
-             ptr(routing.mask), B, T, H, D, routing.block, float(scale), ptr(out), out.stride(0),
+             ptr(routing.kc), ptr(routing.vc), npad, ptr(routing.counts), ptr(routing.mask),
+             B, T, H, D, routing.block, float(scale), ptr(out), out.stride(0),
              out.stride(1), out.stride(2), stream(q.device))
     return out

@@ -51,7 +51,7 @@ inline bool pipeline_head_dim_ok(int64_t D) { return D >= 8 && D <= kKernelD && 
 // Carves the pipeline's intermediates out of one workspace.
 struct Layout {
   int64_t NT, npad, W, TP;
-  int64_t kc, vc, qbar, kc_mean, kc_var, thr, counts, lists, mask;   // byte offsets
+  int64_t kc, vc, qbar, kc_mean, kc_var, thr, counts, mask;   // byte offsets
   int64_t vamax, vscale, qi, qs, ki, ks, vi;                          // INT8 only
   int64_t qp, kp, vp, op;  // zero-padded [B, T, H, 128] q, k, v, o (head dims < 128)
   bool padded;
@@ -76,7 +76,6 @@ struct Layout {
     kc_var = take(B * H * Dk * 4);
     thr = take(B * NT * H * 4);
     counts = take(B * H * NT * 4);
-    lists = take(B * H * NT * NT * 2);
     mask = take(B * H * NT * W * 4);
     vamax = vscale = qi = qs = ki = ks = vi = -1;
     if (int8) {
@@ -110,7 +109,7 @@ using namespace solattn;
 
 extern "C" const char* solattn_last_error(void) { return g_error; }
 
-extern "C" int solattn_abi_version(void) { return (1 << 16) | 0; }
+extern "C" int solattn_abi_version(void) { return (2 << 16) | 0; }
 
 extern "C" int solattn_morton_perm(int64_t frames, int64_t height, int64_t width, int curve,
                                    int64_t roll, int64_t* perm, int64_t* inverse) {
@@ -199,13 +198,11 @@ int run_bf16_pipeline(const Layout& L, void* ws, const Call& call, solattn_strea
     rc = solattn_route(at<float>(ws, L.qbar), at<uint16_t>(ws, L.kc), L.npad,
                        at<float>(ws, L.kc_mean), at<float>(ws, L.kc_var), c.B, c.T, c.H, c.D,
                        c.block, c.scale, c.tau, 0, c.skv_lo, c.skv_hi, c.sq_lo, c.sq_hi,
-                       at<float>(ws, L.thr), at<int32_t>(ws, L.counts), at<int16_t>(ws, L.lists),
-                       at<uint32_t>(ws, L.mask), stream);
+                       at<float>(ws, L.thr), at<int32_t>(ws, L.counts), at<uint32_t>(ws, L.mask), stream);
     if (rc) return rc;
     return solattn_fwd_bf16(c.q, c.sq_b, c.sq_t, c.sq_h, c.k, c.sk_b, c.sk_t, c.sk_h, c.v, c.sv_b,
                             c.sv_t, c.sv_h, at<uint16_t>(ws, L.kc), at<uint16_t>(ws, L.vc), L.npad,
-                            at<int32_t>(ws, L.counts), at<int16_t>(ws, L.lists),
-                            at<uint32_t>(ws, L.mask), c.B, c.T, c.H, c.D, c.block, c.scale, c.o,
+                            at<int32_t>(ws, L.counts), at<uint32_t>(ws, L.mask), c.B, c.T, c.H, c.D, c.block, c.scale, c.o,
                             c.so_b, c.so_t, c.so_h, stream);
   });
 }
@@ -232,8 +229,7 @@ int run_int8_pipeline(const Layout& L, void* ws, const Call& call, int int8_pv,
     rc = solattn_route(at<float>(ws, L.qbar), at<uint16_t>(ws, L.kc), L.npad, nullptr,
                        at<float>(ws, L.kc_var), c.B, c.T, c.H, c.D, c.block, c.scale, c.tau, 1,
                        c.skv_lo, c.skv_hi, c.sq_lo, c.sq_hi, at<float>(ws, L.thr),
-                       at<int32_t>(ws, L.counts), at<int16_t>(ws, L.lists),
-                       at<uint32_t>(ws, L.mask), stream);
+                       at<int32_t>(ws, L.counts), at<uint32_t>(ws, L.mask), stream);
     if (rc) return rc;
     rc = quant_qkv(qk_block ? c.q : nullptr, c.sq_b, c.sq_t, c.sq_h, c.k, c.sk_b, c.sk_t, c.sk_h,
                    c.v, c.sv_b, c.sv_t, c.sv_h, c.B, c.T, c.H, c.D, at<float>(ws, L.kc_mean),
@@ -248,7 +244,7 @@ int run_int8_pipeline(const Layout& L, void* ws, const Call& call, int int8_pv,
                     at<int8_t>(ws, L.ki), at<float>(ws, L.ks),
                     int8_pv ? at<int8_t>(ws, L.vi) : nullptr, vscale, c.v, c.sv_b, c.sv_t, c.sv_h,
                     L.TP, at<uint16_t>(ws, L.kc), at<uint16_t>(ws, L.vc), L.npad,
-                    at<int32_t>(ws, L.counts), at<int16_t>(ws, L.lists), at<uint32_t>(ws, L.mask),
+                    at<int32_t>(ws, L.counts), at<uint32_t>(ws, L.mask),
                     c.B, c.T, c.H, c.D, c.block, c.scale, int8_pv, c.o, c.so_b, c.so_t, c.so_h,
                     stream, qk_block != 0, /*ks_head_major=*/true);
   });

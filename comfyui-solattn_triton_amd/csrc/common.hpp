@@ -94,7 +94,7 @@ int fwd_int8(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h, const 
              const float* qs, const int8_t* ki, const float* ks, const int8_t* vi,
              const float* vscale, const uint16_t* v, int64_t sv_b, int64_t sv_t, int64_t sv_h,
              int64_t TP, const uint16_t* kc, const uint16_t* vc, int64_t npad,
-             const int32_t* counts, const int16_t* lists, const uint32_t* mask, int64_t B,
+             const int32_t* counts, const uint32_t* mask, int64_t B,
              int64_t T, int64_t H, int64_t D, int64_t block, float scale, int int8_pv,
              uint16_t* o, int64_t so_b, int64_t so_t, int64_t so_h, solattn_stream_t stream,
              bool uniform_ks, bool ks_head_major = false);

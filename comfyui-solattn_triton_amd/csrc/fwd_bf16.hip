@@ -226,8 +226,7 @@ fwd_bf16_sbuf_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t,
                 const uint16_t* __restrict__ k, int64_t sk_b, int64_t sk_t, int64_t sk_h,
                 const uint16_t* __restrict__ v, int64_t sv_b, int64_t sv_t, int64_t sv_h,
                 const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc, int64_t npad,
-                const int32_t* __restrict__ counts, const int16_t* __restrict__ lists,
-                const uint32_t* __restrict__ mask, int T, int H, int NT, int W, float c,
+                const int32_t* __restrict__ counts, const uint32_t* __restrict__ mask, int T, int H, int NT, int W, float c,
                 uint16_t* __restrict__ o, int64_t so_b, int64_t so_t, int64_t so_h) {
   constexpr int NTHREADS = BLK * 2;
   __shared__ __align__(256) uint16_t kbuf[kTileElems];
@@ -241,11 +240,11 @@ fwd_bf16_sbuf_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t,
   const int b = bh / H, h = bh % H;
   const int64_t row = static_cast<int64_t>(bh) * NT + qb;
 
-  const int ntiles = build_tile_list<BLK>(tl, counts, lists, mask, row, NT, W, T);
-  if (ntiles == 0) return;  // cannot happen for routed lists: the diagonal is exact
+  const int ntiles = build_tile_list<BLK>(tl, mask, row, NT, W, T);
+  if (ntiles == 0) return;  // cannot happen for routed masks: the diagonal is exact
   // The last exact tile is ragged when block NT-1 is exact and T is not a
   // multiple of 64 (exact blocks are listed in ascending order).
-  const int nrag = ragged_tiles(tl, counts, row, NT, T);
+  const int nrag = ragged_tiles(tl, NT, T);
   const int nplain = tl.npool + nrag;
 
   const KVSource src{k + b * sk_b + h * sk_h, sk_t, v + b * sv_b + h * sv_h, sv_t,
@@ -386,8 +385,7 @@ fwd_bf16_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
                      const uint16_t* __restrict__ k, int64_t sk_b, int64_t sk_t, int64_t sk_h,
                      const uint16_t* __restrict__ v, int64_t sv_b, int64_t sv_t, int64_t sv_h,
                      const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc, int64_t npad,
-                     const int32_t* __restrict__ counts, const int16_t* __restrict__ lists,
-                     const uint32_t* __restrict__ mask, int T, int H, int NT, int W, float c,
+                     const int32_t* __restrict__ counts, const uint32_t* __restrict__ mask, int T, int H, int NT, int W, float c,
                      uint16_t* __restrict__ o, int64_t so_b, int64_t so_t, int64_t so_h) {
   constexpr int NTHREADS = BLK * 2;
   constexpr int kCopiesPerTile = 2 * CopyOffsets<NTHREADS>::U;
@@ -402,9 +400,9 @@ fwd_bf16_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
   const int b = bh / H, h = bh % H;
   const int64_t row = static_cast<int64_t>(bh) * NT + qb;
 
-  const int ntiles = build_tile_list<BLK>(tl, counts, lists, mask, row, NT, W, T);
-  if (ntiles == 0) return;  // cannot happen for routed lists: the diagonal is exact
-  const int nrag = ragged_tiles(tl, counts, row, NT, T);
+  const int ntiles = build_tile_list<BLK>(tl, mask, row, NT, W, T);
+  if (ntiles == 0) return;  // cannot happen for routed masks: the diagonal is exact
+  const int nrag = ragged_tiles(tl, NT, T);
   // Full exact tiles (list tiles 0 .. nfast-1) run through the pipeline when
   // there are at least two; a lone one runs as the first plain tile.
   const int nfast = ntiles - tl.npool - nrag;
@@ -567,13 +565,12 @@ extern "C" int solattn_fwd_bf16(const uint16_t* q, int64_t sq_b, int64_t sq_t, i
                                 const uint16_t* k, int64_t sk_b, int64_t sk_t, int64_t sk_h,
                                 const uint16_t* v, int64_t sv_b, int64_t sv_t, int64_t sv_h,
                                 const uint16_t* kc, const uint16_t* vc, int64_t npad,
-                                const int32_t* counts, const int16_t* lists,
-                                const uint32_t* mask, int64_t B, int64_t T, int64_t H, int64_t D,
+                                const int32_t* counts, const uint32_t* mask, int64_t B, int64_t T, int64_t H, int64_t D,
                                 int64_t block, float scale, uint16_t* o, int64_t so_b,
                                 int64_t so_t, int64_t so_h, solattn_stream_t stream) {
   clear_error();
   if (int rc = check_fwd_args(q, sq_b, sq_t, sq_h, k, sk_b, sk_t, sk_h, v, sv_b, sv_t, sv_h, kc,
-                              vc, npad, counts, lists, mask, B, T, H, D, block, o, so_b, so_t,
+                              vc, npad, counts, mask, B, T, H, D, block, o, so_b, so_t,
                               so_h, "fwd_bf16"))
     return rc;
   const int64_t NT = cdiv(T, block);
@@ -584,12 +581,12 @@ extern "C" int solattn_fwd_bf16(const uint16_t* q, int64_t sq_b, int64_t sq_t, i
   if (block == 128) {
     hipLaunchKernelGGL((bf16fwd::fwd_bf16_kernel<128>), dim3(grid), dim3(256), blist_lds_bytes(NT), s,
                        q, sq_b, sq_t, sq_h, k, sk_b, sk_t, sk_h, v, sv_b, sv_t, sv_h, kc, vc, npad,
-                       counts, lists, mask, static_cast<int>(T), static_cast<int>(H),
+                       counts, mask, static_cast<int>(T), static_cast<int>(H),
                        static_cast<int>(NT), W, c, o, so_b, so_t, so_h);
   } else {
     hipLaunchKernelGGL((bf16fwd::fwd_bf16_sbuf_kernel<64>), dim3(grid), dim3(128), blist_lds_bytes(NT), s, q,
                        sq_b, sq_t, sq_h, k, sk_b, sk_t, sk_h, v, sv_b, sv_t, sv_h, kc, vc, npad,
-                       counts, lists, mask, static_cast<int>(T), static_cast<int>(H),
+                       counts, mask, static_cast<int>(T), static_cast<int>(H),
                        static_cast<int>(NT), W, c, o, so_b, so_t, so_h);
   }
   return check_launch("fwd_bf16");

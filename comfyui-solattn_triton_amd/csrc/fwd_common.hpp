@@ -27,8 +27,10 @@ constexpr float kMaxSlack = 8.f;      // lazy running max (log2 units)
 struct TileList {
   uint64_t pmask[kMaxPool];  // approximate-block mask of each pooled tile
   int16_t pchunk[kMaxPool];  // pooled tile -> chunk of 64 pooled keys
-  int npool;
-  int nexact;
+  int npool;   // pooled tiles
+  int nexact;  // exact 64-key tiles
+  int nblk;    // exact key blocks (the first nblk entries of blist_lds())
+  int last;    // highest exact key block, -1 if none
 };
 
 // The exact key blocks of the workgroup's query block, ascending, live in the
@@ -107,19 +109,19 @@ __device__ __forceinline__ void tile_coords_lpt(const int32_t* __restrict__ coun
   qb = static_cast<int>(logical % static_cast<uint32_t>(NT));
 }
 
+// The workgroup's tiles, from its row of the routing bitmask (bit j of word
+// j/32 = key block j is exact). Needs at least two waves: wave 0 collects the
+// pooled chunks, wave 1 the exact blocks, in parallel. Every entry comes from
+// a set bit below NT, so any mask contents give in-range tiles.
 template <int BLK>
-__device__ int build_tile_list(TileList& tl, const int32_t* __restrict__ counts,
-                               const int16_t* __restrict__ lists, const uint32_t* __restrict__ mask,
-                               int64_t row, int NT, int W, int T) {
-  const int cnt = min(max(counts[row], 0), NT);
-  int16_t* blist = blist_lds();
-  for (int e = threadIdx.x; e < cnt; e += blockDim.x) blist[e] = lists[row * NT + e];
-  // Pooled chunks (64 key blocks each): wave 0 scans one chunk per lane, 64
-  // chunks a pass, so the mask words are loaded together; a ballot prefix
-  // keeps the chunks in ascending order.
-  if (threadIdx.x < 64) {
-    const int lane = threadIdx.x;
-    const uint32_t* mrow = mask + row * W;
+__device__ int build_tile_list(TileList& tl, const uint32_t* __restrict__ mask, int64_t row,
+                               int NT, int W, int T) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const uint32_t* mrow = mask + row * W;
+  if (wave == 0) {
+    // Pooled chunks (64 key blocks each): one chunk per lane, 64 chunks a
+    // pass, so the mask words are loaded together; a ballot prefix keeps the
+    // chunks in ascending order.
     int np = 0;
     for (int c0 = 0; c0 * 64 < NT; c0 += 64) {
       const int c = c0 + lane;
@@ -141,25 +143,45 @@ __device__ int build_tile_list(TileList& tl, const int32_t* __restrict__ counts,
       np += __popcll(has);
     }
     if (lane == 0) tl.npool = np;
+  } else if (wave == 1) {
+    // Exact blocks, ascending: one lane per block, 64 blocks per ballot. The
+    // words of 2048 blocks come in one load per lane and are passed around
+    // with shuffles.
+    int16_t* blist = blist_lds();
+    int ne = 0, last = -1;
+    for (int w0 = 0; w0 < W; w0 += 64) {
+      const uint32_t word = w0 + lane < W ? mrow[w0 + lane] : 0u;
+      const int nw = min(64, W - w0);
+      for (int p = 0; 2 * p < nw; ++p) {
+        const uint32_t mine = __shfl(word, 2 * p + (lane >> 5));
+        const int j = (w0 + 2 * p) * 32 + lane;
+        const bool ex = j < NT && ((mine >> (lane & 31)) & 1u);
+        const uint64_t bal = __ballot(ex);
+        if (ex)
+          blist[ne + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(bal >> 32),
+                                               __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bal), 0))] =
+              static_cast<int16_t>(j);
+        ne += __popcll(bal);
+        if (bal) last = (w0 + 2 * p) * 32 + 63 - __clzll(bal);
+      }
+    }
+    if (lane == 0) {
+      constexpr int S = BLK / kKeys;
+      const int tail = T - (NT - 1) * BLK;
+      tl.nblk = ne;
+      tl.last = last;
+      // at block 128 a last block of at most 64 tokens is one (ragged) tile
+      tl.nexact = ne * S - ((S == 2 && last == NT - 1 && tail <= kKeys) ? 1 : 0);
+    }
   }
-  __syncthreads();  // blist and the pooled chunks are in LDS
-  if (threadIdx.x == 0) {
-    constexpr int S = BLK / kKeys;
-    int ne = cnt * S;
-    const int tail = T - (NT - 1) * BLK;
-    if (S == 2 && cnt > 0 && blist[cnt - 1] == NT - 1 && tail <= kKeys) ne -= 1;
-    tl.nexact = ne;
-  }
-  __syncthreads();
+  __syncthreads();  // the lists and counts are in LDS
   return tl.npool + tl.nexact;
 }
 
 // The last exact tile is ragged when block NT-1 is exact and T is not a
 // multiple of 64 (exact blocks are listed in ascending order).
-__device__ __forceinline__ int ragged_tiles(const TileList& tl, const int32_t* __restrict__ counts,
-                                            int64_t row, int NT, int T) {
-  const int cnt = min(max(counts[row], 0), NT);
-  return (tl.nexact > 0 && blist_lds()[cnt - 1] == NT - 1 && (T % kKeys) != 0) ? 1 : 0;
+__device__ __forceinline__ int ragged_tiles(const TileList& tl, int NT, int T) {
+  return (tl.nexact > 0 && tl.last == NT - 1 && (T % kKeys) != 0) ? 1 : 0;
 }
 
 // Pooled tile p.
@@ -643,7 +665,7 @@ __device__ __forceinline__ void store_rows(const SoftmaxState& st, uint16_t* __r
 // ------------------------------------------------------------ argument checks
 inline int check_fwd_common(const void* q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
                             const void* kc, const void* vc, int64_t npad, const int32_t* counts,
-                            const int16_t* lists, const uint32_t* mask, int64_t B, int64_t T,
+                            const uint32_t* mask, int64_t B, int64_t T,
                             int64_t H, int64_t D, int64_t block, const void* o, int64_t so_b,
                             int64_t so_t, int64_t so_h, const char* what) {
   SOLATTN_REQUIRE(D == kD, SOLATTN_EUNSUPPORTED, "%s: head_dim %lld != 128", what, (long long)D);
@@ -656,26 +678,26 @@ inline int check_fwd_common(const void* q, int64_t sq_b, int64_t sq_t, int64_t s
   SOLATTN_REQUIRE(B * H * NT < (1ll << 31), SOLATTN_EUNSUPPORTED, "%s: grid too large", what);
   SOLATTN_REQUIRE(npad >= cdiv(NT, 64) * 64, SOLATTN_EINVAL,
                   "%s: npad %lld must cover whole 64-block chunks", what, (long long)npad);
-  SOLATTN_REQUIRE(q && kc && vc && counts && lists && mask && o, SOLATTN_EINVAL, "%s: null pointer",
-                  what);
+  SOLATTN_REQUIRE(q && kc && vc && counts && mask && o, SOLATTN_EINVAL, "%s: null pointer", what);
   SOLATTN_REQUIRE(reinterpret_cast<uintptr_t>(q) % 16 == 0 && sq_b % 8 == 0 && sq_t % 8 == 0 &&
                       sq_h % 8 == 0,
                   SOLATTN_EINVAL, "%s: q must be 16-byte aligned with strides multiple of 8", what);
   SOLATTN_REQUIRE(reinterpret_cast<uintptr_t>(kc) % 16 == 0 && reinterpret_cast<uintptr_t>(vc) % 16 == 0,
                   SOLATTN_EINVAL, "%s: kc/vc must be 16-byte aligned", what);
-  SOLATTN_REQUIRE(reinterpret_cast<uintptr_t>(o) % 8 == 0 && so_b % 4 == 0 && so_t % 4 == 0 &&
-                      so_h % 4 == 0,
-                  SOLATTN_EINVAL, "%s: o must be 8-byte aligned with strides multiple of 4", what);
+  // store_rows writes each output row as 16-byte stores
+  SOLATTN_REQUIRE(reinterpret_cast<uintptr_t>(o) % 16 == 0 && so_b % 8 == 0 && so_t % 8 == 0 &&
+                      so_h % 8 == 0,
+                  SOLATTN_EINVAL, "%s: o must be 16-byte aligned with strides multiple of 8", what);
   return 0;
 }
 
 inline int check_fwd_args(const void* q, int64_t sq_b, int64_t sq_t, int64_t sq_h, const void* k,
                           int64_t sk_b, int64_t sk_t, int64_t sk_h, const void* v, int64_t sv_b,
                           int64_t sv_t, int64_t sv_h, const void* kc, const void* vc, int64_t npad,
-                          const int32_t* counts, const int16_t* lists, const uint32_t* mask,
+                          const int32_t* counts, const uint32_t* mask,
                           int64_t B, int64_t T, int64_t H, int64_t D, int64_t block, const void* o,
                           int64_t so_b, int64_t so_t, int64_t so_h, const char* what) {
-  if (int rc = check_fwd_common(q, sq_b, sq_t, sq_h, kc, vc, npad, counts, lists, mask, B, T, H, D,
+  if (int rc = check_fwd_common(q, sq_b, sq_t, sq_h, kc, vc, npad, counts, mask, B, T, H, D,
                                 block, o, so_b, so_t, so_h, what))
     return rc;
   SOLATTN_REQUIRE(k && v, SOLATTN_EINVAL, "%s: null k/v", what);

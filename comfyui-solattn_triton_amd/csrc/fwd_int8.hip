@@ -601,8 +601,7 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
                 const int8_t* __restrict__ vi, const float* __restrict__ vscale,
                 const uint16_t* __restrict__ v, int64_t sv_b, int64_t sv_t, int64_t sv_h,
                 int64_t TP, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
-                int64_t npad, const int32_t* __restrict__ counts, const int16_t* __restrict__ lists,
-                const uint32_t* __restrict__ mask, int T, int H, int NT, int W, float c,
+                int64_t npad, const int32_t* __restrict__ counts, const uint32_t* __restrict__ mask, int T, int H, int NT, int W, float c,
                 uint16_t* __restrict__ o, int64_t so_b, int64_t so_t, int64_t so_h, int kst,
                 int64_t ksh) {
   constexpr int NTHREADS = BLK * 2;
@@ -640,9 +639,9 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
   const int b = bh / H, h = bh % H;
   const int64_t row = static_cast<int64_t>(bh) * NT + qb;
 
-  const int ntiles = build_tile_list<BLK>(tl, counts, lists, mask, row, NT, W, T);
-  if (ntiles == 0) return;  // cannot happen for routed lists: the diagonal is exact
-  const int nrag = ragged_tiles(tl, counts, row, NT, T);
+  const int ntiles = build_tile_list<BLK>(tl, mask, row, NT, W, T);
+  if (ntiles == 0) return;  // cannot happen for routed masks: the diagonal is exact
+  const int nrag = ragged_tiles(tl, NT, T);
   const int nexact = tl.nexact;       // tiles [0, nexact): ragged first, then full
   const int nfast = nexact - nrag;    // tiles [nexact, ntiles): pooled
 
@@ -1066,7 +1065,7 @@ fwd_int8_b128_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t,
                      const int8_t* __restrict__ vi, const float* __restrict__ vscale,
                      int64_t TP, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
                      int64_t npad, const int32_t* __restrict__ counts,
-                     const int16_t* __restrict__ lists, const uint32_t* __restrict__ mask, int T,
+                     const uint32_t* __restrict__ mask, int T,
                      int H, int NT, int W, float c, uint16_t* __restrict__ o, int64_t so_b,
                      int64_t so_t, int64_t so_h, int kst, int64_t ksh) {
   constexpr int BLK = 128, NTHREADS = 256;
@@ -1082,13 +1081,12 @@ fwd_int8_b128_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t,
   const int b = bh / H, h = bh % H;
   const int64_t row = static_cast<int64_t>(bh) * NT + qb;
 
-  const int ntiles = build_tile_list<BLK>(tl, counts, lists, mask, row, NT, W, T);
-  if (ntiles == 0) return;  // cannot happen for routed lists: the diagonal is exact
+  const int ntiles = build_tile_list<BLK>(tl, mask, row, NT, W, T);
+  if (ntiles == 0) return;  // cannot happen for routed masks: the diagonal is exact
   const int nexact = tl.nexact;  // exact 64-key tiles, list order
-  const int cnt = min(max(counts[row], 0), NT);
   // full exact blocks: list entries [0, nfb); a ragged last block (T not a
   // multiple of 128) keeps its tiles [2 nfb, nexact) for the plain path
-  const int nfb = cnt - ((cnt > 0 && blist_lds()[cnt - 1] == NT - 1 && (T % BLK) != 0) ? 1 : 0);
+  const int nfb = tl.nblk - ((tl.last == NT - 1 && (T % BLK) != 0) ? 1 : 0);
 
   const int64_t bhD = (static_cast<int64_t>(b) * npad * H + h) * kD;
   const KVSource src{nullptr, 0, nullptr, 0, kc + bhD, static_cast<int64_t>(H) * kD, vc + bhD};
@@ -1238,12 +1236,12 @@ void launch_i8(uint32_t grid, hipStream_t s, const uint16_t* q, int64_t sq_b, in
                int64_t sq_h, const int8_t* qi, const float* qs, const int8_t* ki, const float* ks,
                const int8_t* vi, const float* vscale, const uint16_t* v, int64_t sv_b,
                int64_t sv_t, int64_t sv_h, int64_t TP, const uint16_t* kc, const uint16_t* vc,
-               int64_t npad, const int32_t* counts, const int16_t* lists, const uint32_t* mask,
+               int64_t npad, const int32_t* counts, const uint32_t* mask,
                int T, int H, int NT, int W, float c, uint16_t* o, int64_t so_b, int64_t so_t,
                int64_t so_h, int kst, int64_t ksh) {
   hipLaunchKernelGGL((fwd_int8_kernel<BLK, PV, UKS>), dim3(grid), dim3(BLK * 2), blist_lds_bytes(NT), s, q, sq_b, sq_t,
                      sq_h, qi, qs, ki, ks, vi, vscale, v, sv_b, sv_t, sv_h, TP, kc, vc, npad,
-                     counts, lists, mask, T, H, NT, W, c, o, so_b, so_t, so_h, kst, ksh);
+                     counts, mask, T, H, NT, W, c, o, so_b, so_t, so_h, kst, ksh);
 }
 
 template <int BLK, bool PV>
@@ -1251,12 +1249,11 @@ void launch_i8_ks(bool uks, uint32_t grid, hipStream_t s, const uint16_t* q, int
                   int64_t sq_t, int64_t sq_h, const int8_t* qi, const float* qs, const int8_t* ki,
                   const float* ks, const int8_t* vi, const float* vscale, const uint16_t* v,
                   int64_t sv_b, int64_t sv_t, int64_t sv_h, int64_t TP, const uint16_t* kc,
-                  const uint16_t* vc, int64_t npad, const int32_t* counts, const int16_t* lists,
-                  const uint32_t* mask, int T, int H, int NT, int W, float c, uint16_t* o,
+                  const uint16_t* vc, int64_t npad, const int32_t* counts, const uint32_t* mask, int T, int H, int NT, int W, float c, uint16_t* o,
                   int64_t so_b, int64_t so_t, int64_t so_h, int kst, int64_t ksh) {
   (uks ? launch_i8<BLK, PV, true> : launch_i8<BLK, PV, false>)(
       grid, s, q, sq_b, sq_t, sq_h, qi, qs, ki, ks, vi, vscale, v, sv_b, sv_t, sv_h, TP, kc, vc,
-      npad, counts, lists, mask, T, H, NT, W, c, o, so_b, so_t, so_h, kst, ksh);
+      npad, counts, mask, T, H, NT, W, c, o, so_b, so_t, so_h, kst, ksh);
 }
 
 }  // namespace int8fwd
@@ -1265,11 +1262,11 @@ int fwd_int8(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h, const 
              const float* qs, const int8_t* ki, const float* ks, const int8_t* vi,
              const float* vscale, const uint16_t* v, int64_t sv_b, int64_t sv_t, int64_t sv_h,
              int64_t TP, const uint16_t* kc, const uint16_t* vc, int64_t npad,
-             const int32_t* counts, const int16_t* lists, const uint32_t* mask, int64_t B,
+             const int32_t* counts, const uint32_t* mask, int64_t B,
              int64_t T, int64_t H, int64_t D, int64_t block, float scale, int int8_pv,
              uint16_t* o, int64_t so_b, int64_t so_t, int64_t so_h, solattn_stream_t stream,
              bool uniform_ks, bool ks_head_major) {
-  if (int rc = check_fwd_common(q, sq_b, sq_t, sq_h, kc, vc, npad, counts, lists, mask, B, T, H, D,
+  if (int rc = check_fwd_common(q, sq_b, sq_t, sq_h, kc, vc, npad, counts, mask, B, T, H, D,
                                 block, o, so_b, so_t, so_h, "fwd_int8"))
     return rc;
   SOLATTN_REQUIRE(TP >= T, SOLATTN_EINVAL, "fwd_int8: TP < T");
@@ -1297,13 +1294,13 @@ int fwd_int8(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h, const 
   const int64_t ksh = ks_head_major ? TP : 1;
 #define SOLATTN_I8_ARGS                                                                          \
   grid, s, q, sq_b, sq_t, sq_h, qi, qs, ki, ks, vi, vscale, v, sv_b, sv_t, sv_h, TP, kc, vc, npad, \
-      counts, lists, mask, static_cast<int>(T), static_cast<int>(H), static_cast<int>(NT), W, c, o, \
+      counts, mask, static_cast<int>(T), static_cast<int>(H), static_cast<int>(NT), W, c, o, \
       so_b, so_t, so_h, kst, ksh
   if (block == 128) {
     if (int8_pv)
       hipLaunchKernelGGL(uniform_ks ? int8fwd::fwd_int8_b128_kernel<true> : int8fwd::fwd_int8_b128_kernel<false>,
                          dim3(grid), dim3(256), blist_lds_bytes(NT), s, q, sq_b, sq_t, sq_h, qi, qs,
-                         ki, ks, vi, vscale, TP, kc, vc, npad, counts, lists, mask,
+                         ki, ks, vi, vscale, TP, kc, vc, npad, counts, mask,
                          static_cast<int>(T), static_cast<int>(H), static_cast<int>(NT), W, c, o,
                          so_b, so_t, so_h, kst, ksh);
     else int8fwd::launch_i8_ks<128, false>(uniform_ks, SOLATTN_I8_ARGS);
@@ -1322,12 +1319,12 @@ extern "C" int solattn_fwd_int8(const uint16_t* q, int64_t sq_b, int64_t sq_t, i
                                 const float* ks, const int8_t* vi, const float* vscale,
                                 const uint16_t* v, int64_t sv_b, int64_t sv_t, int64_t sv_h,
                                 int64_t TP, const uint16_t* kc, const uint16_t* vc, int64_t npad,
-                                const int32_t* counts, const int16_t* lists, const uint32_t* mask,
+                                const int32_t* counts, const uint32_t* mask,
                                 int64_t B, int64_t T, int64_t H, int64_t D, int64_t block,
                                 float scale, int int8_pv, uint16_t* o, int64_t so_b, int64_t so_t,
                                 int64_t so_h, solattn_stream_t stream) {
   solattn::clear_error();
   return solattn::fwd_int8(q, sq_b, sq_t, sq_h, qi, qs, ki, ks, vi, vscale, v, sv_b, sv_t, sv_h,
-                           TP, kc, vc, npad, counts, lists, mask, B, T, H, D, block, scale,
+                           TP, kc, vc, npad, counts, mask, B, T, H, D, block, scale,
                            int8_pv, o, so_b, so_t, so_h, stream, false);
 }

@@ -2,14 +2,14 @@
 //
 // Built with -ffp-contract=off: every fp32 operation below is rounded exactly
 // where it is written, so the CPU oracle (oracle/solattn_oracle.c) reproduces
-// kc, vc, qbar, thresholds and routing lists bit for bit.
+// kc, vc, qbar, thresholds and routing masks bit for bit.
 //
 //  pool    one pass over q, k, v: four waves per (block, tensor, 4 heads),
 //          wave w summing rows w (mod 4), each lane 8 channels of one head in
 //          16-byte loads; HBM-bound; optionally quantises Q on the way (the
 //          INT8 path).
 //  moments per-head kc mean / variance over blocks (+ INT8 centring, V scale).
-//  route   thresholds, scores R[i][j] and per-query-block exact lists / masks.
+//  route   thresholds, scores R[i][j], per-query-block exact masks and counts.
 #include <algorithm>
 
 #include "common.hpp"
@@ -331,8 +331,7 @@ route_kernel(const float* __restrict__ qbar, const uint16_t* __restrict__ kc, in
              const float* __restrict__ kc_mean, const float* __restrict__ kc_var, int H, int NT,
              int W, float c, float c2, float tau, int mode, int64_t skv_lo, int64_t skv_hi,
              int64_t sq_lo, int64_t sq_hi, float* __restrict__ thr_out,
-             int32_t* __restrict__ counts, int16_t* __restrict__ lists,
-             uint32_t* __restrict__ mask) {
+             int32_t* __restrict__ counts, uint32_t* __restrict__ mask) {
   constexpr int kRouteRows = kRouteThreads / TPR;  // kc rows staged per chunk
   constexpr int kQH = kQB / TPR;                   // query blocks per thread
   constexpr int kKcLoads = kRouteRows * (kHeadDim / 8) / kRouteThreads;  // 16-byte loads per thread
@@ -469,7 +468,7 @@ route_kernel(const float* __restrict__ qbar, const uint16_t* __restrict__ kc, in
   }
   __syncthreads();
 
-  // Masks and ascending lists, one query block per wave at a time.
+  // Masks and exact-block counts, one query block per wave at a time.
   for (int i = wave; i < kQB; i += kRouteThreads / 64) {
     const int qi = i0 + i;
     if (qi >= NT) break;
@@ -479,21 +478,10 @@ route_kernel(const float* __restrict__ qbar, const uint16_t* __restrict__ kc, in
       const int w = w0 + lane;
       const uint32_t word = w < W ? smask(i, w) : 0u;
       if (w < W) mask[row * W + w] = word;
-      const int cnt = __popc(word);
-      int incl = cnt;
+      int cnt = __popc(word);
 #pragma unroll
-      for (int s = 1; s < 64; s <<= 1) {
-        const int y = __shfl_up(incl, s);
-        if (lane >= s) incl += y;
-      }
-      int off = base + incl - cnt;
-      uint32_t bits = word;
-      while (bits) {
-        const int bit = __ffs(bits) - 1;
-        bits &= bits - 1;
-        lists[row * NT + off++] = static_cast<int16_t>(w * 32 + bit);
-      }
-      base += __shfl(incl, 63);
+      for (int s = 32; s >= 1; s >>= 1) cnt += __shfl_xor(cnt, s);
+      base += cnt;
     }
     if (lane == 0) counts[row] = base;
   }
@@ -604,8 +592,8 @@ extern "C" int solattn_route(const float* qbar, const uint16_t* kc, int64_t npad
                              const float* kc_mean, const float* kc_var, int64_t B, int64_t T,
                              int64_t H, int64_t D, int64_t block, float scale, float tau, int mode,
                              int64_t sink_kv_lo, int64_t sink_kv_hi, int64_t sink_q_lo,
-                             int64_t sink_q_hi, float* thr, int32_t* counts, int16_t* lists,
-                             uint32_t* mask, solattn_stream_t stream) {
+                             int64_t sink_q_hi, float* thr, int32_t* counts, uint32_t* mask,
+                             solattn_stream_t stream) {
   clear_error();
   SOLATTN_REQUIRE(D == kHeadDim, SOLATTN_EUNSUPPORTED, "route: head_dim %lld != 128", (long long)D);
   SOLATTN_REQUIRE(block > 0 && B > 0 && T > 0 && H > 0 && B <= 65535 && H <= 65535,
@@ -616,7 +604,7 @@ extern "C" int solattn_route(const float* qbar, const uint16_t* kc, int64_t npad
                   (long long)NT, kMaxWords * 32);
   SOLATTN_REQUIRE(npad >= NT, SOLATTN_EINVAL, "route: npad < NT");
   SOLATTN_REQUIRE(mode == 0 || mode == 1, SOLATTN_EINVAL, "route: mode %d", mode);
-  SOLATTN_REQUIRE(qbar && kc && kc_var && (mode == 1 || kc_mean) && thr && counts && lists && mask,
+  SOLATTN_REQUIRE(qbar && kc && kc_var && (mode == 1 || kc_mean) && thr && counts && mask,
                   SOLATTN_EINVAL, "route: null pointer");
   SOLATTN_REQUIRE(reinterpret_cast<uintptr_t>(kc) % 16 == 0, SOLATTN_EINVAL,
                   "route: kc must be 16-byte aligned");
@@ -629,6 +617,6 @@ extern "C" int solattn_route(const float* qbar, const uint16_t* kc, int64_t npad
                      reinterpret_cast<hipStream_t>(stream), qbar, kc, npad,
                      mode == 0 ? kc_mean : kc_var, kc_var, static_cast<int>(H),
                      static_cast<int>(NT), static_cast<int>(W), c, c2, tau, mode, sink_kv_lo,
-                     sink_kv_hi, sink_q_lo, sink_q_hi, thr, counts, lists, mask);
+                     sink_kv_hi, sink_q_lo, sink_q_hi, thr, counts, mask);
   return check_launch("route");
 }

@@ -24,7 +24,7 @@
  *    cost of a D = 128 call.
  *
  * Arithmetic contract (the CPU oracle restates the same operation order, so
- * pooled keys, thresholds, routing lists and INT8 codes are bit-exact):
+ * pooled keys, thresholds, routing masks and INT8 codes are bit-exact):
  *  - pooled sums: for each (block, channel) four fp32 partial sums over rows
  *    r = 0,4,8.. / 1,5,9.. / 2,6,.. / 3,7,.. taken in ascending order (rows past
  *    T add 0.0f), combined as (p0 + p1) + (p2 + p3).
@@ -116,7 +116,7 @@ int solattn_moments(uint16_t* kc, int64_t npad, int64_t B, int64_t NT, int64_t H
                     const float* vamax_part, float* vscale, solattn_stream_t stream);
 
 /* ----------------------------------------------------------------- route --
- * Thresholds, routing decisions and per-query-block exact lists.
+ * Thresholds, routing decisions and per-query-block exact-block masks.
  *   mode 0 (BF16, /root/reference/_preprocess.py:150-163):
  *     mu  = (fmaf chain qbar*kc_mean) * c
  *     var = (fmaf chain (qbar*qbar)*kc_var) * (c*c)
@@ -127,14 +127,15 @@ int solattn_moments(uint16_t* kc, int64_t npad, int64_t B, int64_t NT, int64_t H
  *   exact(i, j) = i in [sink_q_lo, sink_q_hi) ? 1
  *               : R > thr || |i - j| <= 1 || j in [sink_kv_lo, sink_kv_hi)
  *   (the forward's rule, /root/reference/_tri_fwd.py:279-286).
- * Outputs: thr fp32 [B, NT, H]; counts int32 [B, H, NT]; lists int16
- * [B, H, NT, NT] (ascending exact j, first counts[] entries valid); mask
- * uint32 [B, H, NT, ceil(NT/32)] (bit j%32 of word j/32 = exact). */
+ * Outputs: thr fp32 [B, NT, H]; counts int32 [B, H, NT] (exact blocks per
+ * query block); mask uint32 [B, H, NT, ceil(NT/32)] (bit j%32 of word j/32 =
+ * exact; bits j >= NT are 0). The reference keeps no list either: it re-derives
+ * the decisions in every forward program. */
 int solattn_route(const float* qbar, const uint16_t* kc, int64_t npad, const float* kc_mean,
                   const float* kc_var, int64_t B, int64_t T, int64_t H, int64_t D,
                   int64_t block, float scale, float tau, int mode, int64_t sink_kv_lo,
                   int64_t sink_kv_hi, int64_t sink_q_lo, int64_t sink_q_hi, float* thr,
-                  int32_t* counts, int16_t* lists, uint32_t* mask, solattn_stream_t stream);
+                  int32_t* counts, uint32_t* mask, solattn_stream_t stream);
 
 /* ----------------------------------------------------------------- quant --
  * Per-token INT8 of a BTHD bf16 tensor, optionally smoothed by mean [B, H, D]:
@@ -173,17 +174,19 @@ int solattn_quant_v(const uint16_t* v, int64_t sv_b, int64_t sv_t, int64_t sv_h,
  * Sparse attention over exact blocks (flash attention on MFMA) plus the pooled
  * branch (one pooled key kc_j and value vc_j per approximate block, softmax
  * weight times len_j), one online softmax per query row.
- * counts/lists/mask come from solattn_route for the same B, T, H and block:
- * the kernels clamp counts to [0, NT] but take list entries (block indices in
- * [0, NT), ascending) and mask bits as given, so other contents read K/V rows
- * outside the tensors. o: bf16, element (b, t, h, d) at
- * o + b*so_b + t*so_t + h*so_h + d; rows t >= T are not written.
+ * counts/mask come from solattn_route for the same B, T, H and block. Each
+ * workgroup builds its tile list from its mask row (mask bits at or past NT
+ * are ignored, so any mask contents stay inside the tensors); counts only
+ * order the dispatch (longest query blocks first). o: bf16, element
+ * (b, t, h, d) at o + b*so_b + t*so_t + h*so_h + d, 16-byte aligned with
+ * strides multiples of 8 elements (rows are written as 16-byte stores); rows
+ * t >= T are not written.
  * Replaces: _forward_ptr + sol_attn, /root/reference/_tri_fwd.py:215-410. */
 int solattn_fwd_bf16(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
                      const uint16_t* k, int64_t sk_b, int64_t sk_t, int64_t sk_h,
                      const uint16_t* v, int64_t sv_b, int64_t sv_t, int64_t sv_h,
                      const uint16_t* kc, const uint16_t* vc, int64_t npad,
-                     const int32_t* counts, const int16_t* lists, const uint32_t* mask,
+                     const int32_t* counts, const uint32_t* mask,
                      int64_t B, int64_t T, int64_t H, int64_t D, int64_t block, float scale,
                      uint16_t* o, int64_t so_b, int64_t so_t, int64_t so_h,
                      solattn_stream_t stream);
@@ -210,7 +213,7 @@ int solattn_fwd_int8(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h
                      const int8_t* vi, const float* vscale, const uint16_t* v, int64_t sv_b,
                      int64_t sv_t, int64_t sv_h, int64_t TP, const uint16_t* kc,
                      const uint16_t* vc, int64_t npad, const int32_t* counts,
-                     const int16_t* lists, const uint32_t* mask, int64_t B, int64_t T,
+                     const uint32_t* mask, int64_t B, int64_t T,
                      int64_t H, int64_t D, int64_t block, float scale, int int8_pv,
                      uint16_t* o, int64_t so_b, int64_t so_t, int64_t so_h,
                      solattn_stream_t stream);

@@ -17,6 +17,12 @@ def u32(t: torch.Tensor) -> np.ndarray:
     return t.detach().cpu().numpy().view(np.uint32)
 
 
+def mask_bits(mask_u32: np.ndarray, NT: int) -> np.ndarray:
+    """Routing bitmask [..., W] uint32 -> bool [..., NT] (bit j%32 of word j/32)."""
+    bits_ = (mask_u32[..., :, None] >> np.arange(32, dtype=np.uint32)) & 1
+    return bits_.reshape(*mask_u32.shape[:-1], -1)[..., :NT].astype(bool)
+
+
 def cosine(a, b) -> float:
     a = np.asarray(a, np.float64).ravel()
     b = np.asarray(b, np.float64).ravel()

@@ -35,7 +35,7 @@ def test_exports_every_declared_symbol(capi):
 
 
 def test_abi_version(capi):
-    assert capi.abi_version() >> 16 == 1
+    assert capi.abi_version() >> 16 == 2  # 2: routing masks only, no int16 block lists
 
 
 def test_errors_are_reported(capi):
@@ -45,18 +45,18 @@ def test_errors_are_reported(capi):
     rc = L.solattn_pool(null, 0, 0, 0, null, 0, 0, 0, null, 0, 0, 0, 1, 100, 1, 64, 64,
                         null, null, 64, null, null, null)
     assert rc == -2 and b"head_dim" in L.solattn_last_error()
-    rc = L.solattn_fwd_bf16(*([null, 0, 0, 0] * 3), null, null, 64, null, null, null,
+    rc = L.solattn_fwd_bf16(*([null, 0, 0, 0] * 3), null, null, 64, null, null,
                             1, 100, 1, 128, 96, 0.1, null, 0, 0, 0, null)
     assert rc == -2 and b"block" in L.solattn_last_error()
     rc = L.solattn_route(null, null, 1, null, null, 1, 10, 1, 128, 64, 0.1, 1.0, 0, 0, 0, 0, 0,
-                         null, null, null, null, null)
+                         null, null, null, null)
     assert rc == -1
     # more than 16384 query blocks: rejected as unsupported (the node keeps such calls dense)
-    rc = L.solattn_fwd_bf16(*([null, 0, 0, 0] * 3), null, null, 16448, null, null, null,
+    rc = L.solattn_fwd_bf16(*([null, 0, 0, 0] * 3), null, null, 16448, null, null,
                             1, 16385 * 64, 1, 128, 64, 0.1, null, 0, 0, 0, null)
     assert rc == -2 and b"exceed" in L.solattn_last_error()
     rc = L.solattn_route(null, null, 16448, null, null, 1, 16385 * 64, 1, 128, 64, 0.1, 1.0, 0,
-                         0, 0, 0, 0, null, null, null, null, null)
+                         0, 0, 0, 0, null, null, null, null)
     assert rc == -2 and b"exceed" in L.solattn_last_error()
     with pytest.raises(capi.SolAttnError, match="null pointer"):
         capi.call("solattn_reorder_rows", null, 1, 0, 16, null, 0, 16, 1, 1, 16, null, null)
@@ -110,11 +110,44 @@ def test_workspace_bytes(capi):
     L = capi.LIB
     b0 = L.solattn_sol_attn_workspace_bytes(1, 32760, 24, 128, 128, 0)
     b1 = L.solattn_sol_attn_workspace_bytes(1, 32760, 24, 128, 128, 1)
-    NT, npad = 256, 256
-    floor = 2 * npad * 24 * 128 * 2 + 24 * NT * NT * 2
+    NT, npad, W = 256, 256, 8
+    floor = 2 * npad * 24 * 128 * 2 + 24 * NT * 128 * 4 + 24 * NT * W * 4
     assert b0 >= floor and b1 > b0 + 3 * 32760 * 24 * 128
     assert b0 % 256 == 0
     assert L.solattn_sol_attn_workspace_bytes(0, 10, 1, 128, 64, 0) == 0
+
+
+def test_workspace_has_no_block_lists(capi):
+    """Routing is carried by the bitmask alone (NT^2 bits per head): at the
+    kernels' 16384 blocks per head the BF16 workspace is far below what
+    int16 lists (NT^2 x 2 bytes per head, 512 MiB) would need on their own."""
+    L = capi.LIB
+    for block in (64, 128):
+        NT = 16384
+        T = NT * block
+        ws = L.solattn_sol_attn_workspace_bytes(1, T, 1, 128, block, 0)
+        lists = NT * NT * 2
+        mask = NT * (NT // 32) * 4
+        assert mask <= ws < lists / 10, (block, ws)
+
+
+def test_fwd_rejects_misaligned_output(capi):
+    """Output rows are written as 16-byte stores: an o that is only 8-byte
+    aligned, or whose strides are not multiples of 8 elements, is refused
+    before any launch (the pointers are never dereferenced)."""
+    L = capi.LIB
+    a = 1 << 20  # a 256-byte-aligned stand-in address; nothing is launched
+    T, H = 1000, 2
+    st, sb = H * 128, 1000 * H * 128
+    args = lambda o, so_t: ([a, sb, st, 128] * 3 + [a, a, 64, a, a, 1, T, H, 128, 64, 0.1]  # noqa: E731
+                            + [o, sb, so_t, 128, None])
+    for o, so_t in ((a + 8, st), (a, st + 4)):
+        rc = L.solattn_fwd_bf16(*args(o, so_t))
+        assert rc == -1 and b"16-byte aligned" in L.solattn_last_error()
+    int8 = [a, sb, st, 128, a, a, a, a, None, None, a, sb, st, 128, T, a, a, 64, a, a, 1, T, H,
+            128, 64, 0.1, 0, a + 8, sb, st, 128, None]
+    rc = L.solattn_fwd_int8(*int8)
+    assert rc == -1 and b"16-byte aligned" in L.solattn_last_error()
 
 
 def test_host_morton(capi):

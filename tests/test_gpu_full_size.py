@@ -4,7 +4,7 @@ synthetic smooth-field inputs ``bench.py`` times), at block 128 (the
 benchmark's) and block 64.
 
 The permutation and the whole routing state (pooled keys, thresholds, counts,
-lists, bitmask) are compared with the oracle bit for bit over every head and
+bitmask and the exact lists it encodes) are compared with the oracle bit for bit over every head and
 query block; the forward outputs are compared with the oracle's restatement of
 the reference loop on a seeded sample of query blocks (the oracle is a scalar
 loop; 96 BF16 and 32 INT8 query blocks take seconds). The small-case tests
@@ -21,7 +21,7 @@ import torch
 
 import bench
 import oracle
-from _util import bits, check_int8_blocks, compare_rows, u32
+from _util import bits, check_int8_blocks, compare_rows, mask_bits, u32
 
 pytestmark = pytest.mark.gpu
 
@@ -56,10 +56,13 @@ def _route_equal(r, ref):
     assert np.array_equal(r.threshold.cpu().numpy().view(np.uint32), ref["thr"].view(np.uint32))
     assert np.array_equal(r.counts.cpu().numpy(), ref["counts"])
     assert np.array_equal(u32(r.mask), ref["mask"])
-    lists = r.lists.cpu().numpy()
+    # the ascending exact lists the forwards build from the mask rows
+    ex = mask_bits(u32(r.mask), NT)
+    assert np.array_equal(ex.sum(-1), ref["counts"])
     n = ref["counts"]
     valid = np.arange(NT)[None, None, None, :] < n[..., None]
-    assert np.array_equal(np.where(valid, lists, 0), np.where(valid, ref["lists"], 0))
+    order = np.argsort(~ex, axis=-1, kind="stable")  # exact blocks first, ascending
+    assert np.array_equal(np.where(valid, order, 0), np.where(valid, ref["lists"], 0))
 
 
 def _near_ties(ref, ulps=8):
@@ -94,10 +97,12 @@ def test_full_size_bf16(pkg, dev, video, block):
           f"{density:.3f}; {ties} of {pairs} decisions within 8 ulp of the threshold", flush=True)
     rows = _sample_rows(cfg["H"], ref["NT"], 96, seed=5)
     port = oracle.forward_port(qb, kb, vb, ref, rows)
-    err, cos = compare_rows(out.float().cpu().numpy(), port, block)
+    got = out.float().cpu().numpy()
+    err, cos = compare_rows(got, port, block)
+    worst = min(cosine_rows(got, port, block))
     print(f"[full size bf16 block {block}] {len(rows)} query blocks: max|err|={err:.3e} "
-          f"cos={cos:.6f}", flush=True)
-    assert err < BF16_MAXABS and cos >= BF16_COS
+          f"cos={cos:.6f}, worst block cos {worst:.6f}", flush=True)
+    assert err < BF16_MAXABS and cos >= BF16_COS and worst >= BF16_COS
 
 
 INT8_CASES = [  # (block, tau): BASELINE config 3 sweeps tau at block 128
@@ -231,34 +236,60 @@ def cosine_rows(got, port, block):
 
 def test_full_size_long_video(pkg, dev):
     """cfg 4 (B=1, H=40, N=75600 from 21x60x60, block 128: 591 blocks per head,
-    an 80-token last block, a grid of 23640 workgroups): routing bit-exact over
-    every query block, BF16 and INT8 (int8 P.V) forwards on sampled query
-    blocks, including the ragged last one, against the oracle loops."""
+    an 80-token last block, a grid of 23640 workgroups), the whole pipeline:
+    Morton reorder -> routing (bit-exact over every query block) -> BF16 and
+    INT8 forwards (int8 P.V, bf16 P.V and the per-128-token-block variant) on
+    sampled query blocks, including the ragged last one, against the oracle
+    loops -> inverse reorder of the output, against the oracle's inverse."""
     pre = importlib.import_module(f"{pkg.__name__}._preprocess")
     tri = importlib.import_module(f"{pkg.__name__}._tri_fwd")
     fp = importlib.import_module(f"{pkg.__name__}._fused_prep")
     i8 = importlib.import_module(f"{pkg.__name__}._int8_fwd")
+    mort = importlib.import_module(f"{pkg.__name__}._morton")
     cfg, (q, k, v), (qb, kb, vb) = _inputs(pkg, dev, 4)
     block, tau = cfg["block"], cfg["tau"]
     r = pre.route(q, k, v, scale=128 ** -0.5, tau=tau, block=block)
     out = tri.sol_attn(q, k, v, tau=tau, block=block)
+    # inverse reorder of the output back to raster order (the pipeline's last step)
+    _, inv = mort.morton_perm(cfg["grid"], dev, "3d")
+    back = mort.reorder_tokens(out, inv, dim=1)
     torch.cuda.synchronize()
+    _, ref_inv = oracle.morton_perm(cfg["grid"], "3d")
+    assert np.array_equal(bits(back), bits(out)[:, ref_inv])
+    del back
     ref = oracle.prepare(qb, kb, vb, block=block, tau=tau)
     _route_equal(r, ref)
     NT = ref["NT"]
     rows = _sample_rows(cfg["H"], NT, 32, seed=7) + [(0, 0, NT - 1), (0, cfg["H"] - 1, NT - 1)]
     port = oracle.forward_port(qb, kb, vb, ref, rows)
-    err, cos = compare_rows(out.float().cpu().numpy(), port, block)
-    print(f"[full size cfg4 bf16] routing bit-exact; {len(rows)} query blocks: "
-          f"max|err|={err:.3e} cos={cos:.6f}", flush=True)
-    assert err < BF16_MAXABS and cos >= BF16_COS
-    del out, port, ref
+    got = out.float().cpu().numpy()
+    err, cos = compare_rows(got, port, block)
+    worst = min(cosine_rows(got, port, block))
+    print(f"[full size cfg4 bf16] routing bit-exact, inverse reorder bit-exact; {len(rows)} "
+          f"query blocks: max|err|={err:.3e} cos={cos:.6f}, worst block cos {worst:.6f}",
+          flush=True)
+    assert err < BF16_MAXABS and cos >= BF16_COS and worst >= BF16_COS
+    del out, port, ref, got
     r8, qi, qs, ki, ks, vi = fp.fused_preprocess_routing(q, k, v, tau=tau, scale=128 ** -0.5,
                                                          block=block)
-    out8 = i8.forward_int8(q, v, r8, qi, qs, ki, ks, vi, int8_pv=True)
-    torch.cuda.synchronize()
     ref8 = oracle.prepare(qb, kb, vb, block=block, tau=tau, int8=True, int8_pv=True)
     _route_equal(r8, ref8)
+    T = ref8["T"]
+    for name, mine in (("qi", qi), ("ki", ki), ("vi", vi)):
+        assert np.array_equal(mine[:, :T].cpu().numpy(), ref8[name][:, :T]), name
     rows8 = rows[::3] + rows[-2:]
-    check_int8_blocks("full size cfg4 int8", out8.float().cpu().numpy(), qb, vb, ref8, rows8, True,
-                      block)
+    for pv in (True, False):
+        out8 = i8.forward_int8(q, v, r8, qi, qs, ki, ks, vi, int8_pv=pv)
+        one = i8.sol_attn_int8(q, k, v, tau=tau, block=block, int8_pv=pv)
+        torch.cuda.synchronize()
+        assert torch.equal(one.view(torch.int16), out8.view(torch.int16))
+        check_int8_blocks(f"full size cfg4 int8 pv={pv}", out8.float().cpu().numpy(), qb, vb,
+                          ref8, rows8, pv, block)
+        del out8, one
+    del r8, qi, qs, ki, ks, vi, ref8
+    outb = i8.sol_attn_int8(q, k, v, tau=tau, block=block, int8_pv=True, quant_block=128)
+    refb = oracle.prepare(qb, kb, vb, block=block, tau=tau, int8=True, int8_pv=True,
+                          quant_block=128)
+    torch.cuda.synchronize()
+    check_int8_blocks("full size cfg4 int8 quant_block 128", outb.float().cpu().numpy(), qb, vb,
+                      refb, rows8, True, block)

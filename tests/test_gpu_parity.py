@@ -11,7 +11,7 @@ import pytest
 import torch
 
 import oracle
-from _util import bits, check_int8_blocks, compare_rows, cosine, randn_bf16, u32
+from _util import bits, check_int8_blocks, compare_rows, cosine, mask_bits, randn_bf16, u32
 
 pytestmark = pytest.mark.gpu
 
@@ -54,12 +54,14 @@ def test_route_bit_exact(pkg, dev, case, int8):
     assert np.array_equal(r.threshold.cpu().numpy().view(np.uint32), ref["thr"].view(np.uint32))
     assert np.array_equal(r.counts.cpu().numpy(), ref["counts"])
     assert np.array_equal(u32(r.mask), ref["mask"])
-    lists = r.lists.cpu().numpy()
+    # the forwards build each query block's ascending exact list from its mask row
+    ex = mask_bits(u32(r.mask), NT)
+    assert np.array_equal(ex.sum(-1), ref["counts"])
     for b in range(B):
         for h in range(H):
             for i in range(NT):
                 n = ref["counts"][b, h, i]
-                assert np.array_equal(lists[b, h, i, :n], ref["lists"][b, h, i, :n])
+                assert np.array_equal(np.nonzero(ex[b, h, i])[0], ref["lists"][b, h, i, :n])
     if int8:
         assert np.array_equal(r.vscale.cpu().numpy().view(np.uint32), ref["vscale"].view(np.uint32))
 

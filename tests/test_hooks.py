@@ -273,3 +273,32 @@ def test_h3_grid_mismatch_keeps_order(h3):
     assert all(r is model.seen[0] for r in model.seen)  # not reordered
     torch.testing.assert_close(out, mod.H3()._forward(x, None, None, layout_args=(64, 3, 8, 12, 10)),
                                rtol=0, atol=0)
+
+
+def test_hooks_on_host_tensors_use_index_select(pkg):
+    """With Morton on and the pass's tensors on the host, the hooks' own gather
+    (not the kernel, which needs device tensors) permutes them: the Wan and H3
+    stand-ins give the un-hooked outputs, and the blocks saw permuted tables."""
+    wan = importlib.import_module(f"{pkg.__name__}._morton")
+    h3 = importlib.import_module(f"{pkg.__name__}._morton_h3")
+    grid = (2, 4, 6)
+    model = WanModel(2)
+    wan.install_wan_morton(model)
+    x, freqs = _wan_inputs(grid, seed=3)
+    plain = WanModel(2)(x, freqs, {})
+    hooked = model(x, freqs, {"grid_sizes": grid, "sol_morton": True, "sol_morton_curve": "3d"})
+    perm, _ = wan.morton_perm(grid, "cpu", "3d")
+    assert all(torch.equal(f, freqs[:, perm]) for f in model.seen)
+    torch.testing.assert_close(hooked, plain, rtol=1e-6, atol=1e-6)
+
+    mod = _h3_module()
+    m3 = mod.H3()
+    h3.install_h3_morton(m3)
+    layout_args = (37, 4, 16, 16, 10)
+    x3 = torch.randn(37 + 10 + 256, 8, generator=torch.Generator().manual_seed(4))
+    ref3 = mod.H3()._forward(x3, None, None, layout_args=layout_args)
+    out3 = m3._forward(x3, None, None, transformer_options={"sol_morton": True, "sol_block_size": 64},
+                       layout_args=layout_args)
+    table = mod.H3().rope_freqs(torch.arange(x3.shape[0]), "cpu")
+    assert m3.seen and not torch.equal(m3.seen[0], table)  # the blocks saw the permuted table
+    torch.testing.assert_close(out3, ref3, rtol=1e-6, atol=1e-6)
