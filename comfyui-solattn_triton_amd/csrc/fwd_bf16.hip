@@ -78,10 +78,10 @@ __device__ __forceinline__ void fast_step(SoftmaxState& st, f32x16 (&sc)[2], f32
     if (__any(m_new != st.m)) {  // lanes whose max stays recompute the same P
       st.m = m_new;
       psum = 0.f;
-      psum = exp8_f32sum<0>(sc[0], c, -m_new, pb[0], psum);
-      psum = exp8_f32sum<8>(sc[0], c, -m_new, pb[1], psum);
-      psum = exp8_f32sum<0>(sc[1], c, -m_new, pb[2], psum);
-      psum = exp8_f32sum<8>(sc[1], c, -m_new, pb[3], psum);
+      psum = exp8<0>(sc[0], c, -m_new, pb[0], psum);
+      psum = exp8<8>(sc[0], c, -m_new, pb[1], psum);
+      psum = exp8<0>(sc[1], c, -m_new, pb[2], psum);
+      psum = exp8<8>(sc[1], c, -m_new, pb[3], psum);
       mfma_fence(st.acc);  // the rescale reads O
       rescale(st, alpha);
     }
@@ -196,10 +196,10 @@ __device__ __forceinline__ void step3(SoftmaxState& st, const f32x16 (&sc)[2], f
     if (__any(m_new != st.m)) {  // lanes whose max stays recompute the same P
       st.m = m_new;
       psum = 0.f;
-      psum = exp8_f32sum<0>(sc[0], c, -m_new, pn[0], psum);
-      psum = exp8_f32sum<8>(sc[0], c, -m_new, pn[1], psum);
-      psum = exp8_f32sum<0>(sc[1], c, -m_new, pn[2], psum);
-      psum = exp8_f32sum<8>(sc[1], c, -m_new, pn[3], psum);
+      psum = exp8<0>(sc[0], c, -m_new, pn[0], psum);
+      psum = exp8<8>(sc[0], c, -m_new, pn[1], psum);
+      psum = exp8<0>(sc[1], c, -m_new, pn[2], psum);
+      psum = exp8<8>(sc[1], c, -m_new, pn[3], psum);
       if constexpr (PV) mfma_fence(st.acc);  // the rescale reads O
       rescale(st, alpha);
     }

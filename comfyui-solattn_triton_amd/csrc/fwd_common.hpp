@@ -482,10 +482,12 @@ __device__ __forceinline__ void mfma_fence(f32x16 (&x)[N]) {
   else
     asm volatile("s_nop 7\n\ts_nop 7" : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]));
 }
-// p = exp2(s*c + neg) for two scores, packed to bf16 (round to nearest even),
-// both added to the row sum in fp32 (the reference sums the fp32 p,
-// /root/reference/_tri_fwd.py:330). The s_nop covers the one wait state a
-// transcendental result needs before a VALU reads it.
+// p = exp2(s*c + neg) for two scores, packed to bf16 (round to nearest even)
+// and added to the row sum as packed, one v_dot2_f32_bf16 against (1, 1): the
+// denominator is the sum of the P that the P.V MFMA multiplies (the
+// reference sums the fp32 p, /root/reference/_tri_fwd.py:330; the difference
+// is the bf16 rounding of P, already in the numerator). The s_nop covers the
+// one wait state a transcendental result needs before a VALU reads it.
 __device__ __forceinline__ uint32_t exp_pair(float s0, float s1, float c, float neg, float& sum) {
   uint32_t p;
   float t0, t1;
@@ -496,28 +498,11 @@ __device__ __forceinline__ uint32_t exp_pair(float s0, float s1, float c, float 
       "v_exp_f32 %3, %3\n\t"
       "s_nop 0\n\t"
       "v_cvt_pk_bf16_f32 %0, %2, %3\n\t"
-      "v_add_f32 %1, %1, %2\n\t"
-      "v_add_f32 %1, %1, %3"
-      : "=v"(p), "+v"(sum), "=&v"(t0), "=&v"(t1)
-      : "v"(s0), "v"(s1), "v"(c), "v"(neg));
+      "v_dot2_f32_bf16 %1, %0, %8, %1"
+      : "=&v"(p), "+v"(sum), "=&v"(t0), "=&v"(t1)
+      : "v"(s0), "v"(s1), "v"(c), "v"(neg), "s"(0x3F803F80u));
   return p;
 }
-// The same arithmetic in plain code (the rare paths): P words of S elements
-// [R0, R0 + 8) into pk, fp32 row sum.
-template <int R0>
-__device__ __forceinline__ float exp8_f32sum(const f32x16& s, float c, float neg, bf16x8& pk,
-                                             float sum) {
-#pragma unroll
-  for (int e = 0; e < 8; e += 2) {
-    const float p0 = __builtin_amdgcn_exp2f(fmaf(s[R0 + e], c, neg));
-    const float p1 = __builtin_amdgcn_exp2f(fmaf(s[R0 + e + 1], c, neg));
-    pk[e] = static_cast<__bf16>(p0);
-    pk[e + 1] = static_cast<__bf16>(p1);
-    sum = (sum + p0) + p1;
-  }
-  return sum;
-}
-
 // ------------------------------------------------------------ online softmax
 struct SoftmaxState {
   float m;          // running max, in the exp2 domain (score * c)
@@ -553,7 +538,8 @@ __device__ __forceinline__ float new_max(float m_old, float m_tile, float& alpha
 }
 
 // p = exp2(s*c + neg) for elements [R0, R0 + 8) of s, packed to bf16 into pk;
-// the row sum accumulates the packed values (v_dot2 with ones).
+// the row sum accumulates the packed values (v_dot2 with ones), as exp_pair
+// (the plain path and the pipelined steps' rare recompute).
 template <int R0>
 __device__ __forceinline__ float exp8(const f32x16& s, float c, float neg, bf16x8& pk, float sum) {
   const bf16x2 ones = {static_cast<__bf16>(1.f), static_cast<__bf16>(1.f)};

@@ -274,10 +274,10 @@ __device__ __forceinline__ void fast_step_bf16pv(SoftmaxState& st, const f32x16 
     if (__any(m_new != st.m)) {  // lanes whose max stays recompute the same P
       st.m = m_new;
       psum = 0.f;
-      psum = exp8_f32sum<0>(sc[0], qsl, -m_new, pb[0], psum);
-      psum = exp8_f32sum<8>(sc[0], qsl, -m_new, pb[1], psum);
-      psum = exp8_f32sum<0>(sc[1], qsl, -m_new, pb[2], psum);
-      psum = exp8_f32sum<8>(sc[1], qsl, -m_new, pb[3], psum);
+      psum = exp8<0>(sc[0], qsl, -m_new, pb[0], psum);
+      psum = exp8<8>(sc[0], qsl, -m_new, pb[1], psum);
+      psum = exp8<0>(sc[1], qsl, -m_new, pb[2], psum);
+      psum = exp8<8>(sc[1], qsl, -m_new, pb[3], psum);
       mfma_fence(st.acc);  // the rescale reads O
       rescale(st, alpha);
     }
@@ -422,10 +422,10 @@ __device__ __forceinline__ void step3_i8(SoftmaxState& st, const f32x16 (&sc)[2]
     if (__any(m_new != st.m)) {  // lanes whose max stays recompute the same P
       st.m = m_new;
       psum = 0.f;
-      psum = exp8_f32sum<0>(sc[0], qc, -m_new, pn[0], psum);
-      psum = exp8_f32sum<8>(sc[0], qc, -m_new, pn[1], psum);
-      psum = exp8_f32sum<0>(sc[1], qc, -m_new, pn[2], psum);
-      psum = exp8_f32sum<8>(sc[1], qc, -m_new, pn[3], psum);
+      psum = exp8<0>(sc[0], qc, -m_new, pn[0], psum);
+      psum = exp8<8>(sc[0], qc, -m_new, pn[1], psum);
+      psum = exp8<0>(sc[1], qc, -m_new, pn[2], psum);
+      psum = exp8<8>(sc[1], qc, -m_new, pn[3], psum);
       if constexpr (PV) mfma_fence(st.acc);  // the rescale reads O
       rescale(st, alpha);
     }
