@@ -4,10 +4,9 @@
 // where it is written, so the CPU oracle (oracle/solattn_oracle.c) reproduces
 // kc, vc, qbar, thresholds and routing masks bit for bit.
 //
-//  pool    one pass over q, k, v: four waves per (block, tensor, 4 heads),
-//          wave w summing rows w (mod 4), each lane 8 channels of one head in
-//          16-byte loads; HBM-bound; optionally quantises Q on the way (the
-//          INT8 path).
+//  pool    one pass over q, k, v: a workgroup per 128 rows of one head,
+//          sixteen row slots (rows g mod 16), each lane 8 channels in 16-byte
+//          loads; HBM-bound; optionally quantises Q on the way (the INT8 path).
 //  moments per-head kc mean / variance over blocks (+ INT8 centring, V scale).
 //  route   thresholds, scores R[i][j], per-query-block exact masks and counts.
 #include <algorithm>
@@ -21,19 +20,20 @@ constexpr int kHeadDim = 128;
 
 // ------------------------------------------------------------------ pool --
 // /root/reference/_preprocess.py:23-113 (kc = sum/len, vc = sum, |v| max) and
-// the q centroid of :140-149. A workgroup is four waves over (block j, tensor,
-// four heads): lane l holds head 4g + l/16 and channels 8(l%16)..+7, so each
-// 16-byte load instruction of a wave reads four adjacent heads of one token
-// (1 KiB contiguous for a dense BTHD tensor). Wave w sums the rows r = w
-// (mod 4) of the block in ascending order, the partial p_w of the arithmetic
-// contract; the partials meet in LDS and wave 0 combines (p0 + p1) + (p2 + p3).
-// The three tensors of one (block, head group) are adjacent in the grid.
-// With qi != null the Q workgroups also quantise each Q row per token
-// (/root/reference/_fused_prep.py:42-48, the codes of quant_common.hpp), so
-// the INT8 path reads Q once.
-constexpr int kPoolHeads = 4;   // heads per workgroup
-constexpr int kPoolWaves = 4;   // = the contract's 4 partials
-constexpr int kPoolUnroll = 8;  // rows in flight per lane
+// the q centroid of :140-149. A workgroup of four waves covers a span of 128
+// rows of one head (one block at block 128, two at block 64): wave w, lane
+// group u (16 lanes, one DPP row) own slot g = 4w + u, i.e. rows g + 16m
+// (m < 8), and each lane 8 channels (16-byte loads). A lane's serial sum over
+// the rows of one block is partial p_g of the contract (rows r = g mod 16,
+// ascending); the 16 partials meet in LDS and tree16 combines them. All 24
+// rows of a lane (Q, K and V) are in flight before any arithmetic.
+// With qi != null the pass also quantises each Q row per token
+// (/root/reference/_fused_prep.py:42-48, the codes of quant_common.hpp): a
+// row's 128 channels are one lane group, so its |max| is a DPP reduction.
+constexpr int kSpan = 128;                // rows per workgroup
+constexpr int kSlots = 16;                // partials of the pooling contract
+constexpr int kSlotRows = kSpan / kSlots; // rows per lane
+constexpr int kPoolThreads = 256;
 
 // The eight bf16 of a 16-byte load as floats.
 __device__ __forceinline__ void unpack8(const uint4& w, float (&x)[8]) {
@@ -41,144 +41,133 @@ __device__ __forceinline__ void unpack8(const uint4& w, float (&x)[8]) {
   x[4] = lo_bf16(w.z); x[5] = hi_bf16(w.z); x[6] = lo_bf16(w.w); x[7] = hi_bf16(w.w);
 }
 
-// p += x and (AMAX) am = max(am, |x|) for a row inside the block; a row past
-// T adds 0.0f (p + 0.0f == p: a partial that starts at +0.0f never becomes
-// -0.0f).
-template <bool AMAX>
-__device__ __forceinline__ void pool_row(const float (&x)[8], bool valid, float (&p)[8],
-                                         float (&am)[8]) {
+// The pooling layout of this thread.
+struct PoolLane {
+  int g;   // slot: rows r0 + g + 16m of the span
+  int c8;  // first of the lane's 8 channels
+  __device__ __forceinline__ PoolLane()
+      : g(4 * static_cast<int>(threadIdx.x >> 6) + static_cast<int>((threadIdx.x >> 4) & 3)),
+        c8(static_cast<int>(threadIdx.x & 15) * 8) {}
+};
+
+// The lane's kSlotRows rows of one head (xh = x + b*sb + h*sh + c8, row stride
+// st) from span row r0; rows past T re-read row T-1 (unconditional loads, so
+// all are in flight together; the pooling adds 0.0f for them).
+__device__ __forceinline__ void load_span(const uint16_t* xh, int64_t st, int64_t r0, int64_t T,
+                                          int g, uint4 (&raw)[kSlotRows]) {
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float y = valid ? x[e] : 0.f;
-    p[e] = p[e] + y;
-    if (AMAX) am[e] = fmaxf(am[e], fabsf(y));
+  for (int m = 0; m < kSlotRows; ++m)
+    raw[m] = *reinterpret_cast<const uint4*>(xh + min(r0 + g + 16 * m, T - 1) * st);
+}
+
+// Partial p_g of each block of the span into part[blk][g][c] (LDS, fp32), and
+// with AMAX the lane's |max| per block into amx[blk][g][c]; rows past T add
+// 0.0f (p + 0.0f == p: a partial that starts at +0.0f never becomes -0.0f).
+template <int BLK, bool AMAX>
+__device__ __forceinline__ void pool_span(const uint4 (&raw)[kSlotRows], int64_t r0, int64_t T,
+                                          const PoolLane& pl, float* part, float* amx) {
+  constexpr int NB = kSpan / BLK, RB = kSlotRows / NB;  // blocks per span, lane rows per block
+#pragma unroll
+  for (int blk = 0; blk < NB; ++blk) {
+    float p[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float am[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < RB; ++i) {
+      const int m = blk * RB + i;
+      const bool valid = r0 + pl.g + 16 * m < T;
+      float x[8];
+      unpack8(raw[m], x);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float y = valid ? x[e] : 0.f;
+        p[e] = p[e] + y;
+        if (AMAX) am[e] = fmaxf(am[e], fabsf(y));
+      }
+    }
+    float4* dst = reinterpret_cast<float4*>(part + ((blk * kSlots + pl.g) * kHeadDim + pl.c8));
+    dst[0] = make_float4(p[0], p[1], p[2], p[3]);
+    dst[1] = make_float4(p[4], p[5], p[6], p[7]);
+    if (AMAX) {
+      float4* da = reinterpret_cast<float4*>(amx + ((blk * kSlots + pl.g) * kHeadDim + pl.c8));
+      da[0] = make_float4(am[0], am[1], am[2], am[3]);
+      da[1] = make_float4(am[4], am[5], am[6], am[7]);
+    }
+  }
+}
+
+// The contract's combination of the 16 partials of one (block, channel),
+// p[g * stride]: ((((p0+p1)+(p2+p3))+((p4+p5)+(p6+p7))) + (((p8+p9)+..)..)).
+__device__ __forceinline__ float tree16(const float* p, int stride) {
+  float a[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) a[i] = p[(2 * i) * stride] + p[(2 * i + 1) * stride];
+  return ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
+}
+
+// Per-token codes of the lane's Q rows (rows past T repeat row T-1 and store
+// the bytes its owner stores, so no store needs a branch).
+__device__ __forceinline__ void quant_span_rows(const uint4 (&raw)[kSlotRows], int64_t r0, int64_t T,
+                                                const PoolLane& pl, int64_t b, int h, int H,
+                                                int64_t TP, int8_t* __restrict__ qi,
+                                                float* __restrict__ qs) {
+#pragma unroll
+  for (int m = 0; m < kSlotRows; ++m) {
+    float x[8];
+    unpack8(raw[m], x);
+    uint2 codes;
+    const float ss = quant_token_row(x, codes);
+    const int64_t row = (b * TP + min(r0 + pl.g + 16 * m, T - 1)) * H + h;
+    *reinterpret_cast<uint2*>(qi + row * kHeadDim + pl.c8) = codes;
+    if (pl.c8 == 0) qs[row] = ss;
   }
 }
 
 template <int BLK, bool QUANT>
-__global__ void __launch_bounds__(64 * kPoolWaves)
+__global__ void __launch_bounds__(kPoolThreads)
 pool_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
             const uint16_t* __restrict__ k, int64_t sk_b, int64_t sk_t, int64_t sk_h,
             const uint16_t* __restrict__ v, int64_t sv_b, int64_t sv_t, int64_t sv_h, int64_t T,
             int H, int NT, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int64_t npad,
             float* __restrict__ qbar, float* __restrict__ vamax_part, int8_t* __restrict__ qi,
             float* __restrict__ qs, int64_t TP) {
-  constexpr int kRows = BLK / kPoolWaves;  // rows per wave
-  static_assert(kRows % kPoolUnroll == 0, "rows per wave");
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int HG = (H + kPoolHeads - 1) / kPoolHeads;
-  const int tensor = static_cast<int>(blockIdx.x % 3);  // 0 K, 1 V, 2 Q
-  const int cell = static_cast<int>(blockIdx.x / 3);
-  const int j = cell / HG;
-  const int h_lane = (cell % HG) * kPoolHeads + (lane >> 4);
-  const int h = min(h_lane, H - 1);  // lanes past the last head re-read it and store nothing
-  const int b = blockIdx.y;
-  const int c8 = (lane & 15) * 8;
-  const uint16_t* base;
-  int64_t st;
-  if (tensor == 0) {
-    base = k + b * sk_b + h * sk_h + c8;
-    st = sk_t;
-  } else if (tensor == 1) {
-    base = v + b * sv_b + h * sv_h + c8;
-    st = sv_t;
-  } else {
-    base = q + b * sq_b + h * sq_h + c8;
-    st = sq_t;
-  }
-  const bool quant = QUANT && tensor == 2;
-  const int64_t t0 = static_cast<int64_t>(j) * BLK;
-  const int len = static_cast<int>(min<int64_t>(BLK, T - t0));
-  float p[8], am[8];
+  constexpr int NB = kSpan / BLK;
+  __shared__ __align__(16) float part[NB * kSlots * kHeadDim];
+  __shared__ __align__(16) float amx[NB * kSlots * kHeadDim];
+  const int h = blockIdx.y;
+  const int64_t b = blockIdx.z, r0 = static_cast<int64_t>(blockIdx.x) * kSpan;
+  const PoolLane pl;
+  uint4 rk[kSlotRows], rv[kSlotRows], rq[kSlotRows];
+  load_span(k + b * sk_b + h * sk_h + pl.c8, sk_t, r0, T, pl.g, rk);
+  load_span(v + b * sv_b + h * sv_h + pl.c8, sv_t, r0, T, pl.g, rv);
+  load_span(q + b * sq_b + h * sq_h + pl.c8, sq_t, r0, T, pl.g, rq);
+  // this thread's output: block s*NB + blk (if it exists), channel c
+  const int blk = static_cast<int>(threadIdx.x) >> 7, c = static_cast<int>(threadIdx.x) & 127;
+  const int j = static_cast<int>(blockIdx.x) * NB + blk;
+  const bool out = blk < NB && j < NT;
+  const float flen = static_cast<float>(min<int64_t>(BLK, T - static_cast<int64_t>(j) * BLK));
+  const float* pc = part + blk * kSlots * kHeadDim + c;
+
+  pool_span<BLK, false>(rk, r0, T, pl, part, nullptr);
+  __syncthreads();
+  if (out) kc[((b * npad + j) * H + h) * kHeadDim + c] = f2bf(tree16(pc, kHeadDim) / flen);
+  __syncthreads();
+  pool_span<BLK, true>(rv, r0, T, pl, part, amx);
+  __syncthreads();
+  if (out) {
+    vc[((b * npad + j) * H + h) * kHeadDim + c] = f2bf(tree16(pc, kHeadDim));
+    if (vamax_part) {
+      const float* ac = amx + blk * kSlots * kHeadDim + c;
+      float m = ac[0];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) p[e] = am[e] = 0.f;
-#pragma unroll 1
-  for (int i0 = 0; i0 < kRows; i0 += kPoolUnroll) {
-    uint4 raw[kPoolUnroll];
-    // unconditional loads (a row past T re-reads the last row) so the eight
-    // are in flight together; the rows past T then add 0.0f
-#pragma unroll
-    for (int u = 0; u < kPoolUnroll; ++u) {
-      const int r = w + kPoolWaves * (i0 + u);
-      raw[u] = *reinterpret_cast<const uint4*>(base + (t0 + min(r, len - 1)) * st);
+      for (int g = 1; g < kSlots; ++g) m = fmaxf(m, ac[g * kHeadDim]);
+      vamax_part[((b * NT + j) * H + h) * kHeadDim + c] = m;
     }
-    if (quant) {  // uniform per workgroup
-#pragma unroll
-      for (int u = 0; u < kPoolUnroll; ++u) {
-        const int r = w + kPoolWaves * (i0 + u);
-        float x[8];
-        unpack8(raw[u], x);
-        pool_row<false>(x, r < len, p, am);
-        // A row past T holds row T-1 and a lane past H head H-1: both store
-        // the bytes the owning lane stores, so no store needs a branch.
-        uint2 codes;
-        const float ss = quant_token_row(x, codes);
-        const int64_t row = (static_cast<int64_t>(b) * TP + t0 + min(r, len - 1)) * H + h;
-        *reinterpret_cast<uint2*>(qi + row * kHeadDim + c8) = codes;
-        qs[row] = ss;
-      }
-    } else {  // (|max| is kept for V; K and unquantised Q ignore it)
-#pragma unroll
-      for (int u = 0; u < kPoolUnroll; ++u) {
-        float x[8];
-        unpack8(raw[u], x);
-        pool_row<true>(x, w + kPoolWaves * (i0 + u) < len, p, am);
-      }
-    }
-  }
-  // partials of waves 1..3 (and their |max|) through LDS to wave 0
-  __shared__ float4 part[kPoolWaves - 1][4][64];
-  if (w > 0) {
-    part[w - 1][0][lane] = make_float4(p[0], p[1], p[2], p[3]);
-    part[w - 1][1][lane] = make_float4(p[4], p[5], p[6], p[7]);
-    part[w - 1][2][lane] = make_float4(am[0], am[1], am[2], am[3]);
-    part[w - 1][3][lane] = make_float4(am[4], am[5], am[6], am[7]);
   }
   __syncthreads();
-  if (w > 0 || h_lane >= H) return;
-  float pw[kPoolWaves - 1][8];
-#pragma unroll
-  for (int i = 0; i < kPoolWaves - 1; ++i) {
-    const float4 lo = part[i][0][lane], hi = part[i][1][lane];
-    const float4 alo = part[i][2][lane], ahi = part[i][3][lane];
-    pw[i][0] = lo.x, pw[i][1] = lo.y, pw[i][2] = lo.z, pw[i][3] = lo.w;
-    pw[i][4] = hi.x, pw[i][5] = hi.y, pw[i][6] = hi.z, pw[i][7] = hi.w;
-    am[0] = fmaxf(am[0], alo.x), am[1] = fmaxf(am[1], alo.y);
-    am[2] = fmaxf(am[2], alo.z), am[3] = fmaxf(am[3], alo.w);
-    am[4] = fmaxf(am[4], ahi.x), am[5] = fmaxf(am[5], ahi.y);
-    am[6] = fmaxf(am[6], ahi.z), am[7] = fmaxf(am[7], ahi.w);
-  }
-  float sum[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) sum[e] = (p[e] + pw[0][e]) + (pw[1][e] + pw[2][e]);
-  const float flen = static_cast<float>(len);
-  const int64_t kv_off = ((b * npad + j) * H + h) * kHeadDim + c8;
-  if (tensor == 0) {
-    uint4 o;
-    o.x = pack_bf16x2(sum[0] / flen, sum[1] / flen);
-    o.y = pack_bf16x2(sum[2] / flen, sum[3] / flen);
-    o.z = pack_bf16x2(sum[4] / flen, sum[5] / flen);
-    o.w = pack_bf16x2(sum[6] / flen, sum[7] / flen);
-    *reinterpret_cast<uint4*>(kc + kv_off) = o;
-  } else if (tensor == 1) {
-    uint4 o;
-    o.x = pack_bf16x2(sum[0], sum[1]);
-    o.y = pack_bf16x2(sum[2], sum[3]);
-    o.z = pack_bf16x2(sum[4], sum[5]);
-    o.w = pack_bf16x2(sum[6], sum[7]);
-    *reinterpret_cast<uint4*>(vc + kv_off) = o;
-    if (vamax_part) {
-      float4* dst = reinterpret_cast<float4*>(
-          vamax_part + ((static_cast<int64_t>(b) * NT + j) * H + h) * kHeadDim + c8);
-      dst[0] = make_float4(am[0], am[1], am[2], am[3]);
-      dst[1] = make_float4(am[4], am[5], am[6], am[7]);
-    }
-  } else {
-    float4* dst = reinterpret_cast<float4*>(
-        qbar + ((static_cast<int64_t>(b) * H + h) * NT + j) * kHeadDim + c8);
-    dst[0] = make_float4(sum[0] / flen, sum[1] / flen, sum[2] / flen, sum[3] / flen);
-    dst[1] = make_float4(sum[4] / flen, sum[5] / flen, sum[6] / flen, sum[7] / flen);
-  }
+  if (QUANT) quant_span_rows(rq, r0, T, pl, b, h, H, TP, qi, qs);
+  pool_span<BLK, false>(rq, r0, T, pl, part, nullptr);
+  __syncthreads();
+  if (out) qbar[((b * H + h) * NT + j) * kHeadDim + c] = tree16(pc, kHeadDim) / flen;
 }
 
 // --------------------------------------------------------------- moments --
@@ -512,19 +501,19 @@ int launch_pool(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h, con
                 uint16_t* kc, uint16_t* vc, int64_t npad, float* qbar, float* vamax_part,
                 int8_t* qi, float* qs, int64_t TP, hipStream_t s) {
   const int64_t NT = cdiv(T, block);
-  const int64_t HG = cdiv(H, kPoolHeads);
-  SOLATTN_REQUIRE(3 * NT * HG < (1ll << 31) && B <= 65535, SOLATTN_EUNSUPPORTED,
-                  "pool: %lld blocks of %lld x %lld heads", (long long)NT, (long long)block,
-                  (long long)H);
+  const int64_t spans = cdiv(T, kSpan);
+  SOLATTN_REQUIRE(spans < (1ll << 31) && B <= 65535 && H <= 65535, SOLATTN_EUNSUPPORTED,
+                  "pool: %lld tokens x %lld heads x %lld batch", (long long)T, (long long)H,
+                  (long long)B);
   SOLATTN_REQUIRE(!qi || (qs && TP >= T && reinterpret_cast<uintptr_t>(qi) % 8 == 0),
                   SOLATTN_EINVAL, "pool: bad Q quantisation outputs");
-  dim3 grid(static_cast<uint32_t>(3 * NT * HG), static_cast<uint32_t>(B));
-  const dim3 wg(64 * kPoolWaves);
+  // spans fastest, so the workgroups in flight read neighbouring rows of a head
+  dim3 grid(static_cast<uint32_t>(spans), static_cast<uint32_t>(H), static_cast<uint32_t>(B));
   const auto kern = block == 64 ? (qi ? pool_kernel<64, true> : pool_kernel<64, false>)
                                  : (qi ? pool_kernel<128, true> : pool_kernel<128, false>);
-  hipLaunchKernelGGL(kern, grid, wg, 0, s, q, sq_b, sq_t, sq_h, k, sk_b, sk_t, sk_h, v, sv_b, sv_t,
-                     sv_h, T, static_cast<int>(H), static_cast<int>(NT), kc, vc, npad, qbar,
-                     vamax_part, qi, qs, TP);
+  hipLaunchKernelGGL(kern, grid, dim3(kPoolThreads), 0, s, q, sq_b, sq_t, sq_h, k, sk_b, sk_t,
+                     sk_h, v, sv_b, sv_t, sv_h, T, static_cast<int>(H), static_cast<int>(NT), kc,
+                     vc, npad, qbar, vamax_part, qi, qs, TP);
   return check_launch("pool");
 }
 

@@ -25,9 +25,10 @@
  *
  * Arithmetic contract (the CPU oracle restates the same operation order, so
  * pooled keys, thresholds, routing masks and INT8 codes are bit-exact):
- *  - pooled sums: for each (block, channel) four fp32 partial sums over rows
- *    r = 0,4,8.. / 1,5,9.. / 2,6,.. / 3,7,.. taken in ascending order (rows past
- *    T add 0.0f), combined as (p0 + p1) + (p2 + p3).
+ *  - pooled sums: for each (block, channel) sixteen fp32 partial sums p_g over
+ *    the block's rows r = g (mod 16) taken in ascending order (rows past T add
+ *    0.0f), combined pairwise as ((((p0+p1)+(p2+p3))+((p4+p5)+(p6+p7))) +
+ *    (((p8+p9)+(p10+p11))+((p12+p13)+(p14+p15)))).
  *  - kc = bf16_rne(sum / len); vc = bf16_rne(sum); qbar = sum / len (fp32).
  *  - moments: 8 fp32 partials over blocks j = g (mod 8), ascending, combined
  *    ((p0+p1)+(p2+p3)) + ((p4+p5)+(p6+p7)); no FMA.

@@ -8,8 +8,8 @@
  * Each function restates the reference's algorithm (file:line cited) with the
  * operation order fixed by the arithmetic contract in include/solattn.h, so the
  * HIP kernels can be compared bit for bit:
- *   - pooled sums: four fp32 partials over rows r = g (mod 4), ascending,
- *     combined (p0 + p1) + (p2 + p3);
+ *   - pooled sums: sixteen fp32 partials over rows r = g (mod 16), ascending,
+ *     combined by the pairwise tree of tree16() below;
  *   - moments: 8 partials over blocks j = g (mod 8), ascending, combined as
  *     a fixed tree; no FMA;
  *   - dot products for thresholds and routing: fmaf chains over d ascending.
@@ -94,18 +94,24 @@ int or_morton_perm(int64_t frames, int64_t height, int64_t width, int curve, int
  * /root/reference/_preprocess.py:49-57 (kc = sum/len), :100 (vc = sum),
  * :106-113 (per-block |v| max), :140-149 (q centroid = sum/len).
  * x: bf16 BTHD with element strides; rows t >= T read as 0. For every
- * (head, channel) four partials take rows r = g (mod 4) in ascending order and
- * combine as (p0 + p1) + (p2 + p3); rows are streamed so the loop is cache-friendly. */
+ * (head, channel) sixteen partials take rows r = g (mod 16) in ascending order
+ * and combine by tree16; rows are streamed so the loop is cache-friendly. */
+static inline float tree16(const float* p, int64_t stride) {
+  float a[8];
+  for (int i = 0; i < 8; ++i) a[i] = p[(2 * i) * stride] + p[(2 * i + 1) * stride];
+  return ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
+}
+
 static void pool_one(const uint16_t* x, int64_t s_b, int64_t s_t, int64_t s_h, int64_t b,
                      int64_t t0, int64_t T, int64_t H, int64_t D, int64_t block, float* part,
                      float* amax, float* out_sum) {
   int64_t HD = H * D;
-  for (int64_t e = 0; e < 4 * HD; ++e) part[e] = 0.f;
+  for (int64_t e = 0; e < 16 * HD; ++e) part[e] = 0.f;
   if (amax)
     for (int64_t e = 0; e < HD; ++e) amax[e] = 0.f;
   for (int64_t r = 0; r < block; ++r) {
     int64_t t = t0 + r;
-    float* p = part + (r & 3) * HD;
+    float* p = part + (r & 15) * HD;
     for (int64_t h = 0; h < H; ++h) {
       const uint16_t* row = t < T ? x + b * s_b + t * s_t + h * s_h : NULL;
       for (int64_t d = 0; d < D; ++d) {
@@ -118,8 +124,7 @@ static void pool_one(const uint16_t* x, int64_t s_b, int64_t s_t, int64_t s_h, i
       }
     }
   }
-  for (int64_t e = 0; e < HD; ++e)
-    out_sum[e] = (part[e] + part[HD + e]) + (part[2 * HD + e] + part[3 * HD + e]);
+  for (int64_t e = 0; e < HD; ++e) out_sum[e] = tree16(part + e, HD);
 }
 
 void or_pool(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h, const uint16_t* k,
@@ -131,7 +136,7 @@ void or_pool(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h, const 
   int64_t HD = H * D;
 #pragma omp parallel
   {
-    float* part = (float*)malloc(sizeof(float) * (size_t)(4 * HD));
+    float* part = (float*)malloc(sizeof(float) * (size_t)(16 * HD));
     float* sk = (float*)malloc(sizeof(float) * (size_t)HD);
     float* sv = (float*)malloc(sizeof(float) * (size_t)HD);
     float* sq = (float*)malloc(sizeof(float) * (size_t)HD);

@@ -104,17 +104,32 @@ def test_pool_closed_form(block):
 
 
 def test_pool_canonical_order_bits():
-    """kc bits equal an independent numpy restatement of the 4-partial order."""
+    """kc bits equal an independent numpy restatement of the 16-partial order
+    (rows r = g mod 16 summed ascending, then the fixed pairwise tree)."""
     q, k, v = (randn_bf16((1, 200, 2, 128), s) for s in (4, 5, 6))
+    # exponents spread over 2^-14 .. 2^6, so that fp32 sums of bf16 values round
+    # and the order shows in the bits (sums of similar bf16 values are often exact)
+    g = torch.Generator().manual_seed(7)
+    k = (k.float() * torch.exp2(torch.randint(-14, 7, k.shape, generator=g).float())).to(torch.bfloat16)
     kc = oracle.pool(bits(q), bits(k), bits(v), 64)[0]
     x = k.float().numpy()
+    f = np.float32
     for j, (lo, n) in enumerate([(0, 64), (64, 64), (128, 64), (192, 8)]):
-        part = np.zeros((4, 2, 128), np.float32)
+        part = np.zeros((16, 2, 128), f)
         for r in range(64):
-            val = x[0, lo + r] if r < n else np.zeros((2, 128), np.float32)
-            part[r & 3] = (part[r & 3] + val).astype(np.float32)
-        s = ((part[0] + part[1]).astype(np.float32) + (part[2] + part[3]).astype(np.float32)).astype(np.float32)
-        assert np.array_equal(kc[0, j], oracle.f32_to_bf16((s / np.float32(n)).astype(np.float32)))
+            val = x[0, lo + r] if r < n else np.zeros((2, 128), f)
+            part[r % 16] = (part[r % 16] + val).astype(f)
+        pair = [(part[2 * i] + part[2 * i + 1]).astype(f) for i in range(8)]
+        quad = [(pair[2 * i] + pair[2 * i + 1]).astype(f) for i in range(4)]
+        s = ((quad[0] + quad[1]).astype(f) + (quad[2] + quad[3]).astype(f)).astype(f)
+        assert np.array_equal(kc[0, j], oracle.f32_to_bf16((s / f(n)).astype(f)))
+        # a plausible slip, the old 4-partial order, gives other bits somewhere
+        p4 = np.zeros((4, 2, 128), f)
+        for r in range(n):
+            p4[r & 3] = (p4[r & 3] + x[0, lo + r]).astype(f)
+        s4 = ((p4[0] + p4[1]).astype(f) + (p4[2] + p4[3]).astype(f)).astype(f)
+        if n == 64:
+            assert not np.array_equal(s, s4)
 
 
 @pytest.mark.parametrize("centre", [False, True])
