@@ -38,6 +38,9 @@ SIGNATURES = {
                          [_f, _p, _l, _l, _l, _p], _i),
     "solattn_fwd_int8": ([_p, _l, _l, _l, _p, _p, _p, _p, _p, _p, _p, _l, _l, _l, _l, _p, _p, _l,
                           _p, _p] + [_l] * 5 + [_f, _i, _p, _l, _l, _l, _p], _i),
+    "solattn_prep_int8_sync_bytes": ([_l, _l], _l),
+    "solattn_prep_int8": ([_p, _l, _l, _l] * 3 + [_l] * 5 + [_p, _p, _l] + [_p] * 9 + [_i, _p, _l,
+                                                                              _p, _l, _p], _i),
     "solattn_sol_attn_workspace_bytes": ([_l, _l, _l, _l, _l, _i], _l),
     "solattn_sol_attn": ([_p, _l, _l, _l] * 3 + [_l] * 5 + [_f, _f, _l, _l, _l, _l, _p, _l,
                                                            _p, _l, _l, _l, _p], _i),

@@ -67,6 +67,19 @@ int launch_pool(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h, con
                 uint16_t* kc, uint16_t* vc, int64_t npad, float* qbar, float* vamax_part,
                 int8_t* qi, float* qs, int64_t TP, hipStream_t s);
 
+// The INT8 preparation with one read of q, k and v (prep.hip): pooled keys,
+// centred kc, moments, V scale, Q/K/V codes; as solattn_prep_int8, whose
+// SOLATTN_EUNSUPPORTED means: use pool -> moments -> quant instead.
+int64_t single_read_sync_words(int64_t B, int64_t H);
+int prep_int8_single_read(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
+                          const uint16_t* k, int64_t sk_b, int64_t sk_t, int64_t sk_h,
+                          const uint16_t* v, int64_t sv_b, int64_t sv_t, int64_t sv_h, int64_t B,
+                          int64_t T, int64_t H, int64_t D, int64_t block, uint16_t* kc,
+                          uint16_t* vc, int64_t npad, float* qbar, float* kc_mean, float* kc_var,
+                          float* vamax_part, float* vscale, int8_t* qi, float* qs, int8_t* ki,
+                          float* ks, int ks_head_major, int8_t* vi, int64_t TP, uint32_t* sync,
+                          int64_t sync_bytes, hipStream_t stream);
+
 // Copies BTHD rows of din bf16 channels into rows of dout channels, zero
 // filled (din < dout), or the first dout channels back out (din > dout)
 // (reorder.hip).

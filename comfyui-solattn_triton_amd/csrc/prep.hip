@@ -119,6 +119,7 @@ __device__ __forceinline__ void quant_span_rows(const uint4 (&raw)[kSlotRows], i
     const int64_t row = (b * TP + min(r0 + pl.g + 16 * m, T - 1)) * H + h;
     *reinterpret_cast<uint2*>(qi + row * kHeadDim + pl.c8) = codes;
     if (pl.c8 == 0) qs[row] = ss;
+    __builtin_amdgcn_sched_barrier(0);  // one row at a time
   }
 }
 
@@ -297,6 +298,283 @@ moments_kernel(uint16_t* __restrict__ kc, int64_t npad, int NT, int H, int centr
   {
     const int d = threadIdx.x;
     kc_var[(static_cast<int64_t>(b) * H + h) * kHeadDim + d] = tree8(part, d) / fnt;
+  }
+}
+
+// ------------------------------------------------------ single-read INT8 --
+// The INT8 path's preparation with one read of Q, K and V
+// (/root/reference/_fused_prep.py:62-98 reads K and V twice). A head's K codes
+// need the mean of all its pooled keys and its V codes the per-channel |max|
+// over all its tokens, so a workgroup keeps its K and V rows in registers
+// across two barriers over the workgroups of that head:
+//   phase 1  load the span's Q, K and V rows; quantise and pool Q, pool K and
+//            V (as pool_kernel: same partials, same outputs, |v| max per block)
+//   barrier
+//   phase 2  16 workgroups, one per 8-channel slice: kc mean, centred kc, kc
+//            variance and V scale of the head (moments_kernel's order)
+//   barrier
+//   phase 3  K codes (smoothed by the mean, per token) and V codes (per
+//            channel) from the rows still in registers.
+// The grid is launched cooperatively (every workgroup resident) as teams of
+// S = ceil(T / 128) workgroups; team t handles heads t, t + nteams, ..., so
+// one team's VALU phases overlap another's loads. A team's barrier counter
+// (sync[1 + team], zeroed by sync_init_kernel) counts arrivals; barrier n of a
+// head waits for n * S of them. The wait is bounded: a barrier not met within
+// ~0.1 s sets sync[0] and releases its waiter, so no schedule can hang the
+// device (with every workgroup resident, each arrives and the bound is never
+// met).
+constexpr int kMomSlices = kHeadDim / 8;  // 8-channel slices of the moments phase
+constexpr uint32_t kSpinLimit = 1u << 21; // ~0.1 s of 128-cycle sleeps
+
+__global__ void sync_init_kernel(uint32_t* __restrict__ sync, int n) {
+  for (int i = threadIdx.x; i < n; i += blockDim.x) sync[i] = 0u;
+}
+
+// Values one workgroup hands to another inside the launch (pooled keys, |v|
+// maxima, the mean and the V scale) move through relaxed device-scope atomic
+// loads and stores, which write through / read past the XCDs' non-coherent
+// L2s; nothing else needs to be visible before the launch ends, so the
+// barrier itself flushes no cache (a device-scope fence writes back and
+// invalidates a whole L2, and one per wave at every barrier cost ~0.15 ms).
+__device__ __forceinline__ void xstore(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t xload(const uint32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t xload64(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Every thread's stores have completed (s_waitcnt 0) before the workgroup
+// arrives; the counter and the poll are device-scope atomics.
+__device__ __forceinline__ void team_barrier(uint32_t* ctr, uint32_t target, uint32_t* err) {
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    uint32_t spins = 0;
+    while (xload(ctr) < target) {
+      if (++spins > kSpinLimit) {
+        xstore(err, 1u);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+  }
+  __syncthreads();
+}
+
+// Moments of channels [8cs, 8cs + 8) of head (b, h), in moments_kernel's order:
+// 8 partials over blocks j = g (mod 8) ascending, tree8; kc centred in place
+// (bf16), variance of the centred values; vscale from the per-block |v| max.
+// skc: NT x 8 fp32 of dynamic LDS; red: 32 fp32 of LDS.
+__device__ __forceinline__ void moments_slice(uint16_t* __restrict__ kc, int64_t npad,
+                                              const float* __restrict__ vamax_part,
+                                              float* __restrict__ kc_mean,
+                                              float* __restrict__ kc_var,
+                                              float* __restrict__ vscale, int64_t b, int h, int H,
+                                              int NT, int cs, float* skc, float* red) {
+  __shared__ float psum[8][8];
+  __shared__ float smean[8];
+  const int t = threadIdx.x;
+  const int64_t sj = static_cast<int64_t>(H) * kHeadDim;
+  uint16_t* col = kc + (b * npad * H + h) * kHeadDim + 8 * cs;
+  float am[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int j = t; j < NT; j += kPoolThreads) {
+    const uint64_t* kr = reinterpret_cast<const uint64_t*>(col + j * sj);
+    const uint64_t w0 = xload64(kr), w1 = xload64(kr + 1);
+    float x[8];
+    unpack8(make_uint4(static_cast<uint32_t>(w0), static_cast<uint32_t>(w0 >> 32),
+                       static_cast<uint32_t>(w1), static_cast<uint32_t>(w1 >> 32)), x);
+    float4* d = reinterpret_cast<float4*>(skc + 8 * j);
+    d[0] = make_float4(x[0], x[1], x[2], x[3]);
+    d[1] = make_float4(x[4], x[5], x[6], x[7]);
+    if (vamax_part) {
+      const uint64_t* ar = reinterpret_cast<const uint64_t*>(
+          vamax_part + ((b * NT + j) * H + h) * kHeadDim + 8 * cs);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint64_t w = xload64(ar + i);
+        am[2 * i] = fmaxf(am[2 * i], __uint_as_float(static_cast<uint32_t>(w)));
+        am[2 * i + 1] = fmaxf(am[2 * i + 1], __uint_as_float(static_cast<uint32_t>(w >> 32)));
+      }
+    }
+  }
+  if (vamax_part) {
+    // max over the wave (any order: max is exact), then over the 4 waves
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) am[e] = fmaxf(am[e], __shfl_xor(am[e], o));
+    if ((t & 63) == 0)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) red[8 * (t >> 6) + e] = am[e];
+  }
+  __syncthreads();
+  const int g = t >> 3, e = t & 7;  // threads t < 64: partial g, channel e
+  if (t < 64) {
+    float acc = 0.f;
+#pragma unroll 8
+    for (int j = g; j < NT; j += 8) acc = acc + skc[8 * j + e];
+    psum[g][e] = acc;
+  }
+  __syncthreads();
+  const int64_t mo = (b * H + h) * kHeadDim + 8 * cs;
+  if (t < 8) {
+    const float mean = (((psum[0][t] + psum[1][t]) + (psum[2][t] + psum[3][t])) +
+                        ((psum[4][t] + psum[5][t]) + (psum[6][t] + psum[7][t]))) /
+                       static_cast<float>(NT);
+    smean[t] = mean;
+    xstore(reinterpret_cast<uint32_t*>(kc_mean + mo + t), __float_as_uint(mean));
+    if (vamax_part) {
+      const float m = fmaxf(fmaxf(red[t], red[8 + t]), fmaxf(red[16 + t], red[24 + t]));
+      const float sc = m * (1.0f / 127.0f);  // torch's scalar divide: a multiply by 1/127
+      xstore(reinterpret_cast<uint32_t*>(vscale + mo + t), __float_as_uint(sc < 1e-8f ? 1e-8f : sc));
+    }
+  }
+  __syncthreads();
+  for (int j = t; j < NT; j += kPoolThreads) {
+    uint16_t nb[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      nb[c] = f2bf(skc[8 * j + c] - smean[c]);
+      const float y = bf2f(nb[c]);
+      skc[8 * j + c] = y * y;
+    }
+    *reinterpret_cast<uint4*>(col + j * sj) =
+        make_uint4(nb[0] | (static_cast<uint32_t>(nb[1]) << 16), nb[2] | (static_cast<uint32_t>(nb[3]) << 16),
+                   nb[4] | (static_cast<uint32_t>(nb[5]) << 16), nb[6] | (static_cast<uint32_t>(nb[7]) << 16));
+  }
+  __syncthreads();
+  if (t < 64) {
+    float acc = 0.f;
+#pragma unroll 8
+    for (int j = g; j < NT; j += 8) acc = acc + skc[8 * j + e];
+    psum[g][e] = acc;
+  }
+  __syncthreads();
+  if (t < 8)
+    kc_var[mo + t] = (((psum[0][t] + psum[1][t]) + (psum[2][t] + psum[3][t])) +
+                      ((psum[4][t] + psum[5][t]) + (psum[6][t] + psum[7][t]))) /
+                     static_cast<float>(NT);
+  __syncthreads();  // skc, red and psum are reused
+}
+
+struct PrepInt8Args {
+  const uint16_t *q, *k, *v;
+  int64_t sq_b, sq_t, sq_h, sk_b, sk_t, sk_h, sv_b, sv_t, sv_h;
+  int64_t T, TP, npad;
+  int B, H, NT, S, nteams;
+  uint16_t *kc, *vc;
+  float *qbar, *kc_mean, *kc_var, *vscale, *vamax_part;  // vscale, vamax_part: null without V codes
+  int8_t *qi, *ki, *vi;
+  float *qs, *ks;
+  int64_t ks_st, ks_sh;  // element strides of ks within a batch's TP*H scales
+  uint32_t* sync;        // the bound flag, then nteams barrier counters
+};
+
+template <int BLK, bool PV>
+__global__ void __launch_bounds__(kPoolThreads) __attribute__((amdgpu_waves_per_eu(2)))
+prep_int8_single_read_kernel(const PrepInt8Args a) {
+  constexpr int NB = kSpan / BLK;
+  __shared__ __align__(16) float part[NB * kSlots * kHeadDim];
+  __shared__ __align__(16) float amx[NB * kSlots * kHeadDim];
+  extern __shared__ __align__(16) float skc_lds[];  // NT x 8 (moments phase)
+  const int team = static_cast<int>(blockIdx.x) / a.S, s = static_cast<int>(blockIdx.x) % a.S;
+  uint32_t* err = a.sync;
+  uint32_t* ctr = a.sync + 1 + team;
+  const int64_t r0 = static_cast<int64_t>(s) * kSpan, T = a.T;
+  const int H = a.H, NT = a.NT;
+  const PoolLane pl0;
+  const int blk = static_cast<int>(threadIdx.x) >> 7, c = static_cast<int>(threadIdx.x) & 127;
+  const int j = s * NB + blk;
+  const bool out = blk < NB && j < NT;
+  const float flen = static_cast<float>(min<int64_t>(BLK, T - static_cast<int64_t>(j) * BLK));
+  const float* pc = part + blk * kSlots * kHeadDim + c;
+  // the exchange stores go by channel pairs: thread t, block t / 64, channels
+  // 2(t % 64) and 2(t % 64) + 1
+  const int blk2 = static_cast<int>(threadIdx.x) >> 6, c2 = 2 * (static_cast<int>(threadIdx.x) & 63);
+  const int j2 = s * NB + blk2;
+  const bool out2 = blk2 < NB && j2 < NT;
+  const float flen2 = static_cast<float>(min<int64_t>(BLK, T - static_cast<int64_t>(j2) * BLK));
+  const float* pc2 = part + blk2 * kSlots * kHeadDim + c2;
+  uint32_t epoch = 0;
+  const int BH = a.B * H;
+  for (int bh = team; bh < BH; bh += a.nteams) {
+    const int64_t b = bh / H;
+    const int h = bh % H;
+    // The lane's row offsets do not change from head to head; left visible,
+    // the compiler keeps all of them (64-bit each) live across the loop and
+    // spills them. Through the empty asm they are recomputed per head.
+    PoolLane pl = pl0;
+    asm volatile("" : "+v"(pl.g));
+    // ---- phase 1: one read of the span's rows (Q's are processed while K's
+    // and V's land)
+    uint4 rq[kSlotRows], rk[kSlotRows], rv[kSlotRows];
+    load_span(a.q + b * a.sq_b + h * a.sq_h + pl.c8, a.sq_t, r0, T, pl.g, rq);
+    load_span(a.k + b * a.sk_b + h * a.sk_h + pl.c8, a.sk_t, r0, T, pl.g, rk);
+    load_span(a.v + b * a.sv_b + h * a.sv_h + pl.c8, a.sv_t, r0, T, pl.g, rv);
+    quant_span_rows(rq, r0, T, pl, b, h, H, a.TP, a.qi, a.qs);
+    pool_span<BLK, false>(rq, r0, T, pl, part, nullptr);
+    __syncthreads();
+    if (out) a.qbar[((b * H + h) * NT + j) * kHeadDim + c] = tree16(pc, kHeadDim) / flen;
+    __syncthreads();
+    pool_span<BLK, false>(rk, r0, T, pl, part, nullptr);
+    __syncthreads();
+    if (out2)  // read by another workgroup in phase 2: an exchange store
+      xstore(reinterpret_cast<uint32_t*>(a.kc + ((b * a.npad + j2) * H + h) * kHeadDim + c2),
+             pack_bf16x2(tree16(pc2, kHeadDim) / flen2, tree16(pc2 + 1, kHeadDim) / flen2));
+    __syncthreads();
+    pool_span<BLK, PV>(rv, r0, T, pl, part, amx);
+    __syncthreads();
+    if (out) a.vc[((b * a.npad + j) * H + h) * kHeadDim + c] = f2bf(tree16(pc, kHeadDim));
+    if (PV && out2) {
+      const float* ac = amx + blk2 * kSlots * kHeadDim + c2;
+      float m0 = ac[0], m1 = ac[1];
+#pragma unroll
+      for (int g = 1; g < kSlots; ++g) {
+        m0 = fmaxf(m0, ac[g * kHeadDim]);
+        m1 = fmaxf(m1, ac[g * kHeadDim + 1]);
+      }
+      uint32_t* d = reinterpret_cast<uint32_t*>(a.vamax_part + ((b * NT + j2) * H + h) * kHeadDim + c2);
+      xstore(d, __float_as_uint(m0));
+      xstore(d + 1, __float_as_uint(m1));
+    }
+    team_barrier(ctr, ++epoch * static_cast<uint32_t>(a.S), err);
+    // ---- phase 2: the head's moments, one 8-channel slice per workgroup
+    for (int cs = s; cs < kMomSlices; cs += a.S)
+      moments_slice(a.kc, a.npad, PV ? a.vamax_part : nullptr, a.kc_mean, a.kc_var, a.vscale, b,
+                    h, H, NT, cs, skc_lds, part);
+    team_barrier(ctr, ++epoch * static_cast<uint32_t>(a.S), err);
+    // ---- phase 3: K and V codes from the rows in registers
+    const int64_t mo = (b * H + h) * kHeadDim + pl.c8;
+    float mean[8], sv[8], rr[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {  // written by the phase-2 workgroups
+      mean[e] = __uint_as_float(xload(reinterpret_cast<const uint32_t*>(a.kc_mean + mo + e)));
+      sv[e] = PV ? __uint_as_float(xload(reinterpret_cast<const uint32_t*>(a.vscale + mo + e))) : 1.f;
+      rr[e] = __builtin_amdgcn_rcpf(sv[e]);
+    }
+#pragma unroll
+    for (int m = 0; m < kSlotRows; ++m) {
+      // rows past T repeat row T-1 and store what its owner stores
+      const int64_t t = min(r0 + pl.g + 16 * m, T - 1);
+      const int64_t row = (b * a.TP + t) * H + h;
+      float x[8], y[8];
+      unpack8(rk[m], x);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) y[e] = x[e] - mean[e];
+      uint2 codes;
+      const float ss = quant_token_row(y, codes);
+      *reinterpret_cast<uint2*>(a.ki + row * kHeadDim + pl.c8) = codes;
+      if (pl.c8 == 0) a.ks[b * a.TP * H + t * a.ks_st + h * a.ks_sh] = ss;
+      if (PV) {
+        unpack8(rv[m], x);
+        *reinterpret_cast<uint2*>(a.vi + row * kHeadDim + pl.c8) = codes8(x, rr, sv);
+      }
+      __builtin_amdgcn_sched_barrier(0);  // one row at a time: registers stay at one row's
+    }
   }
 }
 
@@ -608,4 +886,126 @@ extern "C" int solattn_route(const float* qbar, const uint16_t* kc, int64_t npad
                      static_cast<int>(NT), static_cast<int>(W), c, c2, tau, mode, sink_kv_lo,
                      sink_kv_hi, sink_q_lo, sink_q_hi, thr, counts, mask);
   return check_launch("route");
+}
+
+namespace solattn {
+
+int64_t single_read_sync_words(int64_t B, int64_t H) { return B * H + 1; }
+
+namespace {
+
+template <int BLK, bool PV>
+const void* single_read_kernel() {
+  return reinterpret_cast<const void*>(&prep_int8_single_read_kernel<BLK, PV>);
+}
+
+// Teams of the single-read schedule that the device holds at once (every
+// workgroup resident), or 0 when fewer than two teams fit: one team would run
+// its phases back to back with nothing to overlap them.
+int single_read_teams(int64_t B, int64_t T, int64_t H, int64_t block, bool pv, size_t lds) {
+  const int64_t S = cdiv(T, kSpan);
+  const void* kern = block == 64 ? (pv ? single_read_kernel<64, true>() : single_read_kernel<64, false>())
+                                 : (pv ? single_read_kernel<128, true>() : single_read_kernel<128, false>());
+  int dev = 0, cus = 0, per_cu = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kPoolThreads, lds) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  const int64_t teams = std::min<int64_t>(B * H, static_cast<int64_t>(per_cu) * cus / S);
+  return teams >= 2 ? static_cast<int>(teams) : 0;
+}
+
+}  // namespace
+
+int prep_int8_single_read(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
+                          const uint16_t* k, int64_t sk_b, int64_t sk_t, int64_t sk_h,
+                          const uint16_t* v, int64_t sv_b, int64_t sv_t, int64_t sv_h, int64_t B,
+                          int64_t T, int64_t H, int64_t D, int64_t block, uint16_t* kc,
+                          uint16_t* vc, int64_t npad, float* qbar, float* kc_mean, float* kc_var,
+                          float* vamax_part, float* vscale, int8_t* qi, float* qs, int8_t* ki,
+                          float* ks, int ks_head_major, int8_t* vi, int64_t TP, uint32_t* sync,
+                          int64_t sync_bytes, hipStream_t stream) {
+  SOLATTN_REQUIRE(D == kHeadDim, SOLATTN_EUNSUPPORTED, "prep_int8: head_dim %lld != 128", (long long)D);
+  SOLATTN_REQUIRE(block == 64 || block == 128, SOLATTN_EUNSUPPORTED,
+                  "prep_int8: block %lld not in {64, 128}", (long long)block);
+  SOLATTN_REQUIRE(B > 0 && T > 0 && H > 0 && B * H < (1ll << 30) && T < (1ll << 31),
+                  SOLATTN_EINVAL, "prep_int8: bad sizes");
+  const int64_t NT = cdiv(T, block);
+  SOLATTN_REQUIRE(npad >= NT && TP >= T, SOLATTN_EINVAL, "prep_int8: npad < NT or TP < T");
+  const bool pv = vscale != nullptr;
+  SOLATTN_REQUIRE(kc && vc && qbar && kc_mean && kc_var && qi && qs && ki && ks &&
+                      (!pv || (vamax_part && vi)),
+                  SOLATTN_EINVAL, "prep_int8: null output");
+  SOLATTN_REQUIRE(sync && sync_bytes >= single_read_sync_words(B, H) * 4, SOLATTN_ESIZE,
+                  "prep_int8: sync buffer %lld < %lld bytes", (long long)sync_bytes,
+                  (long long)(single_read_sync_words(B, H) * 4));
+  SOLATTN_REQUIRE(reinterpret_cast<uintptr_t>(kc) % 16 == 0 && reinterpret_cast<uintptr_t>(qi) % 8 == 0 &&
+                      reinterpret_cast<uintptr_t>(ki) % 8 == 0 &&
+                      reinterpret_cast<uintptr_t>(vamax_part) % 16 == 0 &&
+                      reinterpret_cast<uintptr_t>(vi) % 8 == 0,
+                  SOLATTN_EINVAL, "prep_int8: misaligned outputs");
+  if (int rc = check_bthd(q, sq_b, sq_t, sq_h, "prep_int8 q")) return rc;
+  if (int rc = check_bthd(k, sk_b, sk_t, sk_h, "prep_int8 k")) return rc;
+  if (int rc = check_bthd(v, sv_b, sv_t, sv_h, "prep_int8 v")) return rc;
+  const size_t lds = static_cast<size_t>(NT) * 8 * sizeof(float);
+  SOLATTN_REQUIRE(lds <= 64 * 1024, SOLATTN_EUNSUPPORTED,
+                  "prep_int8: %lld blocks do not fit the single-read schedule", (long long)NT);
+  const int nteams = single_read_teams(B, T, H, block, pv, lds);
+  SOLATTN_REQUIRE(nteams > 0, SOLATTN_EUNSUPPORTED,
+                  "prep_int8: B=%lld T=%lld H=%lld do not fit the single-read schedule on this "
+                  "device (fewer than two heads' rows resident)",
+                  (long long)B, (long long)T, (long long)H);
+  PrepInt8Args a;
+  a.q = q; a.k = k; a.v = v;
+  a.sq_b = sq_b; a.sq_t = sq_t; a.sq_h = sq_h;
+  a.sk_b = sk_b; a.sk_t = sk_t; a.sk_h = sk_h;
+  a.sv_b = sv_b; a.sv_t = sv_t; a.sv_h = sv_h;
+  a.T = T; a.TP = TP; a.npad = npad;
+  a.B = static_cast<int>(B); a.H = static_cast<int>(H); a.NT = static_cast<int>(NT);
+  a.S = static_cast<int>(cdiv(T, kSpan)); a.nteams = nteams;
+  a.kc = kc; a.vc = vc; a.qbar = qbar; a.kc_mean = kc_mean; a.kc_var = kc_var;
+  a.vscale = vscale; a.vamax_part = pv ? vamax_part : nullptr;
+  a.qi = qi; a.ki = ki; a.vi = vi; a.qs = qs; a.ks = ks;
+  a.ks_st = ks_head_major ? 1 : H;
+  a.ks_sh = ks_head_major ? TP : 1;
+  a.sync = sync;
+  hipLaunchKernelGGL(sync_init_kernel, dim3(1), dim3(256), 0, stream, sync, nteams + 1);
+  if (int rc = check_launch("prep_int8 sync init")) return rc;
+  const void* kern = block == 64 ? (pv ? single_read_kernel<64, true>() : single_read_kernel<64, false>())
+                                 : (pv ? single_read_kernel<128, true>() : single_read_kernel<128, false>());
+  void* args[] = {&a};
+  const hipError_t e = hipLaunchCooperativeKernel(kern, dim3(static_cast<uint32_t>(nteams) * a.S),
+                                                  dim3(kPoolThreads), args, lds, stream);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return set_error(SOLATTN_ELAUNCH, "prep_int8: cooperative launch of %d x %d workgroups: %s",
+                     nteams, a.S, hipGetErrorString(e));
+  }
+  return check_launch("prep_int8");
+}
+
+}  // namespace solattn
+
+extern "C" int64_t solattn_prep_int8_sync_bytes(int64_t B, int64_t H) {
+  if (B <= 0 || H <= 0) return 0;
+  return cdiv(single_read_sync_words(B, H) * 4, 256) * 256;
+}
+
+extern "C" int solattn_prep_int8(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
+                                 const uint16_t* k, int64_t sk_b, int64_t sk_t, int64_t sk_h,
+                                 const uint16_t* v, int64_t sv_b, int64_t sv_t, int64_t sv_h,
+                                 int64_t B, int64_t T, int64_t H, int64_t D, int64_t block,
+                                 uint16_t* kc, uint16_t* vc, int64_t npad, float* qbar,
+                                 float* kc_mean, float* kc_var, float* vamax_part, float* vscale,
+                                 int8_t* qi, float* qs, int8_t* ki, float* ks, int ks_head_major,
+                                 int8_t* vi, int64_t TP, void* sync, int64_t sync_bytes,
+                                 solattn_stream_t stream) {
+  clear_error();
+  return prep_int8_single_read(q, sq_b, sq_t, sq_h, k, sk_b, sk_t, sk_h, v, sv_b, sv_t, sv_h, B,
+                               T, H, D, block, kc, vc, npad, qbar, kc_mean, kc_var, vamax_part,
+                               vscale, qi, qs, ki, ks, ks_head_major, vi, TP,
+                               static_cast<uint32_t*>(sync), sync_bytes,
+                               reinterpret_cast<hipStream_t>(stream));
 }

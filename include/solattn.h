@@ -171,6 +171,35 @@ int solattn_quant_v(const uint16_t* v, int64_t sv_b, int64_t sv_t, int64_t sv_h,
                     int64_t T, int64_t H, int64_t D, const float* vscale, int8_t* vi,
                     int64_t TP, solattn_stream_t stream);
 
+/* ------------------------------------------------------- single-read INT8 --
+ * The INT8 path's preparation with one read of q, k and v: pooled keys and
+ * values, query centroids, centred kc and its moments (solattn_moments with
+ * centre = 1), the V scale, per-token Q codes, per-token K codes smoothed by
+ * kc_mean and (vscale != NULL) per-channel V codes -- the outputs of
+ * solattn_pool + solattn_moments + solattn_quant_rows / solattn_quant_v, bit
+ * for bit. Each head's K and V rows stay in registers until its moments are
+ * known: the launch is cooperative (all workgroups resident) and the
+ * workgroups of a head meet at two barriers in device memory. Returns
+ * SOLATTN_EUNSUPPORTED when fewer than two heads' rows fit on the device at
+ * once (or D != 128); the caller then uses the two-pass entry points.
+ * vamax_part: fp32 [B, NT, H, D] scratch (with vscale); ks: [B, H, TP]
+ * (ks_head_major != 0) or [B, TP, H]; sync: device scratch of at least
+ * solattn_prep_int8_sync_bytes(B, H) bytes, reset by the call itself; its
+ * first uint32 is nonzero after the call only if a barrier was not met within
+ * ~0.1 s (results then invalid), which cannot happen with every workgroup
+ * resident.
+ * Replaces: fused_preprocess, /root/reference/_fused_prep.py:62-98, which reads
+ * K and V twice. */
+int64_t solattn_prep_int8_sync_bytes(int64_t B, int64_t H);
+int solattn_prep_int8(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
+                      const uint16_t* k, int64_t sk_b, int64_t sk_t, int64_t sk_h,
+                      const uint16_t* v, int64_t sv_b, int64_t sv_t, int64_t sv_h, int64_t B,
+                      int64_t T, int64_t H, int64_t D, int64_t block, uint16_t* kc,
+                      uint16_t* vc, int64_t npad, float* qbar, float* kc_mean, float* kc_var,
+                      float* vamax_part, float* vscale, int8_t* qi, float* qs, int8_t* ki,
+                      float* ks, int ks_head_major, int8_t* vi, int64_t TP, void* sync,
+                      int64_t sync_bytes, solattn_stream_t stream);
+
 /* ------------------------------------------------------------- forwards --
  * Sparse attention over exact blocks (flash attention on MFMA) plus the pooled
  * branch (one pooled key kc_j and value vc_j per approximate block, softmax
