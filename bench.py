@@ -409,6 +409,10 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                      "traffic": _traffic() if (args.config, block, H) == (2, 128, 24) else None,
+                     "traffic_source": ("profiles/fwd_bf16_video32k_traffic.json: rocprofv3 "
+                                        "FETCH_SIZE + WRITE_SIZE of this kernel, calibrated on "
+                                        "a 512 MiB copy (not measured by this run)")
+                     if (args.config, block, H) == (2, 128, 24) else None,
                      "kernel": ("bf16fwd::fwd_bf16_kernel<128>" if block == 128
                                 else "bf16fwd::fwd_bf16_sbuf_kernel<64>"),
                      "algorithmic_flops_per_launch": rflops, "launch_ms": round(fwd_ms, 4)},
