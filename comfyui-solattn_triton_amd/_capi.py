@@ -54,7 +54,7 @@ SIGNATURES = {
 
 # Size of the per-device scratch array behind solattn_sol_attn_noalloc
 # (SOLATTN_NOALLOC_SCRATCH_BYTES).
-NOALLOC_SCRATCH_BYTES = 64 << 20
+NOALLOC_SCRATCH_BYTES = 32 << 20
 QUANT_BLOCK = 128  # tokens per scale of the per-block INT8 variant (SOLATTN_QUANT_BLOCK)
 
 

@@ -304,8 +304,9 @@ int solattn_sol_attn_int8_qblock(const uint16_t* q, int64_t sq_b, int64_t sq_t, 
  * streams, or threads without ordering) race and must be serialised by the
  * caller. Nothing in the array needs clearing between calls. Same arguments,
  * results and errors as solattn_sol_attn otherwise; the device is the current
- * one. Covers cfg-4-sized calls (B1 H40 T75600 at block 128). */
-#define SOLATTN_NOALLOC_SCRATCH_BYTES (64ll << 20)
+ * one. 32 MiB covers a B1 H40 T75600 call at block 128 (26 MiB) and a B1 H24
+ * T32760 call at either block size (13 MiB at block 64). */
+#define SOLATTN_NOALLOC_SCRATCH_BYTES (32ll << 20)
 int solattn_sol_attn_noalloc(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
                              const uint16_t* k, int64_t sk_b, int64_t sk_t, int64_t sk_h,
                              const uint16_t* v, int64_t sv_b, int64_t sv_t, int64_t sv_h,
