@@ -242,14 +242,16 @@ def run_kernel_only(args, mods, cfg, q, k, v):
         out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
         for _ in range(args.steps):
             mods["_tri_fwd"].forward_bf16(q, k, v, r, out=out)
-    elif args.kernel_only in ("fwd_int8", "fwd_int8_bf16pv"):
+    elif args.kernel_only in ("fwd_int8", "fwd_int8_bf16pv", "fwd_int8_run"):
         fp = mods["_fused_prep"].fused_preprocess_routing(q, k, v, tau=tau, scale=D ** -0.5,
                                                           block=block)
         r, qi, qs, ki, ks, vi = fp
         out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
-        pv = args.kernel_only == "fwd_int8"
+        pv = args.kernel_only != "fwd_int8_bf16pv"
+        codes = "running" if args.kernel_only == "fwd_int8_run" else "block"
         for _ in range(args.steps):
-            mods["_int8_fwd"].forward_int8(q, v, r, qi, qs, ki, ks, vi, int8_pv=pv, out=out)
+            mods["_int8_fwd"].forward_int8(q, v, r, qi, qs, ki, ks, vi, int8_pv=pv, out=out,
+                                           pv_codes=codes)
     elif args.kernel_only == "quant":
         fq = importlib.import_module(mods["_preprocess"].__name__.rsplit(".", 1)[0] + "._fused_quant")
         fp = mods["_fused_prep"].fused_preprocess_routing(q, k, v, tau=tau, scale=D ** -0.5,
@@ -259,10 +261,12 @@ def run_kernel_only(args, mods, cfg, q, k, v):
             fq.quantize_bthd(q)
             fq.quantize_bthd(k, mean=r.kc_mean.reshape(-1, D))
             fq.quantize_v_per_channel(v)
-    elif args.kernel_only in ("int8_call", "int8_bf16pv_call"):
-        pv = args.kernel_only == "int8_call"
+    elif args.kernel_only in ("int8_call", "int8_bf16pv_call", "int8_run_call"):
+        pv = args.kernel_only != "int8_bf16pv_call"
+        codes = "running" if args.kernel_only == "int8_run_call" else "block"
         for _ in range(args.steps):
-            mods["_int8_fwd"].sol_attn_int8(q, k, v, tau=tau, block=block, int8_pv=pv)
+            mods["_int8_fwd"].sol_attn_int8(q, k, v, tau=tau, block=block, int8_pv=pv,
+                                            pv_codes=codes)
     elif args.kernel_only == "bf16_call":
         for _ in range(args.steps):
             mods["_tri_fwd"].sol_attn(q, k, v, tau=tau, block=block)
@@ -335,8 +339,9 @@ def main():
     ap.add_argument("--heads", type=int,
                     help="number of heads instead of the config's, e.g. 3 = one GPU's share of an "
                          "8-way head split at cfg 2 (not the metric)")
-    ap.add_argument("--kernel-only", choices=["fwd", "fwd_int8", "fwd_int8_bf16pv", "prep", "quant",
-                                              "reorder", "int8_call", "int8_bf16pv_call", "bf16_call"],
+    ap.add_argument("--kernel-only", choices=["fwd", "fwd_int8", "fwd_int8_bf16pv", "fwd_int8_run",
+                                              "prep", "quant", "reorder", "int8_call",
+                                              "int8_bf16pv_call", "int8_run_call", "bf16_call"],
                     help="profiling driver: run only this kernel --steps times (after a "
                          "512 MiB device copy used to calibrate memory counters); no JSON")
     args = ap.parse_args()
@@ -427,13 +432,17 @@ def main():
     if args.extra:
         i8 = mods["_int8_fwd"].sol_attn_int8
         # int8 QK, bf16 P.V; the reference's default int8 P.V beside it
-        for key, pv in (("int8_ms", False), ("int8_pv_ms", True)):
-            line[key] = {str(t): round(time_cuda(lambda: i8(q, k, v, tau=t, block=block, int8_pv=pv),
+        # (_run: int8 P.V with codes against the running max, SOLATTN_PV_INT8_RUNNING)
+        for key, pv, codes in (("int8_ms", False, "block"), ("int8_pv_ms", True, "block"),
+                               ("int8_pv_run_ms", True, "running")):
+            line[key] = {str(t): round(time_cuda(lambda: i8(q, k, v, tau=t, block=block, int8_pv=pv,
+                                                            pv_codes=codes),
                                                  args.steps, args.warmup), 4) for t in (0.8, 0.9, 0.95)}
         # config 3's wording, Q/K scales per 128-token block (not the parity mode)
-        for key, pv in (("int8_qblock_ms", False), ("int8_pv_qblock_ms", True)):
+        for key, pv, codes in (("int8_qblock_ms", False, "block"), ("int8_pv_qblock_ms", True, "block"),
+                               ("int8_pv_run_qblock_ms", True, "running")):
             line[key] = {str(t): round(time_cuda(lambda: i8(q, k, v, tau=t, block=block, int8_pv=pv,
-                                                            quant_block=128),
+                                                            quant_block=128, pv_codes=codes),
                                                  args.steps, args.warmup), 4) for t in (0.8, 0.9, 0.95)}
         # the INT8 forward kernel alone at the config's tau, against the MFMA roofline
         fp = mods["_fused_prep"].fused_preprocess_routing(q, k, v, tau=tau, scale=D ** -0.5,
@@ -442,9 +451,11 @@ def main():
         exact, pooled = split_ops(ri.counts.cpu(), ri.mask.cpu(), T, block, D)
         out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
         line["int8_fwd"] = {}
-        for key, pv in (("pv_bf16", False), ("pv_int8", True)):
+        for key, pv, codes in (("pv_bf16", False, "block"), ("pv_int8", True, "block"),
+                               ("pv_int8_run", True, "running")):
             ms_i8 = time_cuda(lambda: mods["_int8_fwd"].forward_int8(q, v, ri, qi, qs, ki, ks, vi,
-                                                                     int8_pv=pv, out=out),
+                                                                     int8_pv=pv, out=out,
+                                                                     pv_codes=codes),
                               args.steps, args.warmup)
             line["int8_fwd"][key] = int8_roofline(ms_i8, exact, pooled, pv)
         line["int8_fwd"]["routed_density"] = round(float(ri.counts.double().sum()

@@ -196,6 +196,12 @@ if _COMFY_ERROR is None:
                     io.Combo.Input("block_size", options=_BLOCK_CHOICES, default="64", optional=True,
                                    tooltip="Routing block in tokens. 64 is the reference's; 128 "
                                            "halves the pooled branch and suits long video."),
+                    io.Combo.Input("int8_pv_codes", options=["block", "running"], default="block",
+                                   optional=True,
+                                   tooltip="With int8_pv: quantise P against each routed block's "
+                                           "max (the reference's) or against the row's running "
+                                           "max (int32 sums across blocks: a faster INT8 "
+                                           "forward, coarser codes for blocks below the max)."),
                 ],
                 outputs=[io.Model.Output()],
             )
@@ -203,7 +209,8 @@ if _COMFY_ERROR is None:
         @classmethod
         def execute(cls, model, tau, start_percent, end_percent, min_tokens, int8_qk,
                     sink_conditioning, morton, morton_curve, dense_blocks, verbose,
-                    tau_profile=None, use_tma=False, int8_pv=True, block_size="64") -> io.NodeOutput:
+                    tau_profile=None, use_tma=False, int8_pv=True, block_size="64",
+                    int8_pv_codes="block") -> io.NodeOutput:
             _require_kernels(int8_qk)
             block = int(block_size)
             diffusion_model = model.get_model_object("diffusion_model")
@@ -226,7 +233,7 @@ if _COMFY_ERROR is None:
                 tau=tau, min_tokens=min_tokens, sigma_start=window[0], sigma_end=window[1],
                 verbose=verbose, int8_qk=int8_qk, sink_conditioning=sink_conditioning,
                 use_tma=use_tma, dense_blocks=dense, tau_profile=profile, int8_pv=int8_pv,
-                previous=previous, block=block)
+                previous=previous, block=block, pv_codes=int8_pv_codes)
             options["sol_block_size"] = block
             if reorder:
                 options.update(sol_morton=True, sol_morton_curve=morton_curve)

@@ -234,7 +234,7 @@ def _ineligible(q, k, mask, dim_head, min_tokens, block=BLOCK_SIZE):
 
 def _run(q, k, v, heads, skip_reshape, skip_output_reshape, scale, tau, min_tokens, verbose,
          int8_qk=False, sink_blocks=(0, 0), sink_q=(0, 0), use_tma=False, int8_pv=True,
-         block=BLOCK_SIZE):
+         block=BLOCK_SIZE, pv_codes="block"):
     """The sparse attention output in the caller's layout, or None when the
     call stays dense (/root/reference/__init__.py:192-231). Strided views go
     to the kernels as they are."""
@@ -251,7 +251,7 @@ def _run(q, k, v, heads, skip_reshape, skip_output_reshape, scale, tau, min_toke
     if int8_qk:
         if _sol_attn_int8_kernel is None:
             raise RuntimeError(f"Sol-Attn INT8 kernel unavailable: {_INT8_IMPORT_ERROR}")
-        out = _sol_attn_int8_kernel(qs, ks, vs, int8_pv=int8_pv, **args)
+        out = _sol_attn_int8_kernel(qs, ks, vs, int8_pv=int8_pv, pv_codes=pv_codes, **args)
     else:
         out = _sol_attn_kernel(qs, ks, vs, **args)
     _stats["sparse"] += 1
@@ -294,6 +294,7 @@ class SparsePolicy:
     tau_profile: Optional[dict] = field(default=None, hash=False)
     int8_pv: bool = True
     block: int = BLOCK_SIZE
+    pv_codes: str = "block"  # int8 P codes: against each block's max, or "running"
 
     def block_index(self, call: AttentionCall):
         if not (self.dense_blocks or self.tau_profile):
@@ -357,7 +358,7 @@ class SolAttnOverride:
         try:
             out = _run(q, k, v, heads, skip_reshape, skip_output_reshape, kwargs.get("scale"),
                        tau, policy.min_tokens, policy.verbose, policy.int8_qk, sink, sink_q,
-                       policy.use_tma, policy.int8_pv, policy.block)
+                       policy.use_tma, policy.int8_pv, policy.block, policy.pv_codes)
         except Exception as exc:
             _stats["errors"] += 1
             _log_kernel_failure(exc)
@@ -368,13 +369,15 @@ class SolAttnOverride:
 def make_override(tau=1.0, min_tokens=MIN_TOKENS, sigma_start=None, sigma_end=None, verbose=False,
                   int8_qk=False, sink_conditioning="exact_kv", use_tma=False,
                   dense_blocks=frozenset(), tau_profile=None, int8_pv=True, previous=None,
-                  block=BLOCK_SIZE):
-    """An optimized_attention_override (/root/reference/__init__.py:256-320)."""
+                  block=BLOCK_SIZE, pv_codes="block"):
+    """An optimized_attention_override (/root/reference/__init__.py:256-320).
+    ``pv_codes="running"`` (with int8_qk and int8_pv): P codes against the row's
+    running max, an option of this build (the default is the reference's)."""
     policy = SparsePolicy(tau=tau, min_tokens=min_tokens, sigma_start=sigma_start,
                           sigma_end=sigma_end, verbose=verbose, int8_qk=int8_qk,
                           sink_conditioning=sink_conditioning, use_tma=use_tma,
                           dense_blocks=frozenset(dense_blocks), tau_profile=tau_profile or None,
-                          int8_pv=int8_pv, block=int(block))
+                          int8_pv=int8_pv, block=int(block), pv_codes=pv_codes)
     return SolAttnOverride(policy, previous)
 
 

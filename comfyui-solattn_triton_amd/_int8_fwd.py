@@ -16,18 +16,36 @@ from ._preprocess import BLOCK_SIZE, Routing, as_kernel_input, check_inputs
 from ._tri_fwd import _workspace
 
 BLOCK = BLOCK_SIZE
+# How the int8 P.V forms its P codes (int8_pv=True): against each routed
+# block's row max (the reference's arithmetic), or against the row's running
+# max with int32 sums across blocks (SOLATTN_PV_INT8_RUNNING: no per-block
+# conversion; coarser codes for blocks below the running max).
+PV_CODES = ("block", "running")
 
-__all__ = ["sol_attn_int8", "forward_int8"]
+__all__ = ["sol_attn_int8", "forward_int8", "PV_CODES"]
+
+
+def _pv_mode(int8_pv, pv_codes) -> int:
+    """The C ABI's int8_pv value: SOLATTN_PV_BF16 (0), SOLATTN_PV_INT8 (1) or
+    SOLATTN_PV_INT8_RUNNING (2)."""
+    if pv_codes not in PV_CODES:
+        raise ValueError(f"pv_codes must be one of {PV_CODES}, got {pv_codes!r}")
+    if not int8_pv:
+        return 0
+    return 2 if pv_codes == "running" else 1
 
 
 def sol_attn_int8(q, k, v, *, scale=None, tau=1.0, sink_blocks=(0, 0), sink_q=(0, 0),
-                  use_tma=False, int8_pv=True, block=BLOCK, quant_block=None):
+                  use_tma=False, int8_pv=True, block=BLOCK, quant_block=None, pv_codes="block"):
     """Sol-Attn with an INT8 exact branch. Same contract as ``sol_attn``.
     ``quant_block=128`` quantises Q and smoothed K with one scale per 128-token
     block instead of per token (an option of this build, BASELINE config 3's
-    wording; the default is the reference's per-token rule)."""
+    wording; the default is the reference's per-token rule). ``pv_codes``
+    (with ``int8_pv``): "block" quantises P against each routed block's row
+    max, as the reference; "running" against the row's running max."""
     if quant_block not in (None, QUANT_BLOCK):
         raise ValueError(f"quant_block must be None or {QUANT_BLOCK}, got {quant_block}")
+    mode = _pv_mode(int8_pv, pv_codes)
     check_inputs(q, k, v, block)
     scale = q.shape[-1] ** -0.5 if scale is None else float(scale)
     q, k, v = as_kernel_input(q), as_kernel_input(k), as_kernel_input(v)
@@ -39,15 +57,16 @@ def sol_attn_int8(q, k, v, *, scale=None, tau=1.0, sink_blocks=(0, 0), sink_q=(0
              ptr(q), q.stride(0), q.stride(1), q.stride(2), ptr(k),
              k.stride(0), k.stride(1), k.stride(2), ptr(v), v.stride(0), v.stride(1), v.stride(2),
              B, T, H, D, block, float(scale), float(tau), int(sink_blocks[0]), int(sink_blocks[1]),
-             int(sink_q[0]), int(sink_q[1]), 1 if int8_pv else 0, ptr(ws), ws.numel(), ptr(out),
+             int(sink_q[0]), int(sink_q[1]), mode, ptr(ws), ws.numel(), ptr(out),
              out.stride(0), out.stride(1), out.stride(2), stream(q.device))
     return out
 
 
 def forward_int8(q, v, routing: Routing, qi, qs, ki, ks, vi=None, *, scale=None, int8_pv=True,
-                 out=None):
+                 out=None, pv_codes="block"):
     """The INT8 forward kernel alone (head dim 128), on the outputs of
     ``fused_preprocess_routing``."""
+    mode = _pv_mode(int8_pv, pv_codes)
     check_inputs(q, q, q, routing.block, padded_ok=False)
     scale = q.shape[-1] ** -0.5 if scale is None else float(scale)
     q, v = as_kernel_input(q), as_kernel_input(v)
@@ -62,6 +81,6 @@ def forward_int8(q, v, routing: Routing, qi, qs, ki, ks, vi=None, *, scale=None,
              ptr(routing.vscale if int8_pv else None), ptr(v), v.stride(0), v.stride(1),
              v.stride(2), TP, ptr(routing.kc), ptr(routing.vc), npad, ptr(routing.counts),
              ptr(routing.mask), B, T, H, D, routing.block, float(scale),
-             1 if int8_pv else 0, ptr(out), out.stride(0), out.stride(1), out.stride(2),
+             mode, ptr(out), out.stride(0), out.stride(1), out.stride(2),
              stream(q.device))
     return out

@@ -109,7 +109,7 @@ using namespace solattn;
 
 extern "C" const char* solattn_last_error(void) { return g_error; }
 
-extern "C" int solattn_abi_version(void) { return (2 << 16) | 0; }
+extern "C" int solattn_abi_version(void) { return (2 << 16) | 1; }
 
 extern "C" int solattn_morton_perm(int64_t frames, int64_t height, int64_t width, int curve,
                                    int64_t roll, int64_t* perm, int64_t* inverse) {
@@ -360,6 +360,8 @@ namespace {
 int sol_attn_int8_call(SOLATTN_INT8_CALL_PARAMS, int qk_block) {
   clear_error();
   if (int rc = check_pipeline(B, T, H, D, block, "sol_attn_int8")) return rc;
+  SOLATTN_REQUIRE(int8_pv >= SOLATTN_PV_BF16 && int8_pv <= SOLATTN_PV_INT8_RUNNING, SOLATTN_EINVAL,
+                  "sol_attn_int8: int8_pv %d is not a SOLATTN_PV_* mode", int8_pv);
   const Layout L(B, T, H, D, block, true);
   SOLATTN_REQUIRE(workspace && workspace_bytes >= L.total, SOLATTN_ESIZE,
                   "sol_attn_int8: workspace %lld < %lld bytes", (long long)workspace_bytes,

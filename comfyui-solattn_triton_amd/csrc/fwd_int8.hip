@@ -128,16 +128,86 @@ __device__ __forceinline__ uint32_t probs_i8(const f32x16& s, float qsl, float n
 }
 constexpr float kLog2_127 = 6.98868468677216585f;  // log2(127)
 
+// ------------------------------------------- running-max int8 P . V (RUN)
+// Codes against the row's running max instead of each block's own max, so
+// that the P.V products of all exact blocks accumulate in int32 with no
+// per-block conversion. During the exact tiles st.m is an integer (log2
+// domain) at or above every scaled score seen; st.acc holds the int32 sums
+// code_p * code_v of O^T (bit for bit in the fp32 registers) and st.l the sum
+// of the codes as an fp32 value, both in units of 2^st.m / 127. A unit (a
+// block, or a 64-key tile) whose max exceeds st.m raises it to ceil(max) and
+// scales both by 2^-(the difference): the int32 sums by an arithmetic shift
+// (rounding toward -inf, less than one unit of sums of order 10^4), the code
+// sum exactly (ldexp; it is split over the two lanes of a row, and small
+// right after a large rise, so flooring it would bias the softmax
+// denominator). Overflow: |sums| <= 127 * (code sum of the row), so while
+// each lane's half of the code sum stays at most 2^23 the sums stay below
+// 127 * 2^24 + 2^21 < 2^31 after one more unit (a unit of 128 keys adds less
+// than 128 * 127 * 127 < 2^21); past that st.m rises by one more, for both
+// lanes of the row.
+constexpr float kRunLaneSumLimit = 8388608.f;  // 2^23
+__device__ __forceinline__ void run_max(SoftmaxState& st, float bmax) {
+  float m_new = fmaxf(st.m, ceilf(bmax));
+  if (xhalf_max(st.l) > kRunLaneSumLimit) m_new += 1.f;
+  const float d = m_new - st.m;  // +inf on the first unit: st.m = -inf, sums 0
+  const int k = d < 31.f ? static_cast<int>(d) : 31;
+  st.m = m_new;
+  if (__any(k != 0)) {
+    // whole-vector shifts: written per element (bit casts of vector
+    // elements), clang 22 -O3 folded the 16 results into one value
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      const i32x16 a = __builtin_bit_cast(i32x16, st.acc[dt]) >> k;
+      st.acc[dt] = __builtin_bit_cast(f32x16, a);
+    }
+    st.l = __builtin_amdgcn_ldexpf(st.l, -k);
+  }
+}
+
+// RUN, after the exact tiles: the int32 sums back to the fp32 state,
+// O^T = sums * vscale[d] / 127 and l = code sum / 127, relative to 2^st.m.
+__device__ __forceinline__ void run_finish(SoftmaxState& st, const float* vsc, int half) {
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) {
+    const i32x16 a = __builtin_bit_cast(i32x16, st.acc[dt]);
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      st.acc[dt][r] = static_cast<float>(a[r]) *
+                      (vsc[32 * dt + 8 * (r >> 2) + 4 * half + (r & 3)] * (1.f / 127.f));
+  }
+  st.l *= 1.f / 127.f;
+}
+
 // O^T += (Vi^T . Pi^T) * f: lane (channel 32dt + col, half) takes keys
 // 32ks + 8i + 4half + j (i, j < 4) of the int8 V tile from two ds_read_tr8:
 // within a 16-lane group, lane s supplies key (s >> 1) of the 8 keys read,
 // channels 8(s & 1) .. +7.
+// RUN: the products accumulate into the int32 sums held in acc (f unused).
+template <bool RUN>
 __device__ __forceinline__ void pv_i8(const char* vt, const i32x4 (&pi)[2], float f, int lane,
                                       f32x16 (&acc)[4]) {
   const i32x16 zero = {};
   const int g = lane >> 4, sl = lane & 15, half = lane >> 5;
   const int kk = sl >> 1;
   const int key_in = 8 * (kk >> 2) + 4 * half + (kk & 3);
+  if constexpr (RUN) {
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      const int chunk = 2 * dt + (g & 1);
+      i32x16 a32 = __builtin_bit_cast(i32x16, acc[dt]);
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const int r0 = 32 * ks + key_in, r1 = r0 + 16;
+        const i32x2 lo = tr8(vt + r0 * kI8Row + swz_vi(r0, chunk) * 16 + 8 * (sl & 1));
+        const i32x2 hi = tr8(vt + r1 * kI8Row + swz_vi(r1, chunk) * 16 + 8 * (sl & 1));
+        const i32x4 a = {lo[0], lo[1], hi[0], hi[1]};
+        a32 = mfma_i8(a, pi[ks], a32);
+      }
+      acc[dt] = __builtin_bit_cast(f32x16, a32);
+      asm volatile("" : "+v"(acc[dt]));
+    }
+    return;
+  }
   const auto tile = [&](int dt) {
     const int chunk = 2 * dt + (g & 1);
     i32x16 pv;
@@ -167,8 +237,9 @@ __device__ __forceinline__ void pv_i8(const char* vt, const i32x4 (&pi)[2], floa
 }
 
 // Softmax + P.V of an exact tile whose scaled scores are in s (masked keys
-// already -inf): /root/reference/_int8_fwd.py:333-368.
-template <bool INT8_PV>
+// already -inf): /root/reference/_int8_fwd.py:333-368. RUN: codes against
+// the running max, into the int32 sums (run_max).
+template <bool INT8_PV, bool RUN = false>
 __device__ __forceinline__ void exact_softmax_pv(SoftmaxState& st, f32x16 (&s)[2], const void* vt,
                                                  float qsl, int lane) {
   float mx = -INFINITY;
@@ -177,6 +248,15 @@ __device__ __forceinline__ void exact_softmax_pv(SoftmaxState& st, f32x16 (&s)[2
 #pragma unroll
     for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[m][r]);
   const float bmax = xhalf_max(mx) * qsl;
+  if constexpr (INT8_PV && RUN) {
+    run_max(st, bmax);
+    i32x4 pi[2];
+    uint32_t csum = probs_i8(s[0], qsl, kLog2_127 - st.m, pi[0], 0u);
+    csum = probs_i8(s[1], qsl, kLog2_127 - st.m, pi[1], csum);
+    st.l += static_cast<float>(csum);
+    pv_i8<true>(static_cast<const char*>(vt), pi, 0.f, lane, st.acc);
+    return;
+  }
   float alpha;
   st.m = new_max(st.m, bmax, alpha);
   if constexpr (INT8_PV) {
@@ -186,7 +266,7 @@ __device__ __forceinline__ void exact_softmax_pv(SoftmaxState& st, f32x16 (&s)[2
     csum = probs_i8(s[1], qsl, kLog2_127 - bmax, pi[1], csum);
     st.l = fmaf(st.l, alpha, beta * (1.f / 127.f) * static_cast<float>(csum));
     rescale(st, alpha);
-    pv_i8(static_cast<const char*>(vt), pi, beta * (1.f / 127.f), lane, st.acc);
+    pv_i8<false>(static_cast<const char*>(vt), pi, beta * (1.f / 127.f), lane, st.acc);
   } else {
     const float neg = -st.m;
     bf16x8 pb[4];
@@ -433,7 +513,7 @@ __device__ __forceinline__ void step3_i8(SoftmaxState& st, const f32x16 (&sc)[2]
   st.l = fmaf(st.l, alpha, psum);
 }
 
-template <bool INT8_PV, bool UKS, typename Mid>
+template <bool INT8_PV, bool UKS, bool RUN, typename Mid>
 __device__ __forceinline__ void fast_step(SoftmaxState& st, f32x16 (&sc)[2], f32x16 (&sn)[2],
                                           const char* kn, const void* vt, const i32x4 (&qi)[4],
                                           float qsl, int lane, Mid&& mid) {
@@ -449,7 +529,7 @@ __device__ __forceinline__ void fast_step(SoftmaxState& st, f32x16 (&sc)[2], f32
   // running max as it stands; the tile max is taken only when a lane's row
   // sum exceeds 255, or is inf on a first tile with the running max -inf), so
   // the running max evolves as if taken every tile. int8 P.V needs the block
-  // max itself: its P codes are relative to it.
+  // max itself: its P codes are relative to it (RUN: to the running max).
   float mx = -INFINITY, alpha = 1.f, bmax = 0.f, neg = INT8_PV ? 0.f : -st.m, psum = 0.f;
   uint32_t csum = 0u;
   bf16x8 pb[4];
@@ -470,11 +550,16 @@ __device__ __forceinline__ void fast_step(SoftmaxState& st, f32x16 (&sc)[2], f32
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[m][r]);
       bmax = xhalf_max(mx) * qsl;
-      st.m = new_max(st.m, bmax, alpha);
+      if constexpr (RUN) {
+        run_max(st, bmax);
+        bmax = st.m;  // the codes' reference
+      } else {
+        st.m = new_max(st.m, bmax, alpha);
+      }
       neg = -st.m;
     } else if (cc == 1) {
       if constexpr (INT8_PV) {
-        csum = probs_i8(sc[0], qsl, kLog2_127 - bmax, pi[0], 0u);
+        csum = probs_i8(sc[0], qsl, kLog2_127 - bmax, pi[0], csum);
       } else {
         psum = exp8<0>(sc[0], qsl, neg, pb[0], psum);
         psum = exp8<8>(sc[0], qsl, neg, pb[1], psum);
@@ -503,17 +588,19 @@ __device__ __forceinline__ void fast_step(SoftmaxState& st, f32x16 (&sc)[2], f32
     }
   }
   float beta = 1.f;
-  if constexpr (INT8_PV) {
+  if constexpr (INT8_PV && RUN) {
+    st.l += static_cast<float>(csum);
+  } else if constexpr (INT8_PV) {
     beta = __builtin_amdgcn_exp2f(bmax - st.m);
     st.l = fmaf(st.l, alpha, beta * (1.f / 127.f) * static_cast<float>(csum));
   } else {
     st.l = fmaf(st.l, alpha, psum);
   }
-  rescale(st, alpha);
+  if constexpr (!RUN) rescale(st, alpha);
   if constexpr (INT8_PV) {
     scale_scores<UKS>(kn, si, half, sn);  // frees the int32 scores before the P.V accumulators
     mid();
-    pv_i8(static_cast<const char*>(vt), pi, beta * (1.f / 127.f), lane, st.acc);
+    pv_i8<RUN>(static_cast<const char*>(vt), pi, beta * (1.f / 127.f), lane, st.acc);
   } else {
     mid();
     pv_tile(static_cast<const uint16_t*>(vt), pb, lane, st.acc);
@@ -592,7 +679,7 @@ __device__ __forceinline__ void issue_i8(uint32_t dst, const int8_t* rows, const
 // with bf16 P.V one bf16 V tile (VSINGLE: 36 KB, four workgroups per CU, two
 // waves on every SIMD), copied after the step's P.V and waited for before the
 // next one's.
-template <int BLK, bool INT8_PV, bool UKS>
+template <int BLK, bool INT8_PV, bool UKS, bool RUN>
 __global__ void __launch_bounds__(BLK * 2)
 __attribute__((amdgpu_waves_per_eu(2)))
 fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
@@ -739,7 +826,7 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
         for (int r = 0; r < 16; ++r)
           s[m][r] = ((bits >> (8 * (r >> 2) + (r & 3))) & 1u) ? s[m][r] : -INFINITY;
       }
-      exact_softmax_pv<INT8_PV>(st, s, Vp(0), tile_qsl<UKS>(kt, kKsOffset, qsl), lane);
+      exact_softmax_pv<INT8_PV, RUN>(st, s, Vp(0), tile_qsl<UKS>(kt, kKsOffset, qsl), lane);
       __syncthreads();
       if constexpr (VSINGLE) {
         if (1 < nexact) issue_exact_full(1, 0u, vbuf_at(0), false, true);
@@ -814,7 +901,7 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
             last(sb, fb, sa, pa, pb);
           }
         } else {
-          exact_softmax_pv<INT8_PV>(st, sa, Vp(bi(n)), fa, lane);
+          exact_softmax_pv<INT8_PV, RUN>(st, sa, Vp(bi(n)), fa, lane);
         }
         __syncthreads();
       } else {
@@ -827,7 +914,7 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
         issue_exact_full(min(n + 2, E - 1), kbuf_at(n & 1), 0u, true, false);
         if constexpr (!VSINGLE) issue_exact_full(n + 1, 0u, vbuf_at((n + 1) & 1), false, true);
         const char* kn = reinterpret_cast<const char*>(Kp((n + 1) & 1));
-        fast_step<INT8_PV, UKS>(st, sc, sn, kn, Vp(n & 1), qireg, qc, lane, [&] {
+        fast_step<INT8_PV, UKS, RUN>(st, sc, sn, kn, Vp(n & 1), qireg, qc, lane, [&] {
           if constexpr (VSINGLE) {
             wait_vmcnt<kKCopies>();
             __syncthreads();
@@ -849,14 +936,14 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
         wait_tile_copies();  // V of the last tile
         __syncthreads();
         if (odd)
-          exact_softmax_pv<INT8_PV>(st, sb, Vp(bi(n)), fb, lane);
+          exact_softmax_pv<INT8_PV, RUN>(st, sb, Vp(bi(n)), fb, lane);
         else
-          exact_softmax_pv<INT8_PV>(st, sa, Vp(bi(n)), fa, lane);
+          exact_softmax_pv<INT8_PV, RUN>(st, sa, Vp(bi(n)), fa, lane);
       } else if (n + 1 < E) {
         step(sa, fa, sb, fb);
-        exact_softmax_pv<INT8_PV>(st, sb, Vp(bi(n)), fb, lane);
+        exact_softmax_pv<INT8_PV, RUN>(st, sb, Vp(bi(n)), fb, lane);
       } else {
-        exact_softmax_pv<INT8_PV>(st, sa, Vp(bi(n)), fa, lane);
+        exact_softmax_pv<INT8_PV, RUN>(st, sa, Vp(bi(n)), fa, lane);
       }
       __syncthreads();
       }
@@ -867,10 +954,14 @@ fwd_int8_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int6
       // hold 64 VGPRs through the whole pipeline.
       const float* vsc = vscale + static_cast<int64_t>(bh) * kD;
       asm volatile("" : "+s"(vsc));
+      if constexpr (RUN) {
+        run_finish(st, vsc, half);
+      } else {
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
+        for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) st.acc[dt][r] *= vsc[32 * dt + 8 * (r >> 2) + 4 * half + (r & 3)];
+          for (int r = 0; r < 16; ++r) st.acc[dt][r] *= vsc[32 * dt + 8 * (r >> 2) + 4 * half + (r & 3)];
+      }
     }
   }
 
@@ -974,33 +1065,39 @@ __device__ __forceinline__ i32x16 qk_chunk(const char* kt, const i32x4 (&qi)[4],
 }
 
 // O^T += (Vi^T . Pi^T) * f over the 128 keys of a block (4 MFMAs per channel
-// tile into one int32 accumulator); lane layout as pv_i8.
-template <typename Mid>
+// tile into one int32 accumulator); lane layout as pv_i8. RUN: the MFMAs
+// accumulate into the int32 sums held in acc (f unused).
+template <bool RUN, typename Mid>
 __device__ __forceinline__ void pv_blk(const char* vt, const i32x4 (&pi)[4], float f, int lane,
                                        f32x16 (&acc)[4], Mid&& mid) {
   const i32x16 zero = {};
   const int g = lane >> 4, sl = lane & 15, half = lane >> 5;
   const int kk = sl >> 1;
   const int key_in = 8 * (kk >> 2) + 4 * half + (kk & 3);
-  const auto tile = [&](int dt) {
+  const auto tile = [&](int dt, i32x16 pv, bool first) {
     const int chunk = 2 * dt + (g & 1);
-    i32x16 pv;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       const int r0 = 32 * ks + key_in, r1 = r0 + 16;
       const i32x2 lo = tr8(vt + r0 * kI8Row + swz_vi(r0, chunk) * 16 + 8 * (sl & 1));
       const i32x2 hi = tr8(vt + r1 * kI8Row + swz_vi(r1, chunk) * 16 + 8 * (sl & 1));
       const i32x4 a = {lo[0], lo[1], hi[0], hi[1]};
-      pv = mfma_i8(a, pi[ks], ks == 0 ? zero : pv);
+      pv = mfma_i8(a, pi[ks], ks == 0 && first ? zero : pv);
     }
     return pv;
   };
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) {
-    const i32x16 pv = tile(dt);
-    mid(dt);  // independent VALU work beside this tile's MFMAs
+    if constexpr (RUN) {
+      const i32x16 pv = tile(dt, __builtin_bit_cast(i32x16, acc[dt]), false);
+      mid(dt);
+      acc[dt] = __builtin_bit_cast(f32x16, pv);
+    } else {
+      const i32x16 pv = tile(dt, zero, true);
+      mid(dt);  // independent VALU work beside this tile's MFMAs
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[dt][r] = fmaf(static_cast<float>(pv[r]), f, acc[dt][r]);
+      for (int r = 0; r < 16; ++r) acc[dt][r] = fmaf(static_cast<float>(pv[r]), f, acc[dt][r]);
+    }
     asm volatile("" : "+v"(acc[dt]));
   }
 }
@@ -1008,8 +1105,9 @@ __device__ __forceinline__ void pv_blk(const char* vt, const i32x4 (&pi)[4], flo
 // Block step: the i8 MFMAs of S(b+1) (chunk 0 beside the row max of block b,
 // chunks 1-2 beside its P codes), then P(b).V(b) and the conversion of
 // S(b+1) into scaled scores while block b+1's ks are in LDS. QK = false: the
-// last block (softmax and P.V only). qsl: the factor of sc's scores.
-template <bool QK, bool UKS>
+// last block (softmax and P.V only). qsl: the factor of sc's scores. RUN:
+// codes against the running max, into the int32 sums (run_max).
+template <bool QK, bool UKS, bool RUN>
 __device__ __forceinline__ void block_step(SoftmaxState& st, const f32x16 (&sc)[4], f32x16 (&sn)[4],
                                            const char* kn, const char* vt, const i32x4 (&qi)[4],
                                            float qsl, int lane) {
@@ -1030,7 +1128,12 @@ __device__ __forceinline__ void block_step(SoftmaxState& st, const f32x16 (&sc)[
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[j][r]);
       bmax = xhalf_max(mx) * qsl;
-      st.m = new_max(st.m, bmax, alpha);
+      if constexpr (RUN) {
+        run_max(st, bmax);
+        bmax = st.m;  // the codes' reference
+      } else {
+        st.m = new_max(st.m, bmax, alpha);
+      }
     } else if (m < 3) {
       // codes of chunks 2(m-1), 2(m-1)+1; the empty asm keeps them in this
       // slot, so S(b) dies while S(b+1) accumulates
@@ -1040,11 +1143,16 @@ __device__ __forceinline__ void block_step(SoftmaxState& st, const f32x16 (&sc)[
       asm volatile("" : "+v"(pi[j0]), "+v"(pi[j0 + 1]), "+v"(csum));
     }
   }
-  const float beta = __builtin_amdgcn_exp2f(bmax - st.m);
-  st.l = fmaf(st.l, alpha, beta * (1.f / 127.f) * static_cast<float>(csum));
-  rescale(st, alpha);
+  float beta = 1.f;
+  if constexpr (RUN) {
+    st.l += static_cast<float>(csum);
+  } else {
+    beta = __builtin_amdgcn_exp2f(bmax - st.m);
+    st.l = fmaf(st.l, alpha, beta * (1.f / 127.f) * static_cast<float>(csum));
+    rescale(st, alpha);
+  }
   // P(b).V(b); chunk dt of S(b+1) is scaled beside channel tile dt's MFMAs
-  pv_blk(vt, pi, beta * (1.f / 127.f), lane, st.acc, [&](int dt) {
+  pv_blk<RUN>(vt, pi, beta * (1.f / 127.f), lane, st.acc, [&](int dt) {
     if constexpr (QK) {
       scale_chunk<UKS>(kn, si[dt], dt, half, sn[dt]);
       asm volatile("" : "+v"(sn[dt]));
@@ -1057,7 +1165,7 @@ __device__ __forceinline__ void block_step(SoftmaxState& st, const f32x16 (&sc)[
 // tiles of a ragged last block (plain, per 64-key tile), the V channel scale,
 // then the pooled tiles in bf16. K and V blocks double buffered: 65 KB of
 // LDS, two workgroups per CU, two waves per SIMD.
-template <bool UKS>
+template <bool UKS, bool RUN>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 fwd_int8_b128_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
                      const int8_t* __restrict__ qi, const float* __restrict__ qs,
@@ -1148,7 +1256,7 @@ fwd_int8_b128_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t,
       const auto step = [&](const f32x16 (&sc)[4], float fc, f32x16 (&sn)[4], float& fn) {
         issue_k(min(e + 2, nfb - 1), e & 1);
         issue_v(e + 1, (e + 1) & 1);
-        block_step<true, UKS>(st, sc, sn, Kp((e + 1) & 1), Vp(e & 1), qireg, fc, lane);
+        block_step<true, UKS, RUN>(st, sc, sn, Kp((e + 1) & 1), Vp(e & 1), qireg, fc, lane);
         fn = tile_qsl<UKS>(Kp((e + 1) & 1), kBlkKsOffset, qsl);
         wait_tile_copies();
         __syncthreads();
@@ -1161,9 +1269,9 @@ fwd_int8_b128_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t,
       f32x16 dummy[4];
       if (e + 1 < nfb) {
         step(sa, fa, sb, fb);
-        block_step<false, UKS>(st, sb, dummy, nullptr, Vp(e & 1), qireg, fb, lane);
+        block_step<false, UKS, RUN>(st, sb, dummy, nullptr, Vp(e & 1), qireg, fb, lane);
       } else {
-        block_step<false, UKS>(st, sa, dummy, nullptr, Vp(e & 1), qireg, fa, lane);
+        block_step<false, UKS, RUN>(st, sa, dummy, nullptr, Vp(e & 1), qireg, fa, lane);
       }
       __syncthreads();
     }
@@ -1186,17 +1294,21 @@ fwd_int8_b128_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t,
         for (int r = 0; r < 16; ++r)
           s[m][r] = ((bits >> (8 * (r >> 2) + (r & 3))) & 1u) ? s[m][r] : -INFINITY;
       }
-      exact_softmax_pv<true>(st, s, Vp(0), tile_qsl<UKS>(kt, kKsOffset, qsl), lane);
+      exact_softmax_pv<true, RUN>(st, s, Vp(0), tile_qsl<UKS>(kt, kKsOffset, qsl), lane);
       __syncthreads();
     }
     // The per-channel V scale, common to every exact block; the empty asm
     // keeps its 64 loads here.
     const float* vsc = vscale + static_cast<int64_t>(bh) * kD;
     asm volatile("" : "+s"(vsc));
+    if constexpr (RUN) {
+      run_finish(st, vsc, half);
+    } else {
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+      for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) st.acc[dt][r] *= vsc[32 * dt + 8 * (r >> 2) + 4 * half + (r & 3)];
+        for (int r = 0; r < 16; ++r) st.acc[dt][r] *= vsc[32 * dt + 8 * (r >> 2) + 4 * half + (r & 3)];
+    }
   }
 
   // ---- pooled tiles (bf16 Q: 32 VGPRs), double buffered
@@ -1231,7 +1343,7 @@ fwd_int8_b128_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t,
   store_rows(st, o + b * so_b + h * so_h, so_t, qrow, T, half);
 }
 
-template <int BLK, bool PV, bool UKS>
+template <int BLK, bool PV, bool UKS, bool RUN>
 void launch_i8(uint32_t grid, hipStream_t s, const uint16_t* q, int64_t sq_b, int64_t sq_t,
                int64_t sq_h, const int8_t* qi, const float* qs, const int8_t* ki, const float* ks,
                const int8_t* vi, const float* vscale, const uint16_t* v, int64_t sv_b,
@@ -1239,19 +1351,19 @@ void launch_i8(uint32_t grid, hipStream_t s, const uint16_t* q, int64_t sq_b, in
                int64_t npad, const int32_t* counts, const uint32_t* mask,
                int T, int H, int NT, int W, float c, uint16_t* o, int64_t so_b, int64_t so_t,
                int64_t so_h, int kst, int64_t ksh) {
-  hipLaunchKernelGGL((fwd_int8_kernel<BLK, PV, UKS>), dim3(grid), dim3(BLK * 2), blist_lds_bytes(NT), s, q, sq_b, sq_t,
+  hipLaunchKernelGGL((fwd_int8_kernel<BLK, PV, UKS, RUN>), dim3(grid), dim3(BLK * 2), blist_lds_bytes(NT), s, q, sq_b, sq_t,
                      sq_h, qi, qs, ki, ks, vi, vscale, v, sv_b, sv_t, sv_h, TP, kc, vc, npad,
                      counts, mask, T, H, NT, W, c, o, so_b, so_t, so_h, kst, ksh);
 }
 
-template <int BLK, bool PV>
+template <int BLK, bool PV, bool RUN = false>
 void launch_i8_ks(bool uks, uint32_t grid, hipStream_t s, const uint16_t* q, int64_t sq_b,
                   int64_t sq_t, int64_t sq_h, const int8_t* qi, const float* qs, const int8_t* ki,
                   const float* ks, const int8_t* vi, const float* vscale, const uint16_t* v,
                   int64_t sv_b, int64_t sv_t, int64_t sv_h, int64_t TP, const uint16_t* kc,
                   const uint16_t* vc, int64_t npad, const int32_t* counts, const uint32_t* mask, int T, int H, int NT, int W, float c, uint16_t* o,
                   int64_t so_b, int64_t so_t, int64_t so_h, int kst, int64_t ksh) {
-  (uks ? launch_i8<BLK, PV, true> : launch_i8<BLK, PV, false>)(
+  (uks ? launch_i8<BLK, PV, true, RUN> : launch_i8<BLK, PV, false, RUN>)(
       grid, s, q, sq_b, sq_t, sq_h, qi, qs, ki, ks, vi, vscale, v, sv_b, sv_t, sv_h, TP, kc, vc,
       npad, counts, mask, T, H, NT, W, c, o, so_b, so_t, so_h, kst, ksh);
 }
@@ -1270,6 +1382,8 @@ int fwd_int8(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h, const 
                                 block, o, so_b, so_t, so_h, "fwd_int8"))
     return rc;
   SOLATTN_REQUIRE(TP >= T, SOLATTN_EINVAL, "fwd_int8: TP < T");
+  SOLATTN_REQUIRE(int8_pv >= SOLATTN_PV_BF16 && int8_pv <= SOLATTN_PV_INT8_RUNNING, SOLATTN_EINVAL,
+                  "fwd_int8: int8_pv %d is not a SOLATTN_PV_* mode", int8_pv);
   SOLATTN_REQUIRE(qi && qs && ki && ks, SOLATTN_EINVAL, "fwd_int8: null int8 operand");
   SOLATTN_REQUIRE(reinterpret_cast<uintptr_t>(qi) % 16 == 0 && reinterpret_cast<uintptr_t>(ki) % 16 == 0 &&
                       reinterpret_cast<uintptr_t>(ks) % 4 == 0,
@@ -1296,16 +1410,23 @@ int fwd_int8(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h, const 
   grid, s, q, sq_b, sq_t, sq_h, qi, qs, ki, ks, vi, vscale, v, sv_b, sv_t, sv_h, TP, kc, vc, npad, \
       counts, mask, static_cast<int>(T), static_cast<int>(H), static_cast<int>(NT), W, c, o, \
       so_b, so_t, so_h, kst, ksh
+  const bool run = int8_pv == SOLATTN_PV_INT8_RUNNING;
   if (block == 128) {
-    if (int8_pv)
-      hipLaunchKernelGGL(uniform_ks ? int8fwd::fwd_int8_b128_kernel<true> : int8fwd::fwd_int8_b128_kernel<false>,
-                         dim3(grid), dim3(256), blist_lds_bytes(NT), s, q, sq_b, sq_t, sq_h, qi, qs,
-                         ki, ks, vi, vscale, TP, kc, vc, npad, counts, mask,
+    if (int8_pv) {
+      const auto kern = uniform_ks ? (run ? int8fwd::fwd_int8_b128_kernel<true, true>
+                                          : int8fwd::fwd_int8_b128_kernel<true, false>)
+                                   : (run ? int8fwd::fwd_int8_b128_kernel<false, true>
+                                          : int8fwd::fwd_int8_b128_kernel<false, false>);
+      hipLaunchKernelGGL(kern, dim3(grid), dim3(256), blist_lds_bytes(NT), s, q, sq_b, sq_t, sq_h,
+                         qi, qs, ki, ks, vi, vscale, TP, kc, vc, npad, counts, mask,
                          static_cast<int>(T), static_cast<int>(H), static_cast<int>(NT), W, c, o,
                          so_b, so_t, so_h, kst, ksh);
-    else int8fwd::launch_i8_ks<128, false>(uniform_ks, SOLATTN_I8_ARGS);
+    } else {
+      int8fwd::launch_i8_ks<128, false>(uniform_ks, SOLATTN_I8_ARGS);
+    }
   } else {
-    if (int8_pv) int8fwd::launch_i8_ks<64, true>(uniform_ks, SOLATTN_I8_ARGS);
+    if (run) int8fwd::launch_i8_ks<64, true, true>(uniform_ks, SOLATTN_I8_ARGS);
+    else if (int8_pv) int8fwd::launch_i8_ks<64, true>(uniform_ks, SOLATTN_I8_ARGS);
     else int8fwd::launch_i8_ks<64, false>(uniform_ks, SOLATTN_I8_ARGS);
   }
 #undef SOLATTN_I8_ARGS

@@ -56,6 +56,13 @@ enum {
 
 enum { SOLATTN_CURVE_3D = 0, SOLATTN_CURVE_2D_FRAME = 1 };
 
+/* int8_pv of the INT8 entry points: how P.V runs (solattn_fwd_int8). */
+enum {
+  SOLATTN_PV_BF16 = 0,         /* bf16 P against bf16 v */
+  SOLATTN_PV_INT8 = 1,         /* int8 codes against each routed block's row max */
+  SOLATTN_PV_INT8_RUNNING = 2  /* int8 codes against the row's running max */
+};
+
 /* Message for the last failing call on this thread ("" if none). */
 const char* solattn_last_error(void);
 /* ABI version: (major << 16) | minor. */
@@ -221,9 +228,10 @@ int solattn_fwd_bf16(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h
                      uint16_t* o, int64_t so_b, int64_t so_t, int64_t so_h,
                      solattn_stream_t stream);
 
-/* INT8 exact branch: S = int32(qi . ki) * (qs * c) * ks. int8_pv == 0 runs P.V
- * in bf16 against v, with P rounded to bf16 as in solattn_fwd_bf16.
- * int8_pv != 0 quantises P per row against the row max of each routed block:
+/* INT8 exact branch: S = int32(qi . ki) * (qs * c) * ks. int8_pv ==
+ * SOLATTN_PV_BF16 runs P.V in bf16 against v, with P rounded to bf16 as in
+ * solattn_fwd_bf16.
+ * SOLATTN_PV_INT8 quantises P per row against the row max of each routed block:
  *   code = v_cvt_pk_u8_f32(exp2(s + log2(127) - rowmax_blk))
  * i.e. round to nearest, ties to even, of 127 * exp2(s - rowmax_blk) (at most
  * 127 by construction); the products int32(code . vi) are scaled by
@@ -235,6 +243,19 @@ int solattn_fwd_bf16(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h
  * code-sum denominator (both within the INT8 tolerance, cosine >= 0.999), and,
  * at block 128, a ragged last block whose tiles take the max of each 64-key
  * tile instead of the whole block's.
+ * SOLATTN_PV_INT8_RUNNING quantises P against the row's running max instead,
+ * an integer m_int (log2 domain) at or above every scaled score seen:
+ *   code = v_cvt_pk_u8_f32(exp2(s + log2(127) - m_int))
+ * so the products of all exact blocks accumulate in int32 with no per-block
+ * conversion; a block whose row max exceeds m_int raises it to ceil(max),
+ * shifts the int32 sums right by the difference (floor) and scales the code
+ * sum, kept in fp32, by the same power of two (exact); when a lane's half of
+ * a row's code sum exceeds 2^23, m_int rises by one more, so the sums (at
+ * most 127 times the code sum) stay below 2^31. After the exact blocks O = sums * vscale[d] / 127 and l = code sum /
+ * 127, relative to 2^m_int. Codes of blocks below the
+ * running max are coarser than against their own max: a further departure
+ * from the reference, within the INT8 tolerance (cosine >= 0.999 per query
+ * block against the reference arithmetic).
  * The pooled branch is BF16 as above (q, kc, vc); routing inputs as for
  * solattn_fwd_bf16. qi/ki/vi int8 [B, TP, H, D]; qs/ks fp32 [B, TP, H].
  * Replaces: _forward_int8_ptr + sol_attn_int8, /root/reference/_int8_fwd.py:208-432. */

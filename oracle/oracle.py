@@ -328,8 +328,13 @@ def forward_int8_port(q, v, prep, rows, int8_pv: bool = True, group: int = 64,
                    beta/127 * sum(pi), and at block 128 a ragged last block of
                    more than 64 keys quantised per 64-key tile, each against its
                    own max -- the HIP kernel's documented departure (the softmax
-                   denominator is that of the quantised P the P.V multiplies)."""
-    assert codes in ("reference", "kernel")
+                   denominator is that of the quantised P the P.V multiplies);
+      "running":   the HIP kernel's SOLATTN_PV_INT8_RUNNING arithmetic
+                   (``_forward_int8_running``), int8_pv only."""
+    assert codes in ("reference", "kernel", "running")
+    if codes == "running":
+        assert int8_pv, "running codes are an int8 P.V arithmetic"
+        return _forward_int8_running(q, v, prep, rows)
     block, T, NT = prep["block"], prep["T"], prep["NT"]
     D = q.shape[3]
     c = np.float32(np.float32(prep["scale"]) * np.float32(LOG2E))
@@ -411,6 +416,109 @@ def forward_int8_port(q, v, prep, rows, int8_pv: bool = True, group: int = 64,
                     acc = acc * alpha[:, None] + pv
                     m = new_max
         out[(b, h, i)] = (acc / l[:, None])[:ln].astype(np.float32)
+    return out
+
+
+RUN_LANE_SUM_LIMIT = 2.0 ** 23  # a lane's half of the code sum before the max rises
+
+
+def _forward_int8_running(q, v, prep, rows):
+    """INT8 forward with P codes against the row's running max
+    (SOLATTN_PV_INT8_RUNNING; a departure from /root/reference/_int8_fwd.py:
+    333-353, which quantises against each block's max). In the HIP kernels'
+    unit order -- block 128: the full exact blocks ascending, then the tiles
+    of a ragged last block (64 keys each); block 64: the ragged last tile
+    first, then the full tiles ascending -- each unit u:
+      m' = max(m, ceil(max_row s_u)), +1 when either half of the row's code
+      sum (keys k with k mod 8 < 4, the rest: the two lanes of a row) exceeds
+      2^23 (the int32 sums' headroom),
+      sums >>= (m' - m) (arithmetic shift, floor), code sums *= 2^-(m' - m)
+      (exact: the kernels keep them in fp32),
+      pi = round-half-even(exp2(s_u + log2(127) - m')) (at most 127),
+      sums += pi . vi (int32), code sum += sum(pi);
+    in the kernels' fp32 operation order: s_u = fl(int32 * ks) * qsl with qsl =
+    fl(qs * c), the row max fl(max(fl(int32 * ks)) * qsl), and the exponent
+    one fma(fl(int32 * ks), qsl, fl(log2(127) - m')), so that P codes flip
+    between the two only where exp2's own rounding lands on a half;
+    then O = sums * vscale / 127, l = code sum / 127 relative to 2^m, and the
+    pooled tiles (64-block chunks) in fp32 as the BF16 forward."""
+    block, T, NT = prep["block"], prep["T"], prep["NT"]
+    D = q.shape[3]
+    c = np.float32(np.float32(prep["scale"]) * np.float32(LOG2E))
+    ex = exact_matrix(prep["mask"], NT)
+    tail = np.float32(T - (NT - 1) * block)
+    inv127 = np.float32(1.0 / 127.0)
+    log2_127 = np.float32(np.log2(127.0))
+    ragged = T % block != 0
+    out = {}
+    for (b, h, i) in rows:
+        lo, ln = _rows(T, block, i)
+        qb = np.zeros((block, D), np.float32)
+        qb[:ln] = bf16_to_f32(q[b, lo:lo + ln, h])
+        qi = np.zeros((block, D), np.int64)
+        qi[:ln] = prep["qi"][b, lo:lo + ln, h]
+        qs = np.zeros(block, np.float32)
+        qs[:ln] = prep["qs"][b, lo:lo + ln, h]
+        qsl = (qs * c).astype(np.float32)
+        vsc = prep["vscale"][b, h].astype(np.float32)
+        exact = [int(j) for j in np.nonzero(ex[b, h, i])[0]]
+        units = []  # (first key, keys)
+        full = [j for j in exact if not (ragged and j == NT - 1)]
+        rag = [j for j in exact if ragged and j == NT - 1]
+        if block == 128:
+            units = [(j * block, block) for j in full]
+            for j in rag:
+                kln = T - j * block
+                units += [(j * block + o, min(64, kln - o)) for o in range(0, kln, 64)]
+        else:
+            units = [(j * block, T - j * block) for j in rag] + [(j * block, block) for j in full]
+        m = np.full(block, -np.inf, np.float32)
+        acc = np.zeros((block, D), np.int64)
+        lsum = np.zeros((block, 2), np.float64)  # per lane half
+        for k0, kn in units:
+            ki = np.zeros((kn, D), np.int64)
+            ki[:] = prep["ki"][b, k0:k0 + kn, h]
+            ks = prep["ks"][b, k0:k0 + kn, h].astype(np.float32)
+            sk = ((qi @ ki.T).astype(np.float32) * ks[None, :]).astype(np.float32)
+            bmax = (sk.max(axis=1) * qsl).astype(np.float32)
+            m_new = np.maximum(m, np.ceil(bmax)).astype(np.float32)
+            m_new = m_new + (lsum.max(axis=1) > RUN_LANE_SUM_LIMIT).astype(np.float32)
+            with np.errstate(invalid="ignore"):
+                d = np.where(np.isinf(m), 31, np.minimum(m_new - m, 31)).astype(np.int64)
+            acc >>= d[:, None]
+            lsum = np.ldexp(lsum, -d[:, None])
+            m = m_new
+            arg = (sk.astype(np.float64) * qsl[:, None].astype(np.float64)
+                   + (log2_127 - m).astype(np.float64)[:, None]).astype(np.float32)  # one fma
+            x127 = np.exp2(arg.astype(np.float64)).astype(np.float32)
+            pi = np.rint(x127).astype(np.int64)
+            assert pi.max() <= 127
+            vi = prep["vi"][b, k0:k0 + kn, h].astype(np.int64)
+            acc += pi @ vi
+            upper = (np.arange(kn) % 8) >= 4
+            lsum[:, 0] += pi[:, ~upper].sum(axis=1)
+            lsum[:, 1] += pi[:, upper].sum(axis=1)
+            assert np.abs(acc).max() < 2 ** 31
+        accf = (acc.astype(np.float32) * (vsc * inv127)[None, :]).astype(np.float32)
+        l = (lsum.sum(axis=1).astype(np.float32) * inv127).astype(np.float32)  # fp32 in the kernels
+        for g0 in range(0, NT, 64):
+            idx = np.arange(g0, min(g0 + 64, NT))
+            approx = ~ex[b, h, i, idx]
+            if not approx.any():
+                continue
+            idx = idx[approx]
+            kcg = bf16_to_f32(prep["kc"][b, idx, h])
+            vcg = bf16_to_f32(prep["vc"][b, idx, h])
+            sc = ((qb @ kcg.T).astype(np.float32) * c).astype(np.float32)
+            nm = np.maximum(m, sc.max(axis=1))
+            with np.errstate(invalid="ignore"):
+                alpha = np.exp2(np.where(m == nm, np.float32(0), m - nm)).astype(np.float32)
+            p = np.exp2(sc - nm[:, None]).astype(np.float32)
+            lengths = np.where(idx == NT - 1, tail, np.float32(block)).astype(np.float32)
+            accf = accf * alpha[:, None] + _bf16_round(p) @ vcg
+            l = l * alpha + (p * lengths[None, :]).sum(axis=1, dtype=np.float32)
+            m = nm
+        out[(b, h, i)] = (accf / l[:, None])[:ln].astype(np.float32)
     return out
 
 

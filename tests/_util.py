@@ -65,13 +65,15 @@ def per_block(got: np.ndarray, ref: dict, block: int):
 
 
 def check_int8_blocks(label, got, qb, vb, prep, rows, int8_pv, block,
-                      kernel_maxabs=INT8_KERNEL_MAXABS):
-    """Per-query-block INT8 checks against the oracle's two arithmetics, with
-    the worst block of each printed."""
+                      kernel_maxabs=INT8_KERNEL_MAXABS, pv_codes="block"):
+    """Per-query-block INT8 checks against the oracle's two arithmetics (the
+    reference's, and the kernel's: block-max codes, or running-max codes with
+    pv_codes="running"), with the worst block of each printed."""
     import oracle
 
     ref = oracle.forward_int8_port(qb, vb, prep, rows, int8_pv=int8_pv)
-    ker = oracle.forward_int8_port(qb, vb, prep, rows, int8_pv=int8_pv, codes="kernel") \
+    codes = "running" if pv_codes == "running" else "kernel"
+    ker = oracle.forward_int8_port(qb, vb, prep, rows, int8_pv=int8_pv, codes=codes) \
         if int8_pv else ref
     s_ref, s_ker = per_block(got, ref, block), per_block(got, ker, block)
     w_ref = min(s_ref, key=lambda s: s[2])

@@ -36,6 +36,7 @@ def test_exports_every_declared_symbol(capi):
 
 def test_abi_version(capi):
     assert capi.abi_version() >> 16 == 2  # 2: routing masks only, no int16 block lists
+    assert capi.abi_version() & 0xFFFF >= 1  # 2.1: int8_pv = SOLATTN_PV_INT8_RUNNING
 
 
 def test_errors_are_reported(capi):
@@ -89,6 +90,34 @@ def test_quant_block_variant_rejects_bad_arguments(capi, pkg):
             i8.sol_attn_int8(x, x, x, tau=0.9, quant_block=bad)
         with pytest.raises(ValueError, match="quant_block"):
             fp.fused_preprocess_routing(x, x, x, tau=0.9, scale=0.1, quant_block=bad)
+
+
+def test_int8_pv_modes(capi, pkg):
+    """int8_pv takes the three SOLATTN_PV_* modes (bf16, block-max codes,
+    running-max codes): another value is refused before any launch (stand-in
+    addresses, never dereferenced), and the Python option maps onto them."""
+    import importlib
+    L = capi.LIB
+    hdr = open(HEADER).read()
+    for name, val in (("SOLATTN_PV_BF16", 0), ("SOLATTN_PV_INT8", 1), ("SOLATTN_PV_INT8_RUNNING", 2)):
+        assert f"{name} = {val}" in hdr
+    a = 1 << 20
+    T, H = 1000, 2
+    st, sb = H * 128, 1000 * H * 128
+    for bad in (3, -1):
+        args = [a, sb, st, 128, a, a, a, a, a, a, a, sb, st, 128, T, a, a, 64, a, a, 1, T, H, 128,
+                64, 0.1, bad, a, sb, st, 128, None]
+        rc = L.solattn_fwd_int8(*args)
+        assert rc == -1 and b"SOLATTN_PV" in L.solattn_last_error()
+        ws = L.solattn_sol_attn_workspace_bytes(1, T, H, 128, 64, 1)
+        rc = L.solattn_sol_attn_int8(*([a, sb, st, 128] * 3), 1, T, H, 128, 64, 0.1, 1.0, 0, 0, 0,
+                                     0, bad, a, ws, a, sb, st, 128, None)
+        assert rc == -1 and b"SOLATTN_PV" in L.solattn_last_error()
+    i8 = importlib.import_module(f"{pkg.__name__}._int8_fwd")
+    assert i8._pv_mode(True, "block") == 1 and i8._pv_mode(True, "running") == 2
+    assert i8._pv_mode(False, "running") == 0
+    with pytest.raises(ValueError, match="pv_codes"):
+        i8._pv_mode(True, "tile")
 
 
 def test_noalloc_rejects_oversize_before_device_work(capi):

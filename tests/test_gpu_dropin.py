@@ -31,6 +31,7 @@ BF16_MAXABS, BF16_COS = 2e-2, 0.9995
 MODES = {
     "bf16": dict(int8_qk=False),
     "int8_pv": dict(int8_qk=True, int8_pv=True),
+    "int8_pv_running": dict(int8_qk=True, int8_pv=True, pv_codes="running"),
     "int8_bf16pv": dict(int8_qk=True, int8_pv=False),
 }
 
@@ -54,7 +55,8 @@ def _direct(pkg, q, k, v, mode, **kw):
     _, tri, i8 = _mods(pkg)
     if mode == "bf16":
         return tri.sol_attn(q, k, v, **kw)
-    return i8.sol_attn_int8(q, k, v, int8_pv=MODES[mode]["int8_pv"], **kw)
+    return i8.sol_attn_int8(q, k, v, int8_pv=MODES[mode]["int8_pv"],
+                            pv_codes=MODES[mode].get("pv_codes", "block"), **kw)
 
 
 def _against_oracle(label, got, hq, hk, hv, mode, block, tau, sink_kv=(0, 0), sink_q=(0, 0)):
@@ -68,7 +70,8 @@ def _against_oracle(label, got, hq, hk, hv, mode, block, tau, sink_kv=(0, 0), si
     rows = [(0, h, i) for h in range(H) for i in range(ref["NT"])]
     out = got.float().cpu().numpy()
     if int8:
-        check_int8_blocks(label, out, qb, vb, ref, rows, pv, block)
+        check_int8_blocks(label, out, qb, vb, ref, rows, pv, block,
+                          pv_codes=MODES[mode].get("pv_codes", "block"))
         return
     port = oracle.forward_port(qb, kb, vb, ref, rows)
     err, cos = compare_rows(out, port, block)

@@ -140,6 +140,14 @@ def test_full_size_int8(pkg, dev, video, int8_pv, block, tau):
     rows = sorted(set(_sample_rows(cfg["H"], NT, 32, seed=6)) | {(0, 0, NT - 1), (0, 23, NT - 1)})
     check_int8_blocks(f"full size int8 block {block} tau {tau} pv={int8_pv}",
                       out.float().cpu().numpy(), qb, vb, ref, rows, int8_pv, block)
+    if int8_pv:  # the running-max codes on the same routing and codes
+        run = i8.forward_int8(q, v, r, qi, qs, ki, ks, vi, pv_codes="running")
+        one = i8.sol_attn_int8(q, k, v, tau=tau, block=block, pv_codes="running")
+        torch.cuda.synchronize()
+        assert torch.equal(one.view(torch.int16), run.view(torch.int16))
+        check_int8_blocks(f"full size int8 block {block} tau {tau} running codes",
+                          run.float().cpu().numpy(), qb, vb, ref, rows, True, block,
+                          pv_codes="running")
 
 
 @pytest.mark.parametrize("int8_pv", [True, False])
@@ -227,6 +235,10 @@ def test_cfg1_image_dit_int8(pkg, dev, image, int8_pv):
         rows = rows[::3]  # the bf16-P.V loop is the slower one on the host
     check_int8_blocks(f"cfg1 int8 pv={int8_pv}", out.float().cpu().numpy(), qb, vb, ref, rows,
                       int8_pv, block)
+    if int8_pv:  # the running-max codes on the same routing and codes
+        run = i8.forward_int8(q, v, r, qi, qs, ki, ks, vi, pv_codes="running")
+        check_int8_blocks("cfg1 int8 running codes", run.float().cpu().numpy(), qb, vb, ref, rows,
+                          True, block, pv_codes="running")
 
 
 def cosine_rows(got, port, block):
@@ -278,13 +290,13 @@ def test_full_size_long_video(pkg, dev):
     for name, mine in (("qi", qi), ("ki", ki), ("vi", vi)):
         assert np.array_equal(mine[:, :T].cpu().numpy(), ref8[name][:, :T]), name
     rows8 = rows[::3] + rows[-2:]
-    for pv in (True, False):
-        out8 = i8.forward_int8(q, v, r8, qi, qs, ki, ks, vi, int8_pv=pv)
-        one = i8.sol_attn_int8(q, k, v, tau=tau, block=block, int8_pv=pv)
+    for pv, codes in ((True, "block"), (True, "running"), (False, "block")):
+        out8 = i8.forward_int8(q, v, r8, qi, qs, ki, ks, vi, int8_pv=pv, pv_codes=codes)
+        one = i8.sol_attn_int8(q, k, v, tau=tau, block=block, int8_pv=pv, pv_codes=codes)
         torch.cuda.synchronize()
         assert torch.equal(one.view(torch.int16), out8.view(torch.int16))
-        check_int8_blocks(f"full size cfg4 int8 pv={pv}", out8.float().cpu().numpy(), qb, vb,
-                          ref8, rows8, pv, block)
+        check_int8_blocks(f"full size cfg4 int8 pv={pv} {codes}", out8.float().cpu().numpy(), qb,
+                          vb, ref8, rows8, pv, block, pv_codes=codes)
         del out8, one
     del r8, qi, qs, ki, ks, vi, ref8
     outb = i8.sol_attn_int8(q, k, v, tau=tau, block=block, int8_pv=True, quant_block=128)

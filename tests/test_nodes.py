@@ -24,7 +24,7 @@ def test_node_layer_registered(pkg):
     names = [i.name for i in schema.inputs]
     for name in ("model", "tau", "start_percent", "end_percent", "min_tokens", "int8_qk",
                  "sink_conditioning", "morton", "morton_curve", "int8_pv", "verbose", "use_tma",
-                 "tau_profile", "dense_blocks"):
+                 "tau_profile", "dense_blocks", "block_size", "int8_pv_codes"):
         assert name in names
     assert schema.node_id == "SolAttnPatch"
 
@@ -148,7 +148,13 @@ def test_int8_dispatch(disp, monkeypatch):
                         lambda qs, ks, vs, **kw: seen.update(kw) or qs)
     q, k, v = _qkv()
     disp._run(q, k, v, 2, False, False, 0.1, 1.0, 0, False, int8_qk=True, int8_pv=False)
-    assert seen["int8_pv"] is False and seen["scale"] == 0.1
+    assert seen["int8_pv"] is False and seen["scale"] == 0.1 and seen["pv_codes"] == "block"
+    # the running-max P codes reach the kernel from the override's policy
+    seen.clear()
+    ov = disp.make_override(min_tokens=0, int8_qk=True, pv_codes="running")
+    assert ov.policy.pv_codes == "running"
+    disp._run(q, k, v, 2, False, False, 0.1, 1.0, 0, False, int8_qk=True, pv_codes="running")
+    assert seen["pv_codes"] == "running"
 
 
 def test_kernel_error_falls_back_dense(disp, monkeypatch):

@@ -467,6 +467,91 @@ def test_forward_int8_kernel_codes_track_reference_per_block():
     assert max(np.abs(ker2[r] - ref2[r]).max() for r in rows) < 1e-5
 
 
+def _hand_prep(T, block, qs_val, ki0, ks_val, vi0, vscale0=1.0):
+    """A one-head INT8 prep by hand: every block exact for every query block;
+    query rows carry qi[:, 0] = 1 (scale qs_val), key t carries ki[t, 0] =
+    ki0[t] with scale ks_val and vi[t, 0] = vi0[t]; other channels zero.
+    scale = ln 2, so the log2-domain score of key t is ki0[t] * qs_val * ks_val."""
+    NT = -(-T // block)
+    W = -(-NT // 32)
+    mask = np.zeros((1, 1, NT, W), np.uint32)
+    for j in range(NT):
+        mask[..., j >> 5] |= np.uint32(1) << np.uint32(j & 31)
+    qi = np.zeros((1, T, 1, 128), np.int8)
+    qi[..., 0] = 1
+    ki = np.zeros((1, T, 1, 128), np.int8)
+    ki[0, :, 0, 0] = ki0
+    vi = np.zeros((1, T, 1, 128), np.int8)
+    vi[0, :, 0, 0] = vi0
+    vscale = np.zeros((1, 1, 128), np.float32)
+    vscale[..., 0] = vscale0
+    npad = -(-NT // 64) * 64
+    kc = np.zeros((1, npad, 1, 128), np.uint16)  # pooled keys/values: unused (nothing approximate)
+    return dict(block=block, T=T, NT=NT, scale=float(np.float32(math.log(2.0))), mask=mask, qi=qi,
+                kc=kc, vc=kc,
+                qs=np.full((1, T, 1), qs_val, np.float32), ki=ki,
+                ks=np.full((1, T, 1), ks_val, np.float32), vi=vi, vscale=vscale)
+
+
+def test_forward_int8_running_known_answer():
+    """Running-max codes by hand (block 64, two exact blocks, log2 scores
+    ki/8): block 0 has one key at 2.5 and 63 at 0, so m = ceil(2.5) = 3, codes
+    rint(127 * 2^-0.5) = 90 and rint(127 / 8) = 16; block 1 has one key at 4.25
+    and 63 at 0, so m = 5: the int32 sums shift right by 2 (floor) and the
+    code sum scales by 1/4 (exact) before codes rint(127 * 2^-0.75) = 76 and
+    rint(127 / 32) = 4 add. With v codes 100 / 1 in block 0 and -50 / 2 in
+    block 1: sums 90*100 + 63*16 = 10008, code sum 1098; then 2502 and 274.5;
+    + 76*(-50) + 63*4*2 = -3296 and + 76 + 252: -794 and 602.5; output
+    -794 / 602.5 on channel 0."""
+    T, block = 128, 64
+    ki0 = np.zeros(T, np.int64)
+    ki0[0], ki0[64] = 20, 34
+    vi0 = np.array([100] + [1] * 63 + [-50] + [2] * 63)
+    prep = _hand_prep(T, block, 1.0, ki0, 0.125, vi0)
+    q = np.zeros((1, T, 1, 128), np.uint16)  # the pooled branch is empty: every block exact
+    out = oracle.forward_int8_port(q, q, prep, [(0, 0, 0)], codes="running")[(0, 0, 0)]
+    assert np.allclose(out[:, 0], -794.0 / 602.5, rtol=1e-6, atol=0)
+    assert np.all(out[:, 1:] == 0)
+    # the block-max arithmetics give other values (codes 127 at each block's max)
+    ker = oracle.forward_int8_port(q, q, prep, [(0, 0, 0)], codes="kernel")[(0, 0, 0)]
+    assert abs(float(ker[0, 0]) - (-794.0 / 602.5)) > 1e-2
+
+
+def test_forward_int8_running_headroom_rise():
+    """The running max rises by one more when a lane's half of a row's code
+    sum passes 2^23 (the int32 sums' headroom): 2070 blocks of 64 keys, every
+    score 0, so m = 0 and every code is 127; each block adds 32 * 127 = 4064
+    to each half (keys k mod 8 < 4 and the rest), which passes 2^23 after 2065
+    blocks (8392160), so block 2066 raises m to 1: sums >> 1, code sum halved,
+    codes rint(63.5) = 64 (half to even). v codes 1 in the first 2065 blocks,
+    3 in the last five: sums 2065*64*127 = 16784320 -> 8392160 + 5*64*64*3 =
+    8453600, code sum 8392160 + 5*64*64 = 8412640."""
+    T, block = 2070 * 64, 64
+    vi0 = np.where(np.arange(T) < 2065 * 64, 1, 3)
+    prep = _hand_prep(T, block, 1.0, np.zeros(T, np.int64), 1.0, vi0)
+    q = np.zeros((1, T, 1, 128), np.uint16)
+    out = oracle.forward_int8_port(q, q, prep, [(0, 0, 0)], codes="running")[(0, 0, 0)]
+    assert np.allclose(out[:, 0], 8453600.0 / 8412640.0, rtol=1e-7, atol=0)
+    no_rise = (16784320 + 5 * 64 * 127 * 3) / (16784320 + 5 * 64 * 127)
+    assert abs(float(out[0, 0]) - no_rise) > 1e-5
+
+
+@pytest.mark.parametrize("block", [64, 128])
+def test_forward_int8_running_tracks_reference_per_block(block):
+    """The running-max arithmetic against the reference's per query block
+    (north_star's INT8 tolerance), on Gaussian inputs -- the hard case for
+    codes against the running max: the blocks' maxima spread, so blocks below
+    the running max get coarse codes (measured worst 0.9992-0.9993) -- with a
+    ragged last block (T % block != 0)."""
+    B, T, H = 1, 3000, 2
+    q, k, v = (randn_bf16((B, T, H, 128), s) for s in (55, 56, 57))
+    p = oracle.prepare(bits(q), bits(k), bits(v), block=block, tau=0.9, int8=True, int8_pv=True)
+    rows = _rows(p, B, H)
+    run = oracle.forward_int8_port(bits(q), bits(v), p, rows, codes="running")
+    ref = oracle.forward_int8_port(bits(q), bits(v), p, rows, codes="reference")
+    assert min(cosine(run[r], ref[r]) for r in rows) >= 0.999
+
+
 def test_cfg0_plumbing_d64():
     """BASELINE config 0 (B1 H4 D64, 4x32x32 grid -> N 4096, block 64, tau 0.9,
     smooth field + 0.3 noise, Morton 3d) through the CPU path: the Morton
