@@ -306,12 +306,14 @@ def run_sweep(args, mods, dev):
         for block in (64, 128):
             line = {"N": T, "H": H, "block": block, "sdpa_ms": sdpa.get("ms"),
                     "sdpa_backend": sdpa.get("backend"), "bf16_ms": {}, "int8_pv_ms": {},
-                    "int8_bf16pv_ms": {}, "density": {}}
+                    "int8_pv_run_ms": {}, "int8_bf16pv_ms": {}, "density": {}}
             for tau in SWEEP_TAUS:
                 line["bf16_ms"][str(tau)] = round(time_cuda(
                     lambda: sol_attn(q, k, v, tau=tau, block=block), steps, 2), 4)
                 line["int8_pv_ms"][str(tau)] = round(time_cuda(
                     lambda: i8(q, k, v, tau=tau, block=block, int8_pv=True), steps, 2), 4)
+                line["int8_pv_run_ms"][str(tau)] = round(time_cuda(
+                    lambda: i8(q, k, v, tau=tau, block=block, pv_codes="running"), steps, 2), 4)
                 line["int8_bf16pv_ms"][str(tau)] = round(time_cuda(
                     lambda: i8(q, k, v, tau=tau, block=block, int8_pv=False), steps, 2), 4)
                 r = mods["_preprocess"].route(q, k, v, scale=D ** -0.5, tau=tau, block=block)
