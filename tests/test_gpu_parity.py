@@ -435,7 +435,7 @@ def test_wan_hooks_neutral_through_gather_kernel(pkg, dev, curve):
     assert cosine(hooked.float().cpu().numpy(), plain.float().cpu().numpy()) >= BF16_COS
 
 
-@pytest.mark.parametrize("mode", ["bf16", "int8_pv", "int8_bf16pv"])
+@pytest.mark.parametrize("mode", ["bf16", "int8_pv", "int8_pv_running", "int8_bf16pv"])
 @pytest.mark.parametrize("case", ["cfg0", "random"])
 def test_head_dim_64(pkg, dev, mode, case):
     """Head dim 64 (BASELINE config 0's shape, and a ragged random case): the
@@ -459,7 +459,8 @@ def test_head_dim_64(pkg, dev, mode, case):
     print(f"[d64] case={case} mode={mode} shape={tuple(q.shape)} block={block}", flush=True)
     qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
     int8 = mode != "bf16"
-    pv = mode == "int8_pv"
+    pv = mode in ("int8_pv", "int8_pv_running")
+    codes = "running" if mode == "int8_pv_running" else "block"
     ref = oracle.prepare(bits(q), bits(k), bits(v), block=block, tau=tau, int8=int8, int8_pv=pv)
     if int8:
         r, qi, qs, ki, ks, vi = fp.fused_preprocess_routing(qd, kd, vd, tau=tau, scale=D ** -0.5,
@@ -468,7 +469,7 @@ def test_head_dim_64(pkg, dev, mode, case):
         assert np.array_equal(ks.cpu().numpy().view(np.uint32), ref["ks"].view(np.uint32))
         if pv:
             assert np.array_equal(vi.cpu().numpy(), ref["vi"])
-        out = i8.sol_attn_int8(qd, kd, vd, tau=tau, block=block, int8_pv=pv)
+        out = i8.sol_attn_int8(qd, kd, vd, tau=tau, block=block, int8_pv=pv, pv_codes=codes)
     else:
         r = prep.route(qd, kd, vd, scale=D ** -0.5, tau=tau, block=block)
         out = tri.sol_attn(qd, kd, vd, tau=tau, block=block)
@@ -481,7 +482,7 @@ def test_head_dim_64(pkg, dev, mode, case):
     rows = _rows(B, H, NT, limit=48, seed=3)
     if int8:
         check_int8_blocks(f"d64 {case} {mode}", out.float().cpu().numpy(), bits(q), bits(v), ref,
-                          rows, pv, block)
+                          rows, pv, block, pv_codes=codes)
     else:
         port = oracle.forward_port(bits(q), bits(k), bits(v), ref, rows)
         err, cos = compare_rows(out.float().cpu().numpy(), port, block)
