@@ -46,8 +46,57 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return static_cast<uint32_t>(f2bf(lo)) | (static_cast<uint32_t>(f2bf(hi)) << 16);
 }
 
+// Two fp32 -> a packed bf16 pair (lo, hi) in one v_cvt_pk_bf16_f32: round to
+// nearest even, the bits of f2bf for every non-NaN input (denormals included:
+// f32 denormals are not flushed in this build).
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
+  typedef __attribute__((ext_vector_type(2))) float f2;
+  typedef __attribute__((ext_vector_type(2))) __bf16 h2;
+  const f2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, h2));
+}
+
 __device__ __forceinline__ float lo_bf16(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float hi_bf16(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// Raw buffer access: base is wave-uniform (a scalar resource), off a per-lane
+// byte offset (one VGPR instead of a 64-bit address per load). The hardware
+// range check returns zeros for a 16-byte load whose end passes nbytes (and
+// drops such a store); callers keep each 16-byte access wholly inside or
+// wholly past nbytes. Word 3 0x00020000: 32-bit data format, no swizzle.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t nbytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(nbytes),
+                                           0x00020000);
+}
+__device__ __forceinline__ uint4 buffer_load16(const void* base, uint32_t nbytes, uint32_t off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(buffer_rsrc(base, nbytes), off, 0, 0);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ uint32_t buffer_load4(const void* base, uint32_t nbytes, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(buffer_rsrc(base, nbytes), off, 0, 0);
+}
+__device__ __forceinline__ uint16_t buffer_load2(const void* base, uint32_t nbytes, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(base, nbytes), off, 0, 0);
+}
+__device__ __forceinline__ void buffer_store2(void* base, uint32_t nbytes, uint32_t off, uint16_t x) {
+  __builtin_amdgcn_raw_buffer_store_b16(x, buffer_rsrc(base, nbytes), off, 0, 0);
+}
+__device__ __forceinline__ void buffer_store16(void* base, uint32_t nbytes, uint32_t off,
+                                               const uint4& x) {
+  typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
+  const u32x4 v = {x.x, x.y, x.z, x.w};
+  __builtin_amdgcn_raw_buffer_store_b128(v, buffer_rsrc(base, nbytes), off, 0, 0);
+}
+
+// Bytes of a row-strided buffer that rows [r, n) span when the last row ends
+// `tail` bytes after its start (row pitch `pitch` bytes), capped at `cap`: the
+// nbytes of buffer_load16 for a base at row r; 0 when r >= n.
+__device__ __forceinline__ uint32_t rows_nbytes(int64_t r, int64_t n, int64_t pitch, int64_t tail,
+                                                int64_t cap) {
+  if (r >= n) return 0u;
+  const int64_t bytes = (n - 1 - r) * pitch + tail;
+  return static_cast<uint32_t>(bytes < cap ? bytes : cap);
+}
 
 constexpr float kLog2e = 1.4426950408889634f;
 

@@ -123,7 +123,50 @@ __device__ __forceinline__ void quant_span_rows(const uint4 (&raw)[kSlotRows], i
   }
 }
 
-template <int BLK, bool QUANT>
+// pool_kernel's row access: raw buffer loads with a wave-uniform base per
+// 16-row step and one offset VGPR for all of the lane's rows (in place of a
+// 64-bit address each). Rows past T read zeros (or, for a row stride below
+// 128 elements, rows the pooling masks out). Row strides are 0 <= st < 2^26.
+__device__ __forceinline__ void load_span_buf(const uint16_t* xh, int64_t st, int64_t r0, int64_t T,
+                                              const PoolLane& pl, uint4 (&raw)[kSlotRows]) {
+  const uint32_t off = static_cast<uint32_t>((pl.g * st + pl.c8) * 2);
+  const int64_t cap = max<int64_t>(32 * st, 2 * kHeadDim);
+#pragma unroll
+  for (int m = 0; m < kSlotRows; ++m) {
+    const int64_t rb = r0 + 16 * m;
+    raw[m] = buffer_load16(xh + rb * st, rows_nbytes(rb, T, 2 * st, 2 * kHeadDim, cap), off);
+  }
+}
+
+// Per-token codes of the lane's Q rows; stores of rows past T fall outside the
+// range of their buffer store and are dropped.
+__device__ __forceinline__ void quant_span_rows_buf(const uint4 (&raw)[kSlotRows], int64_t r0,
+                                                    int64_t T, const PoolLane& pl, int64_t b, int h,
+                                                    int H, int64_t TP, int8_t* __restrict__ qi,
+                                                    float* __restrict__ qs) {
+  typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u32x2;
+  const int64_t pitch = static_cast<int64_t>(H) * kHeadDim;  // bytes per token of qi
+  const uint32_t off = static_cast<uint32_t>(pl.g * pitch + pl.c8);
+#pragma unroll
+  for (int m = 0; m < kSlotRows; ++m) {
+    float x[8];
+    unpack8(raw[m], x);
+    uint2 codes;
+    const float ss = quant_token_row(x, codes);
+    const int64_t rb = r0 + 16 * m;
+    const u32x2 cv = {codes.x, codes.y};
+    __builtin_amdgcn_raw_buffer_store_b64(
+        cv, buffer_rsrc(qi + ((b * TP + rb) * H + h) * kHeadDim, rows_nbytes(rb, T, pitch, kHeadDim, 16 * pitch)),
+        off, 0, 0);
+    if (pl.c8 == 0 && rb + pl.g < T) qs[(b * TP + rb + pl.g) * H + h] = ss;
+    __builtin_amdgcn_sched_barrier(0);  // one row at a time
+  }
+}
+
+// QUANT: Q's rows come first and are quantised while K's and V's land, then
+// Q, K and V are pooled in that order; otherwise K, V, Q. AMAX: the per-block
+// |v| max (vamax_part).
+template <int BLK, bool QUANT, bool AMAX>
 __global__ void __launch_bounds__(kPoolThreads)
 pool_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
             const uint16_t* __restrict__ k, int64_t sk_b, int64_t sk_t, int64_t sk_h,
@@ -133,30 +176,41 @@ pool_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int64_t 
             float* __restrict__ qs, int64_t TP) {
   constexpr int NB = kSpan / BLK;
   __shared__ __align__(16) float part[NB * kSlots * kHeadDim];
-  __shared__ __align__(16) float amx[NB * kSlots * kHeadDim];
-  const int h = blockIdx.y;
-  const int64_t b = blockIdx.z, r0 = static_cast<int64_t>(blockIdx.x) * kSpan;
+  __shared__ __align__(16) float amx[AMAX ? NB * kSlots * kHeadDim : 4];
+  const int h = blockIdx.x;
+  const int64_t b = blockIdx.z, r0 = static_cast<int64_t>(blockIdx.y) * kSpan;
   const PoolLane pl;
   uint4 rk[kSlotRows], rv[kSlotRows], rq[kSlotRows];
-  load_span(k + b * sk_b + h * sk_h + pl.c8, sk_t, r0, T, pl.g, rk);
-  load_span(v + b * sv_b + h * sv_h + pl.c8, sv_t, r0, T, pl.g, rv);
-  load_span(q + b * sq_b + h * sq_h + pl.c8, sq_t, r0, T, pl.g, rq);
+  if (QUANT) load_span_buf(q + b * sq_b + h * sq_h, sq_t, r0, T, pl, rq);
+  load_span_buf(k + b * sk_b + h * sk_h, sk_t, r0, T, pl, rk);
+  load_span_buf(v + b * sv_b + h * sv_h, sv_t, r0, T, pl, rv);
+  if (!QUANT) load_span_buf(q + b * sq_b + h * sq_h, sq_t, r0, T, pl, rq);
   // this thread's output: block s*NB + blk (if it exists), channel c
   const int blk = static_cast<int>(threadIdx.x) >> 7, c = static_cast<int>(threadIdx.x) & 127;
-  const int j = static_cast<int>(blockIdx.x) * NB + blk;
+  const int j = static_cast<int>(blockIdx.y) * NB + blk;
   const bool out = blk < NB && j < NT;
   const float flen = static_cast<float>(min<int64_t>(BLK, T - static_cast<int64_t>(j) * BLK));
   const float* pc = part + blk * kSlots * kHeadDim + c;
+  const auto pool_q = [&]() {
+    pool_span<BLK, false>(rq, r0, T, pl, part, nullptr);
+    __syncthreads();
+    if (out) qbar[((b * H + h) * NT + j) * kHeadDim + c] = tree16(pc, kHeadDim) / flen;
+    __syncthreads();
+  };
 
+  if (QUANT) {
+    quant_span_rows_buf(rq, r0, T, pl, b, h, H, TP, qi, qs);
+    pool_q();
+  }
   pool_span<BLK, false>(rk, r0, T, pl, part, nullptr);
   __syncthreads();
   if (out) kc[((b * npad + j) * H + h) * kHeadDim + c] = f2bf(tree16(pc, kHeadDim) / flen);
   __syncthreads();
-  pool_span<BLK, true>(rv, r0, T, pl, part, amx);
+  pool_span<BLK, AMAX>(rv, r0, T, pl, part, amx);
   __syncthreads();
   if (out) {
     vc[((b * npad + j) * H + h) * kHeadDim + c] = f2bf(tree16(pc, kHeadDim));
-    if (vamax_part) {
+    if (AMAX) {
       const float* ac = amx + blk * kSlots * kHeadDim + c;
       float m = ac[0];
 #pragma unroll
@@ -164,141 +218,119 @@ pool_kernel(const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, int64_t 
       vamax_part[((b * NT + j) * H + h) * kHeadDim + c] = m;
     }
   }
-  __syncthreads();
-  if (QUANT) quant_span_rows(rq, r0, T, pl, b, h, H, TP, qi, qs);
-  pool_span<BLK, false>(rq, r0, T, pl, part, nullptr);
-  __syncthreads();
-  if (out) qbar[((b * H + h) * NT + j) * kHeadDim + c] = tree16(pc, kHeadDim) / flen;
+  if (!QUANT) {
+    __syncthreads();
+    pool_q();
+  }
 }
 
 // --------------------------------------------------------------- moments --
 // /root/reference/_preprocess.py:241-243 and /root/reference/_fused_prep.py:77-81.
 // 8 partial groups sum blocks j = g (mod 8) in ascending order; the partials
 // are combined ((p0+p1)+(p2+p3)) + ((p4+p5)+(p6+p7)).
-__device__ __forceinline__ float tree8(const float (*part)[kHeadDim], int d) {
+template <int N>
+__device__ __forceinline__ float tree8(const float (*part)[N], int d) {
   return ((part[0][d] + part[1][d]) + (part[2][d] + part[3][d])) +
          ((part[4][d] + part[5][d]) + (part[6][d] + part[7][d]));
 }
 
-// One workgroup of 128 threads per (head, batch): thread t owns partial group
-// g = t / 16 and channels c8 .. c8+7 (16-byte loads of 8 bf16). Loads are
-// issued in chunks of kMomU before they are summed, in the same ascending
-// order as a plain loop.
-constexpr int kMomThreads = 128;
-constexpr int kMomU = 16;
+// One workgroup of 8 x kMomCh threads per (channel slice, head, batch), kMomCh
+// channels a slice: thread t owns partial group g = t / kMomCh (blocks j = g
+// mod 8, summed in ascending order) and channel c = slice * kMomCh + t %
+// kMomCh. A thread's serial work is one channel and each SIMD holds at most one
+// of the launch's waves, so the chains run side by side on 8 CUs per head. A
+// thread loads kMomR of its blocks at once (2-byte buffer loads); up to NT = 8
+// * kMomR (every block of the head) they stay in registers for the centring
+// pass, so the kernel reads kc from HBM once. With vamax_part the same thread
+// takes the |v| max of its channel over the same blocks, loaded beside them.
+constexpr int kMomCh = 16;
+constexpr int kMomThreads = 8 * kMomCh;
+constexpr int kMomR = 32;
+template <bool CENTRE>
 __global__ void __launch_bounds__(kMomThreads)
-moments_kernel(uint16_t* __restrict__ kc, int64_t npad, int NT, int H, int centre,
+moments_kernel(uint16_t* __restrict__ kc, int64_t npad, int NT, int H,
                float* __restrict__ kc_mean, float* __restrict__ kc_var,
                const float* __restrict__ vamax_part, float* __restrict__ vscale) {
-  const int h = blockIdx.x, b = blockIdx.y;
-  const int g = threadIdx.x >> 4, c8 = (threadIdx.x & 15) * 8;
-  __shared__ float part[8][kHeadDim];
-  __shared__ float amx[8][kHeadDim];
-  __shared__ float smean[kHeadDim];
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int t = threadIdx.x, g = t / kMomCh, cl = t % kMomCh;
+  const int c = static_cast<int>(blockIdx.x) * kMomCh + cl;
+  __shared__ float part[8][kMomCh];
+  __shared__ float amx[8][kMomCh];
+  __shared__ float smean[kMomCh];
   const float fnt = static_cast<float>(NT);
-  uint16_t* col = kc + (static_cast<int64_t>(b) * npad * H + h) * kHeadDim + c8;
+  // Rows through raw buffer loads: per chunk of 8 * kMomR rows from row r, a
+  // wave-uniform base at row r and the lane's row g + 8u, channel c at a
+  // 32-bit offset (below 2^32 for H < 65536); rows past NT read 0.
+  constexpr int kChunk = 8 * kMomR;
+  uint16_t* kch = kc + (static_cast<int64_t>(b) * npad * H + h) * kHeadDim;
+  const float* ah = vamax_part + (static_cast<int64_t>(b) * NT * H + h) * kHeadDim;
   const int64_t sj = static_cast<int64_t>(H) * kHeadDim;
-  float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  float am[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int j0 = g; j0 < NT; j0 += 8 * kMomU) {
-    uint4 w[kMomU];
+  const auto koff = [&](int u) { return static_cast<uint32_t>(((g + 8 * u) * sj + c) * 2); };
+  const auto kbytes = [&](int64_t r) { return rows_nbytes(r, NT, 2 * sj, 2 * kHeadDim, kChunk * 2 * sj); };
+  const auto abytes = [&](int64_t r) { return rows_nbytes(r, NT, 4 * sj, 4 * kHeadDim, kChunk * 4 * sj); };
+  const bool resident = NT <= kChunk;
+  uint16_t w[kMomR];
+  float s = 0.f, am = 0.f;
+  for (int r = 0; r < NT; r += kChunk) {  // this thread's rows r + g + 8u
+    const uint32_t kb = kbytes(r);
 #pragma unroll
-    for (int u = 0; u < kMomU; ++u)  // clamped row: no branch around the load
-      w[u] = *reinterpret_cast<const uint4*>(col + min(j0 + 8 * u, NT - 1) * sj);
-#pragma unroll
-    for (int u = 0; u < kMomU; ++u) {
-      if (j0 + 8 * u < NT) {
-        float x[8];
-        unpack8(w[u], x);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) s[e] = s[e] + x[e];
-      }
-    }
-  }
-  if (vamax_part) {
-    const float* a = vamax_part + (static_cast<int64_t>(b) * NT * H + h) * kHeadDim + c8;
-    for (int j0 = g; j0 < NT; j0 += 8 * kMomU) {
-      float4 w[kMomU][2];
-#pragma unroll
-      for (int u = 0; u < kMomU; ++u) {
-        const float4* p = reinterpret_cast<const float4*>(a + min(j0 + 8 * u, NT - 1) * sj);
-        w[u][0] = p[0];
-        w[u][1] = p[1];
-      }
-#pragma unroll
-      for (int u = 0; u < kMomU; ++u) {  // duplicated rows leave the max unchanged
-        am[0] = fmaxf(am[0], w[u][0].x); am[1] = fmaxf(am[1], w[u][0].y);
-        am[2] = fmaxf(am[2], w[u][0].z); am[3] = fmaxf(am[3], w[u][0].w);
-        am[4] = fmaxf(am[4], w[u][1].x); am[5] = fmaxf(am[5], w[u][1].y);
-        am[6] = fmaxf(am[6], w[u][1].z); am[7] = fmaxf(am[7], w[u][1].w);
-      }
-    }
-  }
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    part[g][c8 + e] = s[e];
-    amx[g][c8 + e] = am[e];
-  }
-  __syncthreads();
-  {
-    const int d = threadIdx.x;  // one channel per thread
-    const float mean = tree8(part, d) / fnt;
-    smean[d] = mean;
-    kc_mean[(static_cast<int64_t>(b) * H + h) * kHeadDim + d] = mean;
+    for (int u = 0; u < kMomR; ++u) w[u] = buffer_load2(kch + r * sj, kb, koff(u));
     if (vamax_part) {
-      float m = amx[0][d];
-      for (int i = 1; i < 8; ++i) m = fmaxf(m, amx[i][d]);
-      // absmax.div(127.0) in torch is a multiply by the fp32 reciprocal
-      // (/root/reference/_fused_quant.py:104).
-      const float sc = m * (1.0f / 127.0f);
-      vscale[(static_cast<int64_t>(b) * H + h) * kHeadDim + d] = sc < 1e-8f ? 1e-8f : sc;
+      const uint32_t ab = abytes(r);
+      float a[kMomR];
+#pragma unroll
+      for (int u = 0; u < kMomR; ++u)
+        a[u] = __uint_as_float(buffer_load4(ah + r * sj, ab, 2 * koff(u)));
+#pragma unroll
+      for (int u = 0; u < kMomR; ++u) am = fmaxf(am, a[u]);  // rows past NT read 0
     }
+#pragma unroll
+    for (int u = 0; u < kMomR; ++u)
+      if (r + g + 8 * u < NT) s = s + bf2f(w[u]);
+  }
+  part[g][cl] = s;
+  amx[g][cl] = am;
+  __syncthreads();
+  const int64_t mo = (static_cast<int64_t>(b) * H + h) * kHeadDim + c;
+  if (t < kMomCh) {
+    const float mean = tree8(part, t) / fnt;
+    smean[t] = mean;
+    kc_mean[mo] = mean;
+  } else if (vamax_part && t < 2 * kMomCh) {
+    const int d = t - kMomCh;
+    float m = amx[0][d];
+    for (int i = 1; i < 8; ++i) m = fmaxf(m, amx[i][d]);
+    // absmax.div(127.0) in torch is a multiply by the fp32 reciprocal
+    // (/root/reference/_fused_quant.py:104).
+    const float sc = m * (1.0f / 127.0f);
+    vscale[mo] = sc < 1e-8f ? 1e-8f : sc;  // c = slice * kMomCh + d
   }
   __syncthreads();
-  float mean[8];
+  const float mean = smean[cl];
+  float acc = 0.f;
+  for (int r = 0; r < NT; r += kChunk) {
+    const uint32_t kb = kbytes(r);
+    if (!resident) {
 #pragma unroll
-  for (int e = 0; e < 8; ++e) mean[e] = smean[c8 + e];
-  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int j0 = g; j0 < NT; j0 += 8 * kMomU) {
-    uint4 w[kMomU];
+      for (int u = 0; u < kMomR; ++u) w[u] = buffer_load2(kch + r * sj, kb, koff(u));
+    }
 #pragma unroll
-    for (int u = 0; u < kMomU; ++u)
-      w[u] = *reinterpret_cast<const uint4*>(col + min(j0 + 8 * u, NT - 1) * sj);
-#pragma unroll
-    for (int u = 0; u < kMomU; ++u) {
-      const int j = j0 + 8 * u;
-      if (j < NT) {
-        float x[8];
-        unpack8(w[u], x);
-        uint16_t nb[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          float y = x[e] - mean[e];
-          if (centre) {
-            nb[e] = f2bf(y);
-            y = bf2f(nb[e]);
-          }
-          acc[e] = acc[e] + y * y;
+    for (int u = 0; u < kMomR; ++u) {
+      if (r + g + 8 * u < NT) {
+        float y = bf2f(w[u]) - mean;
+        if (CENTRE) {  // bf16 of the centred value (round to nearest even, as f2bf)
+          const uint16_t nb = static_cast<uint16_t>(cvt_pk_bf16(y, 0.f));
+          y = bf2f(nb);
+          buffer_store2(kch + r * sj, kb, koff(u), nb);
         }
-        if (centre) {
-          uint4 o;
-          o.x = nb[0] | (static_cast<uint32_t>(nb[1]) << 16);
-          o.y = nb[2] | (static_cast<uint32_t>(nb[3]) << 16);
-          o.z = nb[4] | (static_cast<uint32_t>(nb[5]) << 16);
-          o.w = nb[6] | (static_cast<uint32_t>(nb[7]) << 16);
-          *reinterpret_cast<uint4*>(col + j * sj) = o;
-        }
+        acc = acc + y * y;
       }
     }
   }
   __syncthreads();  // every thread has read part[] above
-#pragma unroll
-  for (int e = 0; e < 8; ++e) part[g][c8 + e] = acc[e];
+  part[g][cl] = acc;
   __syncthreads();
-  {
-    const int d = threadIdx.x;
-    kc_var[(static_cast<int64_t>(b) * H + h) * kHeadDim + d] = tree8(part, d) / fnt;
-  }
+  if (t < kMomCh) kc_var[mo] = tree8(part, t) / fnt;
 }
 
 // ------------------------------------------------------ single-read INT8 --
@@ -605,64 +637,32 @@ route_kernel(const float* __restrict__ qbar, const uint16_t* __restrict__ kc, in
   static_assert(kRouteRows % 64 == 0 && kQB % TPR == 0, "route tiling");
   const int i0 = blockIdx.x * kQB, h = blockIdx.y, b = blockIdx.z;
   const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
-  __shared__ float sthr[kQB];
   // exact bits of the kQB query blocks, W words each, in dynamic LDS
   extern __shared__ __align__(16) uint32_t smask_lds[];
   const auto smask = [&](int i, int w) -> uint32_t& { return smask_lds[i * W + w]; };
   __shared__ __align__(16) uint16_t skc[kRouteRows * kKcStride];
+  __shared__ __align__(16) float sq[kQB][kHeadDim];  // the kQB query centroids
+  __shared__ __align__(16) float smk[kHeadDim];      // kc mean (mode 0)
+  __shared__ __align__(16) float svk[kHeadDim];      // kc variance
+  static_assert(kQB * kHeadDim / 4 == kRouteThreads && 2 * kHeadDim == kRouteThreads,
+                "one float4 of the centroids and one moment per thread");
   const int64_t bh = static_cast<int64_t>(b) * H + h;
-  // Query rows past NT (a ragged last workgroup) read row NT-1; nothing of
-  // theirs is stored.
   // Threads t, t + kRouteRows, ... score the same kc row, against query blocks
   // qh*kQH .. +kQH-1 (qh is the same for the whole wave).
   const int qh = __builtin_amdgcn_readfirstlane(t / kRouteRows);
-  const float* qrow[kQH];
-#pragma unroll
-  for (int i = 0; i < kQH; ++i)
-    qrow[i] = qbar + (bh * NT + min(i0 + qh * kQH + i, NT - 1)) * kHeadDim;
-  for (int e = t; e < kQB * W; e += kRouteThreads) smask_lds[e] = 0u;
-  if (wave == 0) {
-    // Lane i < kQB: the threshold of query block i0 + i, one fma chain per
-    // moment in ascending d. Its row comes in 16-float chunks ahead of the
-    // chain; the kc moments are the same for every lane (scalar loads).
-    const int i = min(lane, kQB - 1);
-    const float4* q4 = reinterpret_cast<const float4*>(qbar + (bh * NT + min(i0 + i, NT - 1)) * kHeadDim);
-    const float* mk = kc_mean + bh * kHeadDim;
-    const float* vk = kc_var + bh * kHeadDim;
-    float mu = 0.f, var = 0.f;
-    for (int d0 = 0; d0 < kHeadDim; d0 += 16) {
-      float qv[16];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const float4 x = q4[d0 / 4 + u];
-        qv[4 * u] = x.x, qv[4 * u + 1] = x.y, qv[4 * u + 2] = x.z, qv[4 * u + 3] = x.w;
-      }
-      if (mode == 0) {
-#pragma unroll
-        for (int dd = 0; dd < 16; ++dd) {
-          mu = fmaf(qv[dd], mk[d0 + dd], mu);
-          var = fmaf(qv[dd] * qv[dd], vk[d0 + dd], var);
-        }
-      } else {
-#pragma unroll
-        for (int dd = 0; dd < 16; ++dd) var = fmaf(qv[dd] * qv[dd], vk[d0 + dd], var);
-      }
-    }
-    float th;
-    if (mode == 0) {
-      mu = mu * c;
-      var = var * c2;
-      const float sd = sqrtf(fmaxf(var, 0.f) + 1e-6f);
-      th = mu + tau * sd;
-    } else {
-      var = var * c2;
-      th = tau * sqrtf(var + 1e-6f);
-    }
-    if (lane < kQB) {
-      sthr[lane] = th;
-      if (i0 + lane < NT) thr_out[(static_cast<int64_t>(b) * NT + i0 + lane) * H + h] = th;
-    }
+  {
+    // The centroids and moments, one load per thread, published by the first
+    // chunk's barrier. Query rows past NT (a ragged last workgroup) read row
+    // NT-1; nothing of theirs is stored.
+    const int qb = t >> 5, q4 = t & 31;
+    const float4 x =
+        reinterpret_cast<const float4*>(qbar + (bh * NT + min(i0 + qb, NT - 1)) * kHeadDim)[q4];
+    const float mv = t < kHeadDim ? kc_mean[bh * kHeadDim + t] : kc_var[bh * kHeadDim + t - kHeadDim];
+    reinterpret_cast<float4*>(&sq[qb][0])[q4] = x;
+    (t < kHeadDim ? smk[t] : svk[t - kHeadDim]) = mv;
   }
+  for (int e = t; e < kQB * W; e += kRouteThreads) smask_lds[e] = 0u;
+  float th = 0.f;  // lane i < kQB of every wave: the threshold of query block i0 + i
 
   for (int j0 = 0; j0 < NT; j0 += kRouteRows) {
     // Stage kc rows j0 .. j0+kRouteRows-1 (coalesced 16-byte loads, all issued
@@ -691,7 +691,45 @@ route_kernel(const float* __restrict__ qbar, const uint16_t* __restrict__ kc, in
         dst[1] = make_uint2(v[u].z, v[u].w);
       }
     }
-    __syncthreads();  // (the first one also publishes the thresholds)
+    __syncthreads();  // (the first one also publishes the centroids and moments)
+    if (j0 == 0) {
+      // Every wave computes the kQB thresholds (lane i: query block i0 + i),
+      // one fma chain per moment in ascending d, so no barrier waits on them.
+      const float* qv = sq[min(lane, kQB - 1)];
+      float mu = 0.f, var = 0.f;
+#pragma unroll 4
+      for (int d = 0; d < kHeadDim; d += 4) {
+        const float4 x = *reinterpret_cast<const float4*>(qv + d);
+        const float4 vk = *reinterpret_cast<const float4*>(svk + d);
+        if (mode == 0) {
+          const float4 mk = *reinterpret_cast<const float4*>(smk + d);
+          mu = fmaf(x.x, mk.x, mu);
+          var = fmaf(x.x * x.x, vk.x, var);
+          mu = fmaf(x.y, mk.y, mu);
+          var = fmaf(x.y * x.y, vk.y, var);
+          mu = fmaf(x.z, mk.z, mu);
+          var = fmaf(x.z * x.z, vk.z, var);
+          mu = fmaf(x.w, mk.w, mu);
+          var = fmaf(x.w * x.w, vk.w, var);
+        } else {
+          var = fmaf(x.x * x.x, vk.x, var);
+          var = fmaf(x.y * x.y, vk.y, var);
+          var = fmaf(x.z * x.z, vk.z, var);
+          var = fmaf(x.w * x.w, vk.w, var);
+        }
+      }
+      if (mode == 0) {
+        mu = mu * c;
+        var = var * c2;
+        const float sd = sqrtf(fmaxf(var, 0.f) + 1e-6f);
+        th = mu + tau * sd;
+      } else {
+        var = var * c2;
+        th = tau * sqrtf(var + 1e-6f);
+      }
+      if (wave == 0 && lane < kQB && i0 + lane < NT)
+        thr_out[(static_cast<int64_t>(b) * NT + i0 + lane) * H + h] = th;
+    }
     const int rr = t % kRouteRows;
     const int j = j0 + rr;
     const bool active = j < NT;
@@ -699,8 +737,8 @@ route_kernel(const float* __restrict__ qbar, const uint16_t* __restrict__ kc, in
 #pragma unroll
     for (int i = 0; i < kQH; ++i) acc[i] = 0.f;
     const uint16_t* krow = &skc[rr * kKcStride];
-    // The query centroids are the same for every lane: scalar loads, so each
-    // fma takes its q operand from an SGPR.
+    // The query centroids are the same for every lane of a wave: broadcast
+    // LDS reads.
 #pragma unroll 2
     for (int d4 = 0; d4 < kHeadDim / 4; ++d4) {
       const uint2 kw = *reinterpret_cast<const uint2*>(krow + 4 * d4);
@@ -708,7 +746,7 @@ route_kernel(const float* __restrict__ qbar, const uint16_t* __restrict__ kc, in
       const float k2 = lo_bf16(kw.y), k3 = hi_bf16(kw.y);
 #pragma unroll
       for (int i = 0; i < kQH; ++i) {
-        const float4 qv = *reinterpret_cast<const float4*>(qrow[i] + 4 * d4);
+        const float4 qv = *reinterpret_cast<const float4*>(&sq[qh * kQH + i][4 * d4]);
         acc[i] = fmaf(qv.x, k0, acc[i]);
         acc[i] = fmaf(qv.y, k1, acc[i]);
         acc[i] = fmaf(qv.z, k2, acc[i]);
@@ -724,7 +762,8 @@ route_kernel(const float* __restrict__ qbar, const uint16_t* __restrict__ kc, in
       const float r = acc[i] * c;
       const int dij = qi > j ? qi - j : j - qi;
       const bool q_in_sink = qi >= sq_lo && qi < sq_hi;
-      const bool routed = (r > sthr[il]) || dij <= 1 || in_skv;
+      const float thr = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, th), il));
+      const bool routed = (r > thr) || dij <= 1 || in_skv;
       const bool exact = active && qi < NT && (q_in_sink || routed);
       const uint64_t bal = __ballot(exact);
       if (lane == 0 && w0 < W) {
@@ -780,15 +819,24 @@ int launch_pool(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h, con
                 int8_t* qi, float* qs, int64_t TP, hipStream_t s) {
   const int64_t NT = cdiv(T, block);
   const int64_t spans = cdiv(T, kSpan);
-  SOLATTN_REQUIRE(spans < (1ll << 31) && B <= 65535 && H <= 65535, SOLATTN_EUNSUPPORTED,
+  SOLATTN_REQUIRE(spans <= 65535 && B <= 65535 && H <= 65535, SOLATTN_EUNSUPPORTED,
                   "pool: %lld tokens x %lld heads x %lld batch", (long long)T, (long long)H,
                   (long long)B);
   SOLATTN_REQUIRE(!qi || (qs && TP >= T && reinterpret_cast<uintptr_t>(qi) % 8 == 0),
                   SOLATTN_EINVAL, "pool: bad Q quantisation outputs");
-  // spans fastest, so the workgroups in flight read neighbouring rows of a head
-  dim3 grid(static_cast<uint32_t>(spans), static_cast<uint32_t>(H), static_cast<uint32_t>(B));
-  const auto kern = block == 64 ? (qi ? pool_kernel<64, true> : pool_kernel<64, false>)
-                                 : (qi ? pool_kernel<128, true> : pool_kernel<128, false>);
+  SOLATTN_REQUIRE(sq_t >= 0 && sk_t >= 0 && sv_t >= 0 &&
+                      std::max(sq_t, std::max(sk_t, sv_t)) < (1ll << 26),
+                  SOLATTN_EUNSUPPORTED, "pool: token strides must lie in [0, 2^26)");
+  // heads fastest, so the workgroups in flight read whole token rows (all heads)
+  // of neighbouring spans
+  dim3 grid(static_cast<uint32_t>(H), static_cast<uint32_t>(spans), static_cast<uint32_t>(B));
+  const bool amax = vamax_part != nullptr;
+  const auto kern =
+      block == 64
+          ? (qi ? (amax ? pool_kernel<64, true, true> : pool_kernel<64, true, false>)
+                : (amax ? pool_kernel<64, false, true> : pool_kernel<64, false, false>))
+          : (qi ? (amax ? pool_kernel<128, true, true> : pool_kernel<128, true, false>)
+                : (amax ? pool_kernel<128, false, true> : pool_kernel<128, false, false>));
   hipLaunchKernelGGL(kern, grid, dim3(kPoolThreads), 0, s, q, sq_b, sq_t, sq_h, k, sk_b, sk_t,
                      sk_h, v, sv_b, sv_t, sv_h, T, static_cast<int>(H), static_cast<int>(NT), kc,
                      vc, npad, qbar, vamax_part, qi, qs, TP);
@@ -845,13 +893,16 @@ extern "C" int solattn_moments(uint16_t* kc, int64_t npad, int64_t B, int64_t NT
                   SOLATTN_EINVAL, "moments: bad sizes");
   SOLATTN_REQUIRE(kc && kc_mean && kc_var, SOLATTN_EINVAL, "moments: null pointer");
   SOLATTN_REQUIRE(!vamax_part || vscale, SOLATTN_EINVAL, "moments: vamax_part needs vscale");
+  SOLATTN_REQUIRE(!vamax_part || H < 32768, SOLATTN_EUNSUPPORTED,
+                  "moments: %lld heads with vamax_part (at most 32767)", (long long)H);
   SOLATTN_REQUIRE(reinterpret_cast<uintptr_t>(kc) % 16 == 0 &&
                       reinterpret_cast<uintptr_t>(vamax_part) % 16 == 0,
                   SOLATTN_EINVAL, "moments: kc and vamax_part must be 16-byte aligned");
-  hipLaunchKernelGGL(moments_kernel, dim3(static_cast<uint32_t>(H), static_cast<uint32_t>(B)),
-                     dim3(kMomThreads), 0, reinterpret_cast<hipStream_t>(stream), kc, npad,
-                     static_cast<int>(NT), static_cast<int>(H), centre ? 1 : 0, kc_mean, kc_var,
-                     vamax_part, vscale);
+  hipLaunchKernelGGL(centre ? moments_kernel<true> : moments_kernel<false>,
+                     dim3(kHeadDim / kMomCh, static_cast<uint32_t>(H), static_cast<uint32_t>(B)),
+                     dim3(kMomThreads),
+                     0, reinterpret_cast<hipStream_t>(stream), kc, npad, static_cast<int>(NT),
+                     static_cast<int>(H), kc_mean, kc_var, vamax_part, vscale);
   return check_launch("moments");
 }
 
