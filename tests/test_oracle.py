@@ -311,6 +311,40 @@ def test_division_free_scale_matches_ieee():
     assert f(0, 1 << 23, 1) == 0                # denormals
 
 
+def test_biased_code_fast_path_matches_contract():
+    """The quantisers' fast path: with rr within 1 ulp of 1/s (v_rcp_f32),
+    v = fl(fl(x * rr) + 128) and v farther than 4e-5 from every half-integer,
+    rint(v) - 128 is the contract's code trunc(fl(q + copysign(0.5, q))) of the
+    IEEE quotient q = fl(x / s). Random rows at their own scales, plus values
+    placed on and around half-integer quotients (the cases the guard sends to
+    the division path); rr at RN(1/s) and one ulp either side."""
+    rng = np.random.default_rng(11)
+    f32 = np.float32
+    n = 400_000
+    amax = (10.0 ** rng.uniform(-7, 2, n)).astype(f32)
+    s = np.maximum(amax / f32(127), f32(1e-8)).astype(f32)
+    # quotients uniform in [-127, 127], and clustered near k + 1/2
+    k = rng.integers(-127, 127, n).astype(np.float64)
+    target = np.where(rng.random(n) < 0.5, rng.uniform(-127, 127, n),
+                      k + 0.5 + rng.normal(0, 3e-5, n))
+    target = np.clip(target, -127, 127)
+    x = oracle.bf16_to_f32(oracle.f32_to_bf16((target * s).astype(f32)))
+    x = np.where(np.abs(x) <= f32(127) * s, x, np.sign(x) * f32(127) * s).astype(f32)
+    q = (x / s).astype(f32)
+    t = (q + np.copysign(f32(0.5), q)).astype(f32)
+    want = np.clip(np.trunc(t), -127, 127)
+    r0 = (f32(1) / s).astype(f32)
+    taken = 0
+    for rr in (np.nextafter(r0, f32(0)), r0, np.nextafter(r0, f32(np.inf))):
+        v = ((x * rr).astype(f32) + f32(128)).astype(f32)
+        fast = np.abs(v - np.rint(v)) < f32(0.5) - f32(4e-5)
+        got = np.rint(v) - 128
+        assert np.array_equal(got[fast], want[fast])
+        assert np.all(np.abs(got[fast]) <= 127)
+        taken += int(fast.sum())
+    assert taken > 2 * n       # most values take the fast path
+
+
 def test_quant_smoothing_and_v():
     x = randn_bf16((2, 50, 3, 128), 17, scale=4.0)
     mean = np.random.default_rng(3).standard_normal((2, 3, 128)).astype(np.float32)
