@@ -613,47 +613,35 @@ prep_int8_single_read_kernel(const PrepInt8Args a) {
 // ----------------------------------------------------------------- route --
 // Thresholds (/root/reference/_preprocess.py:149-163, /root/reference/_fused_prep.py:50-59)
 // and the routing rule of the forward (/root/reference/_tri_fwd.py:279-286),
-// for kQB query blocks per workgroup; thread t scores key block j0 + t.
+// for kQB query blocks per workgroup.
 constexpr int kQB = 8;
 constexpr int kRouteThreads = 256;
 constexpr int kMaxWords = 512;  // NT <= 16384 (the forwards' limit)
-constexpr int kKcStride = kHeadDim + 4;  // bf16 per staged kc row (264 B): conflict-free 8-byte reads
-// TPR threads score each staged kc row, each against kQB / TPR query blocks:
-// kRouteThreads / TPR rows per chunk (TPR 2: 33 KB of LDS, four workgroups per
-// CU; TPR 4: 17 KB). Against one row per thread (67 KB, two workgroups per
-// CU): 34.8 -> 24.1 us (TPR 2) / 25.6 us (TPR 4) at NT 256 and 83 -> 61 / 58 us
-// at NT 512, same bits; the launch takes TPR 2 up to NT 256, else 4.
-
-template <int TPR>
+// Thread t scores key block (kc row) j0 + t against all kQB query blocks of
+// the workgroup, its row streaming through registers 32 channels at a time
+// (the next 32 in flight); the query centroids are wave-uniform, so each fma
+// takes its q operand from an SGPR (scalar loads). Against kc rows staged in
+// LDS with two or four threads per row: 20.0 -> 19.7 us at NT 256 and
+// 63.0 -> 47.2 us at NT 512, same bits.
 __global__ void __launch_bounds__(kRouteThreads)
 route_kernel(const float* __restrict__ qbar, const uint16_t* __restrict__ kc, int64_t npad,
              const float* __restrict__ kc_mean, const float* __restrict__ kc_var, int H, int NT,
              int W, float c, float c2, float tau, int mode, int64_t skv_lo, int64_t skv_hi,
              int64_t sq_lo, int64_t sq_hi, float* __restrict__ thr_out,
              int32_t* __restrict__ counts, uint32_t* __restrict__ mask) {
-  constexpr int kRouteRows = kRouteThreads / TPR;  // kc rows staged per chunk
-  constexpr int kQH = kQB / TPR;                   // query blocks per thread
-  constexpr int kKcLoads = kRouteRows * (kHeadDim / 8) / kRouteThreads;  // 16-byte loads per thread
-  static_assert(kRouteRows % 64 == 0 && kQB % TPR == 0, "route tiling");
   const int i0 = blockIdx.x * kQB, h = blockIdx.y, b = blockIdx.z;
   const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
-  // exact bits of the kQB query blocks, W words each, in dynamic LDS
   extern __shared__ __align__(16) uint32_t smask_lds[];
   const auto smask = [&](int i, int w) -> uint32_t& { return smask_lds[i * W + w]; };
-  __shared__ __align__(16) uint16_t skc[kRouteRows * kKcStride];
   __shared__ __align__(16) float sq[kQB][kHeadDim];  // the kQB query centroids
   __shared__ __align__(16) float smk[kHeadDim];      // kc mean (mode 0)
   __shared__ __align__(16) float svk[kHeadDim];      // kc variance
   static_assert(kQB * kHeadDim / 4 == kRouteThreads && 2 * kHeadDim == kRouteThreads,
                 "one float4 of the centroids and one moment per thread");
   const int64_t bh = static_cast<int64_t>(b) * H + h;
-  // Threads t, t + kRouteRows, ... score the same kc row, against query blocks
-  // qh*kQH .. +kQH-1 (qh is the same for the whole wave).
-  const int qh = __builtin_amdgcn_readfirstlane(t / kRouteRows);
   {
-    // The centroids and moments, one load per thread, published by the first
-    // chunk's barrier. Query rows past NT (a ragged last workgroup) read row
-    // NT-1; nothing of theirs is stored.
+    // The centroids and moments, one load per thread. Query rows past NT (a
+    // ragged last workgroup) read row NT-1; nothing of theirs is stored.
     const int qb = t >> 5, q4 = t & 31;
     const float4 x =
         reinterpret_cast<const float4*>(qbar + (bh * NT + min(i0 + qb, NT - 1)) * kHeadDim)[q4];
@@ -662,113 +650,107 @@ route_kernel(const float* __restrict__ qbar, const uint16_t* __restrict__ kc, in
     (t < kHeadDim ? smk[t] : svk[t - kHeadDim]) = mv;
   }
   for (int e = t; e < kQB * W; e += kRouteThreads) smask_lds[e] = 0u;
-  float th = 0.f;  // lane i < kQB of every wave: the threshold of query block i0 + i
-
-  for (int j0 = 0; j0 < NT; j0 += kRouteRows) {
-    // Stage kc rows j0 .. j0+kRouteRows-1 (coalesced 16-byte loads, all issued
-    // before the LDS stores; rows past NT are 0), then the TPR threads
-    // t = r (mod kRouteRows) score row r.
-    {
-      uint4 v[kKcLoads];
+  const float* qrow[kQB];  // wave-uniform rows of the centroids
 #pragma unroll
-      for (int u = 0; u < kKcLoads; ++u) {
-        const int e = t + kRouteThreads * u;
-        const int r = e >> 4, cc = e & 15;
-        v[u] = *reinterpret_cast<const uint4*>(
-            kc + ((static_cast<int64_t>(b) * npad + min(j0 + r, NT - 1)) * H + h) * kHeadDim +
-            cc * 8);
-      }
-#pragma unroll
-      for (int u = 0; u < kKcLoads; ++u)
-        if (j0 + ((t + kRouteThreads * u) >> 4) >= NT) v[u] = make_uint4(0u, 0u, 0u, 0u);
-      __syncthreads();  // the previous chunk's rows have been read
-#pragma unroll
-      for (int u = 0; u < kKcLoads; ++u) {
-        const int e = t + kRouteThreads * u;
-        const int r = e >> 4, cc = e & 15;
-        uint2* dst = reinterpret_cast<uint2*>(&skc[r * kKcStride + cc * 8]);
-        dst[0] = make_uint2(v[u].x, v[u].y);
-        dst[1] = make_uint2(v[u].z, v[u].w);
-      }
-    }
-    __syncthreads();  // (the first one also publishes the centroids and moments)
-    if (j0 == 0) {
-      // Every wave computes the kQB thresholds (lane i: query block i0 + i),
-      // one fma chain per moment in ascending d, so no barrier waits on them.
-      const float* qv = sq[min(lane, kQB - 1)];
-      float mu = 0.f, var = 0.f;
+  for (int i = 0; i < kQB; ++i) qrow[i] = qbar + (bh * NT + min(i0 + i, NT - 1)) * kHeadDim;
+  // kc rows through raw buffer loads: base at row j0 (wave-uniform), the lane's
+  // row t further; rows past NT read 0 (and are not active).
+  const uint16_t* kch = kc + (static_cast<int64_t>(b) * npad * H + h) * kHeadDim;
+  const int64_t sj = static_cast<int64_t>(H) * kHeadDim;
+  const uint32_t roff = static_cast<uint32_t>(t * sj * 2);
+  __syncthreads();  // the centroids, moments and cleared mask words
+  // Every wave computes the kQB thresholds (lane i: query block i0 + i), one
+  // fma chain per moment in ascending d, so no barrier waits on them.
+  float th;
+  {
+    const float* qv = sq[min(lane, kQB - 1)];
+    float mu = 0.f, var = 0.f;
 #pragma unroll 4
-      for (int d = 0; d < kHeadDim; d += 4) {
-        const float4 x = *reinterpret_cast<const float4*>(qv + d);
-        const float4 vk = *reinterpret_cast<const float4*>(svk + d);
-        if (mode == 0) {
-          const float4 mk = *reinterpret_cast<const float4*>(smk + d);
-          mu = fmaf(x.x, mk.x, mu);
-          var = fmaf(x.x * x.x, vk.x, var);
-          mu = fmaf(x.y, mk.y, mu);
-          var = fmaf(x.y * x.y, vk.y, var);
-          mu = fmaf(x.z, mk.z, mu);
-          var = fmaf(x.z * x.z, vk.z, var);
-          mu = fmaf(x.w, mk.w, mu);
-          var = fmaf(x.w * x.w, vk.w, var);
-        } else {
-          var = fmaf(x.x * x.x, vk.x, var);
-          var = fmaf(x.y * x.y, vk.y, var);
-          var = fmaf(x.z * x.z, vk.z, var);
-          var = fmaf(x.w * x.w, vk.w, var);
-        }
-      }
+    for (int d = 0; d < kHeadDim; d += 4) {
+      const float4 x = *reinterpret_cast<const float4*>(qv + d);
+      const float4 vk = *reinterpret_cast<const float4*>(svk + d);
       if (mode == 0) {
-        mu = mu * c;
-        var = var * c2;
-        const float sd = sqrtf(fmaxf(var, 0.f) + 1e-6f);
-        th = mu + tau * sd;
+        const float4 mk = *reinterpret_cast<const float4*>(smk + d);
+        mu = fmaf(x.x, mk.x, mu);
+        var = fmaf(x.x * x.x, vk.x, var);
+        mu = fmaf(x.y, mk.y, mu);
+        var = fmaf(x.y * x.y, vk.y, var);
+        mu = fmaf(x.z, mk.z, mu);
+        var = fmaf(x.z * x.z, vk.z, var);
+        mu = fmaf(x.w, mk.w, mu);
+        var = fmaf(x.w * x.w, vk.w, var);
       } else {
-        var = var * c2;
-        th = tau * sqrtf(var + 1e-6f);
+        var = fmaf(x.x * x.x, vk.x, var);
+        var = fmaf(x.y * x.y, vk.y, var);
+        var = fmaf(x.z * x.z, vk.z, var);
+        var = fmaf(x.w * x.w, vk.w, var);
       }
-      if (wave == 0 && lane < kQB && i0 + lane < NT)
-        thr_out[(static_cast<int64_t>(b) * NT + i0 + lane) * H + h] = th;
     }
-    const int rr = t % kRouteRows;
-    const int j = j0 + rr;
+    if (mode == 0) {
+      mu = mu * c;
+      var = var * c2;
+      const float sd = sqrtf(fmaxf(var, 0.f) + 1e-6f);
+      th = mu + tau * sd;
+    } else {
+      var = var * c2;
+      th = tau * sqrtf(var + 1e-6f);
+    }
+    if (wave == 0 && lane < kQB && i0 + lane < NT)
+      thr_out[(static_cast<int64_t>(b) * NT + i0 + lane) * H + h] = th;
+  }
+  constexpr int kCh = 32;                  // channels of the row per step
+  constexpr int kChLoads = kCh / 8;        // 16-byte loads per step
+  for (int j0 = 0; j0 < NT; j0 += kRouteThreads) {
+    const int j = j0 + t;
     const bool active = j < NT;
-    float acc[kQH];
+    const uint16_t* base = kch + j0 * sj;
+    const uint32_t nb = rows_nbytes(j0, NT, 2 * sj, 2 * kHeadDim, kRouteThreads * 2 * sj);
+    float acc[kQB];
 #pragma unroll
-    for (int i = 0; i < kQH; ++i) acc[i] = 0.f;
-    const uint16_t* krow = &skc[rr * kKcStride];
-    // The query centroids are the same for every lane of a wave: broadcast
-    // LDS reads.
-#pragma unroll 2
-    for (int d4 = 0; d4 < kHeadDim / 4; ++d4) {
-      const uint2 kw = *reinterpret_cast<const uint2*>(krow + 4 * d4);
-      const float k0 = lo_bf16(kw.x), k1 = hi_bf16(kw.x);
-      const float k2 = lo_bf16(kw.y), k3 = hi_bf16(kw.y);
+    for (int i = 0; i < kQB; ++i) acc[i] = 0.f;
+    uint4 kn[kChLoads];  // the next channel step of this thread's row, in flight
 #pragma unroll
-      for (int i = 0; i < kQH; ++i) {
-        const float4 qv = *reinterpret_cast<const float4*>(&sq[qh * kQH + i][4 * d4]);
-        acc[i] = fmaf(qv.x, k0, acc[i]);
-        acc[i] = fmaf(qv.y, k1, acc[i]);
-        acc[i] = fmaf(qv.z, k2, acc[i]);
-        acc[i] = fmaf(qv.w, k3, acc[i]);
+    for (int u = 0; u < kChLoads; ++u) kn[u] = buffer_load16(base, nb, roff + 16 * u);
+#pragma unroll 1
+    for (int d0 = 0; d0 < kHeadDim; d0 += kCh) {
+      uint4 kr[kChLoads];
+#pragma unroll
+      for (int u = 0; u < kChLoads; ++u) kr[u] = kn[u];
+      if (d0 + kCh < kHeadDim) {
+#pragma unroll
+        for (int u = 0; u < kChLoads; ++u)
+          kn[u] = buffer_load16(base, nb, roff + 2 * (d0 + kCh) + 16 * u);
+      }
+#pragma unroll
+      for (int d4 = 0; d4 < kCh / 4; ++d4) {
+        const uint4& w = kr[d4 / 2];
+        const uint32_t k01 = (d4 & 1) ? w.z : w.x, k23 = (d4 & 1) ? w.w : w.y;
+        const float k0 = lo_bf16(k01), k1 = hi_bf16(k01), k2 = lo_bf16(k23), k3 = hi_bf16(k23);
+#pragma unroll
+        for (int i = 0; i < kQB; ++i) {
+          const float4 qv = *reinterpret_cast<const float4*>(qrow[i] + d0 + 4 * d4);
+          acc[i] = fmaf(qv.x, k0, acc[i]);
+          acc[i] = fmaf(qv.y, k1, acc[i]);
+          acc[i] = fmaf(qv.z, k2, acc[i]);
+          acc[i] = fmaf(qv.w, k3, acc[i]);
+        }
       }
     }
     const bool in_skv = j >= skv_lo && j < skv_hi;
-    const int w0 = (j0 + (rr & ~63)) >> 5;  // this wave's 64 rows
+    const int w0 = (j0 + 64 * wave) >> 5;  // this wave's 64 rows
 #pragma unroll
-    for (int i = 0; i < kQH; ++i) {
-      const int il = qh * kQH + i;
-      const int qi = i0 + il;
+    for (int i = 0; i < kQB; ++i) {
+      const int qi = i0 + i;
       const float r = acc[i] * c;
       const int dij = qi > j ? qi - j : j - qi;
       const bool q_in_sink = qi >= sq_lo && qi < sq_hi;
-      const float thr = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, th), il));
+      const float thr = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, th), i));
       const bool routed = (r > thr) || dij <= 1 || in_skv;
       const bool exact = active && qi < NT && (q_in_sink || routed);
       const uint64_t bal = __ballot(exact);
       if (lane == 0 && w0 < W) {
-        smask(il, w0) = static_cast<uint32_t>(bal);
-        if (w0 + 1 < W) smask(il, w0 + 1) = static_cast<uint32_t>(bal >> 32);
+        smask(i, w0) = static_cast<uint32_t>(bal);
+        if (w0 + 1 < W) smask(i, w0 + 1) = static_cast<uint32_t>(bal >> 32);
       }
     }
   }
@@ -930,7 +912,7 @@ extern "C" int solattn_route(const float* qbar, const uint16_t* kc, int64_t npad
   const float c2 = c * c;
   dim3 grid(static_cast<uint32_t>(cdiv(NT, kQB)), static_cast<uint32_t>(H),
             static_cast<uint32_t>(B));
-  hipLaunchKernelGGL(NT <= 256 ? route_kernel<2> : route_kernel<4>, grid, dim3(kRouteThreads),
+  hipLaunchKernelGGL(route_kernel, grid, dim3(kRouteThreads),
                      static_cast<size_t>(kQB * W * sizeof(uint32_t)),
                      reinterpret_cast<hipStream_t>(stream), qbar, kc, npad,
                      mode == 0 ? kc_mean : kc_var, kc_var, static_cast<int>(H),
