@@ -97,6 +97,8 @@ int solattn_reorder_rows(const void* src, int64_t src_rows, int64_t src_stride_b
  *   vc[b, j, h, :] = bf16_rne(sum_v)              (rows j >= NT are not written)
  *   qbar[b, h, j, :] = sum_q / len_j              qbar: fp32 [B, H, NT, D]
  *   vamax_part[b, j, h, :] = max_r |v|            fp32 [B, NT, H, D], may be NULL
+ * Token strides must lie in [0, 2^26) elements and T <= 65535 * 128
+ * (SOLATTN_EUNSUPPORTED otherwise).
  * Replaces: _reduce_kc_kernel / _reduce_vc_kernel / _reduce_kv,
  * /root/reference/_preprocess.py:23-113,172-224, and the Q centroid of
  * _diag_threshold_kernel (:144-149) / _q_quant_threshold_kernel
@@ -118,7 +120,8 @@ int solattn_pool(const uint16_t* q, int64_t sq_b, int64_t sq_t, int64_t sq_h,
  * kc_mean, kc_var: fp32 [B, H, D].
  * If vamax_part != NULL also vscale[b, h, d] = max(max_j vamax_part * (1/127)f, 1e-8)
  * (/root/reference/_fused_quant.py:102-105: torch divides by a scalar as a
- * multiply by its fp32 reciprocal). kc and vamax_part must be 16-byte aligned. */
+ * multiply by its fp32 reciprocal). kc and vamax_part must be 16-byte aligned;
+ * with vamax_part, H < 32768 (SOLATTN_EUNSUPPORTED otherwise). */
 int solattn_moments(uint16_t* kc, int64_t npad, int64_t B, int64_t NT, int64_t H,
                     int64_t D, int centre, float* kc_mean, float* kc_var,
                     const float* vamax_part, float* vscale, solattn_stream_t stream);

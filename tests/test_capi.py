@@ -59,6 +59,18 @@ def test_errors_are_reported(capi):
     rc = L.solattn_route(null, null, 16448, null, null, 1, 16385 * 64, 1, 128, 64, 0.1, 1.0, 0,
                          0, 0, 0, 0, null, null, null, null)
     assert rc == -2 and b"exceed" in L.solattn_last_error()
+    # the pool's buffer offsets are 32-bit: token strides of 2^26 elements and more,
+    # and more than 65535 spans of 128 tokens, are unsupported (no device work)
+    fake = 1 << 20  # 16-byte aligned, never dereferenced
+    big = 1 << 26
+    rc = L.solattn_pool(fake, big * 8, big, 128, fake, 0, 128, 0, fake, 0, 128, 0, 1, 4, 1, 128,
+                        128, fake, fake, 1, fake, null, null)
+    assert rc == -2 and b"token strides" in L.solattn_last_error()
+    rc = L.solattn_pool(fake, 0, 128, 0, fake, 0, 128, 0, fake, 0, 128, 0, 1, 65536 * 128, 1,
+                        128, 128, fake, fake, 65536, fake, null, null)
+    assert rc == -2 and b"tokens" in L.solattn_last_error()
+    rc = L.solattn_moments(fake, 4, 1, 4, 32768, 128, 1, fake, fake, fake, fake, null)
+    assert rc == -2 and b"heads" in L.solattn_last_error()
     with pytest.raises(capi.SolAttnError, match="null pointer"):
         capi.call("solattn_reorder_rows", null, 1, 0, 16, null, 0, 16, 1, 1, 16, null, null)
     ws = L.solattn_sol_attn_workspace_bytes(1, 1000, 2, 128, 64, 0)
