@@ -318,6 +318,26 @@ def test_strided_qkv_view(pkg, dev):
     assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("block", [64, 128])
+def test_strided_views_every_path(pkg, dev, block):
+    """Batch 2, q/k/v as views of a fused [B, T, 3, H, 256] buffer narrowed to
+    128 channels (token stride 3*H*256, head stride 256): both forwards and
+    every INT8 P.V mode give the bits of contiguous copies of the same data."""
+    tri, i8 = _mods(pkg)[1], _mods(pkg)[2]
+    B, T, H = 2, 1000, 3
+    print(f"[strided views] block={block}", flush=True)
+    buf = randn_bf16((B, T, 3, H, 256), 51).to(dev)
+    q, k, v = (buf[:, :, i, :, :128] for i in range(3))
+    assert q.stride(1) == 3 * H * 256 and q.stride(2) == 256
+    qc, kc, vc = q.contiguous(), k.contiguous(), v.contiguous()
+    assert torch.equal(tri.sol_attn(q, k, v, tau=0.8, block=block),
+                       tri.sol_attn(qc, kc, vc, tau=0.8, block=block))
+    for pv, codes in PV_MODES.values():
+        a = i8.sol_attn_int8(q, k, v, tau=0.8, block=block, int8_pv=pv, pv_codes=codes)
+        b = i8.sol_attn_int8(qc, kc, vc, tau=0.8, block=block, int8_pv=pv, pv_codes=codes)
+        assert torch.equal(a, b), (pv, codes)
+
+
 TINY_CASES = [  # (T, block): one partial block, exactly one block, one block + 1 row
     (1, 64), (63, 64), (64, 64), (65, 64), (100, 128), (128, 128), (129, 128),
 ]
