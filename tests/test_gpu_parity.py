@@ -31,6 +31,10 @@ CASES = [  # (B, T, H, block, tau, sink_kv, sink_q)
     (2, 777, 3, 128, 0.5, (0, 2), (0, 0)),
     (1, 4096, 4, 64, 1.3, (0, 3), (0, 3)),
     (1, 2500, 2, 128, -1e30, (0, 0), (0, 0)),
+    # just past the 256 blocks a moments thread holds in registers and a route
+    # workgroup scores in one pass (NT 257, ragged; NT 513)
+    (1, 256 * 64 + 10, 2, 64, 0.9, (0, 0), (0, 0)),
+    (1, 512 * 128 + 50, 1, 128, 0.8, (0, 1), (0, 0)),
 ]
 
 
