@@ -617,12 +617,15 @@ prep_int8_single_read_kernel(const PrepInt8Args a) {
 constexpr int kQB = 8;
 constexpr int kRouteThreads = 256;
 constexpr int kMaxWords = 512;  // NT <= 16384 (the forwards' limit)
-// Thread t scores key block (kc row) j0 + t against all kQB query blocks of
-// the workgroup, its row streaming through registers 32 channels at a time
-// (the next 32 in flight); the query centroids are wave-uniform, so each fma
-// takes its q operand from an SGPR (scalar loads). Against kc rows staged in
-// LDS with two or four threads per row: 20.0 -> 19.7 us at NT 256 and
-// 63.0 -> 47.2 us at NT 512, same bits.
+// The workgroup's threads form G groups of R = kRouteThreads / G (a multiple
+// of 64: whole waves); thread t scores key block (kc row) j0 + t % R against
+// the kQB / G query blocks of its group, its row streaming through registers
+// 32 channels at a time (the next 32 in flight); the query centroids are
+// wave-uniform, so each fma takes its q operand from an SGPR (scalar loads).
+// G > 1 serves short sequences (NT <= 128), whose rows would leave waves idle.
+// Against kc rows staged in LDS with two or four threads per row: 20.0 ->
+// 19.7 us at NT 256 and 63.0 -> 47.2 us at NT 512, same bits.
+template <int G>
 __global__ void __launch_bounds__(kRouteThreads)
 route_kernel(const float* __restrict__ qbar, const uint16_t* __restrict__ kc, int64_t npad,
              const float* __restrict__ kc_mean, const float* __restrict__ kc_var, int H, int NT,
@@ -650,14 +653,18 @@ route_kernel(const float* __restrict__ qbar, const uint16_t* __restrict__ kc, in
     (t < kHeadDim ? smk[t] : svk[t - kHeadDim]) = mv;
   }
   for (int e = t; e < kQB * W; e += kRouteThreads) smask_lds[e] = 0u;
-  const float* qrow[kQB];  // wave-uniform rows of the centroids
+  constexpr int R = kRouteThreads / G, kQG = kQB / G;  // rows per pass, query blocks per thread
+  static_assert(R % 64 == 0 && kQB % G == 0, "route groups are whole waves");
+  const int rr = t % R;
+  const int ig = __builtin_amdgcn_readfirstlane(t / R) * kQG;  // the group's first query block
+  const float* qrow[kQG];  // wave-uniform rows of the centroids
 #pragma unroll
-  for (int i = 0; i < kQB; ++i) qrow[i] = qbar + (bh * NT + min(i0 + i, NT - 1)) * kHeadDim;
+  for (int i = 0; i < kQG; ++i) qrow[i] = qbar + (bh * NT + min(i0 + ig + i, NT - 1)) * kHeadDim;
   // kc rows through raw buffer loads: base at row j0 (wave-uniform), the lane's
-  // row t further; rows past NT read 0 (and are not active).
+  // row rr further; rows past NT read 0 (and are not active).
   const uint16_t* kch = kc + (static_cast<int64_t>(b) * npad * H + h) * kHeadDim;
   const int64_t sj = static_cast<int64_t>(H) * kHeadDim;
-  const uint32_t roff = static_cast<uint32_t>(t * sj * 2);
+  const uint32_t roff = static_cast<uint32_t>(rr * sj * 2);
   __syncthreads();  // the centroids, moments and cleared mask words
   // Every wave computes the kQB thresholds (lane i: query block i0 + i), one
   // fma chain per moment in ascending d, so no barrier waits on them.
@@ -700,14 +707,14 @@ route_kernel(const float* __restrict__ qbar, const uint16_t* __restrict__ kc, in
   }
   constexpr int kCh = 32;                  // channels of the row per step
   constexpr int kChLoads = kCh / 8;        // 16-byte loads per step
-  for (int j0 = 0; j0 < NT; j0 += kRouteThreads) {
-    const int j = j0 + t;
+  for (int j0 = 0; j0 < NT; j0 += R) {
+    const int j = j0 + rr;
     const bool active = j < NT;
     const uint16_t* base = kch + j0 * sj;
-    const uint32_t nb = rows_nbytes(j0, NT, 2 * sj, 2 * kHeadDim, kRouteThreads * 2 * sj);
-    float acc[kQB];
+    const uint32_t nb = rows_nbytes(j0, NT, 2 * sj, 2 * kHeadDim, R * 2 * sj);
+    float acc[kQG];
 #pragma unroll
-    for (int i = 0; i < kQB; ++i) acc[i] = 0.f;
+    for (int i = 0; i < kQG; ++i) acc[i] = 0.f;
     uint4 kn[kChLoads];  // the next channel step of this thread's row, in flight
 #pragma unroll
     for (int u = 0; u < kChLoads; ++u) kn[u] = buffer_load16(base, nb, roff + 16 * u);
@@ -727,7 +734,7 @@ route_kernel(const float* __restrict__ qbar, const uint16_t* __restrict__ kc, in
         const uint32_t k01 = (d4 & 1) ? w.z : w.x, k23 = (d4 & 1) ? w.w : w.y;
         const float k0 = lo_bf16(k01), k1 = hi_bf16(k01), k2 = lo_bf16(k23), k3 = hi_bf16(k23);
 #pragma unroll
-        for (int i = 0; i < kQB; ++i) {
+        for (int i = 0; i < kQG; ++i) {
           const float4 qv = *reinterpret_cast<const float4*>(qrow[i] + d0 + 4 * d4);
           acc[i] = fmaf(qv.x, k0, acc[i]);
           acc[i] = fmaf(qv.y, k1, acc[i]);
@@ -737,20 +744,21 @@ route_kernel(const float* __restrict__ qbar, const uint16_t* __restrict__ kc, in
       }
     }
     const bool in_skv = j >= skv_lo && j < skv_hi;
-    const int w0 = (j0 + 64 * wave) >> 5;  // this wave's 64 rows
+    const int w0 = (j0 + 64 * (wave % (R / 64))) >> 5;  // this wave's 64 rows
 #pragma unroll
-    for (int i = 0; i < kQB; ++i) {
-      const int qi = i0 + i;
+    for (int i = 0; i < kQG; ++i) {
+      const int il = ig + i;
+      const int qi = i0 + il;
       const float r = acc[i] * c;
       const int dij = qi > j ? qi - j : j - qi;
       const bool q_in_sink = qi >= sq_lo && qi < sq_hi;
-      const float thr = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, th), i));
+      const float thr = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, th), il));
       const bool routed = (r > thr) || dij <= 1 || in_skv;
       const bool exact = active && qi < NT && (q_in_sink || routed);
       const uint64_t bal = __ballot(exact);
       if (lane == 0 && w0 < W) {
-        smask(i, w0) = static_cast<uint32_t>(bal);
-        if (w0 + 1 < W) smask(i, w0 + 1) = static_cast<uint32_t>(bal >> 32);
+        smask(il, w0) = static_cast<uint32_t>(bal);
+        if (w0 + 1 < W) smask(il, w0 + 1) = static_cast<uint32_t>(bal >> 32);
       }
     }
   }
@@ -912,7 +920,8 @@ extern "C" int solattn_route(const float* qbar, const uint16_t* kc, int64_t npad
   const float c2 = c * c;
   dim3 grid(static_cast<uint32_t>(cdiv(NT, kQB)), static_cast<uint32_t>(H),
             static_cast<uint32_t>(B));
-  hipLaunchKernelGGL(route_kernel, grid, dim3(kRouteThreads),
+  hipLaunchKernelGGL(NT <= 64 ? route_kernel<4> : NT <= 128 ? route_kernel<2> : route_kernel<1>,
+                     grid, dim3(kRouteThreads),
                      static_cast<size_t>(kQB * W * sizeof(uint32_t)),
                      reinterpret_cast<hipStream_t>(stream), qbar, kc, npad,
                      mode == 0 ? kc_mean : kc_var, kc_var, static_cast<int>(H),

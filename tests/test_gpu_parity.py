@@ -35,6 +35,7 @@ CASES = [  # (B, T, H, block, tau, sink_kv, sink_q)
     # workgroup scores in one pass (NT 257, ragged; NT 513)
     (1, 256 * 64 + 10, 2, 64, 0.9, (0, 0), (0, 0)),
     (1, 512 * 128 + 50, 1, 128, 0.8, (0, 1), (0, 0)),
+    (2, 6000, 2, 64, 0.9, (0, 1), (2, 3)),  # NT 94: the route's two-group form
 ]
 
 
